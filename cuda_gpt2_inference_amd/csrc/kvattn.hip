@@ -1,0 +1,1209 @@
+// kvattn.hip -- decode-phase KV-cache attention for MI355X (gfx950, CDNA4, wave64).
+//
+// One head row (hs = 64 elements) is spread over the lanes of one 64-lane wavefront so
+// that every lane issues one 16-byte load per row chunk:
+//   FP32 row = 256 B -> 16 lanes per row, 4 rows per wave load instruction
+//   BF16 row = 128 B ->  8 lanes per row, 8 rows per wave load instruction
+//   8-bit row = 64 B ->  4 lanes per row, 16 rows per wave load instruction
+// A lane keeps the q values of its own channel slice in registers, forms a partial dot
+// product, and the lanes of a row finish it with DPP row permutations.  V rows use the
+// same lane mapping, so each lane accumulates its channel slice of the weighted V sum;
+// the slices of different rows are combined once per segment.  Everything is bandwidth
+// bound (1 flop per BF16 byte), so no matrix cores are involved.
+//
+// Strategies (host side at the bottom of this file):
+//   fused_single     one 256-thread workgroup per (b,h); scores staged in LDS, then a
+//                    V pass with the exact maximum (reference strategy 1)
+//   split            one workgroup per (b,h,segment); per-lane-group online softmax
+//                    (m, l, acc) in base 2, then a workgroup merge into the reference's
+//                    partial format (max in natural-log units, exp-sum, weighted V sum)
+//   merge            one wave per (b,h) combining the segment partials
+//   split+lastblock  split whose last finishing segment of a (b,h) merges, ordered by an
+//                    agent-scope release/acquire counter; one ordinary launch
+//   split+coop       split + grid barrier + merge by segment 0 (cooperative launch)
+//   split+graph      split and merge kernel nodes in a hipGraph, one hipGraphLaunch
+#include <hip/hip_runtime.h>
+#include <hip/hip_cooperative_groups.h>
+
+#include <float.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <map>
+#include <mutex>
+#include <tuple>
+
+#include "kvattn.h"
+
+namespace {
+
+constexpr int kHeadDim = 64;
+constexpr int kWave = 64;
+constexpr int kBlock = 256;
+constexpr int kWaves = kBlock / kWave;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.69314718055994531f;
+constexpr float kEmptyMax = -FLT_MAX;   // max of an empty segment (reference sentinel)
+constexpr float kStartMax = -1.0e30f;   // finite start value of every running max
+constexpr int kMinSegRows = 64;         // smallest automatic segment length
+constexpr int kMaxSegments = 1 << 16;   // upper bound on segments per (b,h)
+constexpr int kMaxT = 1 << 23;          // keeps per-slot byte offsets inside 32 bits
+constexpr size_t kFusedMaxLds = 64 * 1024;  // dynamic LDS of fused_single (scores)
+
+// ------------------------------------------------------------------------------------
+// Per-dtype row geometry.
+// ------------------------------------------------------------------------------------
+template <int DT> struct Row;
+template <> struct Row<KVATTN_KV_F32> {
+    static constexpr int kLanes = 16, kElems = 4, kBytes = 256;
+    static constexpr bool k8bit = false, kActF32 = true;
+};
+template <> struct Row<KVATTN_KV_BF16> {
+    static constexpr int kLanes = 8, kElems = 8, kBytes = 128;
+    static constexpr bool k8bit = false, kActF32 = false;
+};
+template <> struct Row<KVATTN_KV_INT8> {
+    static constexpr int kLanes = 4, kElems = 16, kBytes = 64;
+    static constexpr bool k8bit = true, kActF32 = false;
+};
+template <> struct Row<KVATTN_KV_FP8_E4M3> {
+    static constexpr int kLanes = 4, kElems = 16, kBytes = 64;
+    static constexpr bool k8bit = true, kActF32 = false;
+};
+template <int DT> constexpr int kRowsPerLoad = kWave / Row<DT>::kLanes;
+// Row chunks per lane and tile in the unrolled main loops (8-bit rows are 4x denser).
+template <int DT> constexpr int kUnroll = Row<DT>::k8bit ? 4 : 8;
+
+// ------------------------------------------------------------------------------------
+// Element helpers.
+// ------------------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+// float -> bfloat16 bits, round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+// OCP E4M3 ("FN": max 448, no infinities) encode of y, round to nearest even, finite
+// overflow saturates to +-448 (the reference's __NV_SATFINITE request).
+__device__ __forceinline__ uint8_t f32_to_e4m3_sat(float y) {
+    if (y != y) return 0x7F;
+    const uint32_t sign = (__float_as_uint(y) >> 24) & 0x80u;
+    const float a = fabsf(y);
+    if (a >= 448.0f) return (uint8_t)(sign | 0x7Eu);
+    if (a < 0.015625f) {                       // subnormal grid m * 2^-9; 8 -> 2^-6
+        return (uint8_t)(sign | (uint32_t)rintf(a * 512.0f));
+    }
+    const uint32_t u = __float_as_uint(a);
+    uint32_t keep = u >> 20;                   // exponent | top 3 mantissa bits
+    const uint32_t rem = u & 0xFFFFFu;
+    keep += (rem > 0x80000u || (rem == 0x80000u && (keep & 1u))) ? 1u : 0u;
+    uint32_t code = keep - (120u << 3);        // rebias 127 -> 7
+    code = code > 0x7Eu ? 0x7Eu : code;
+    return (uint8_t)(sign | code);
+}
+
+__device__ __forceinline__ uint4 load16(const uint8_t* p) {
+    return *reinterpret_cast<const uint4*>(p);
+}
+
+// Decode one lane's 16-byte chunk of a row into kElems floats.
+template <int DT>
+__device__ __forceinline__ void decode(const uint4& d, float (&x)[Row<DT>::kElems]) {
+    const uint32_t w[4] = {d.x, d.y, d.z, d.w};
+    if constexpr (DT == KVATTN_KV_F32) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = __uint_as_float(w[i]);
+    } else if constexpr (DT == KVATTN_KV_BF16) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { x[2 * i] = bf16_lo(w[i]); x[2 * i + 1] = bf16_hi(w[i]); }
+    } else if constexpr (DT == KVATTN_KV_INT8) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) x[4 * i + k] = (float)(int8_t)(w[i] >> (8 * k));
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], false);
+            const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], true);
+            x[4 * i] = lo[0]; x[4 * i + 1] = lo[1]; x[4 * i + 2] = hi[0]; x[4 * i + 3] = hi[1];
+        }
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ float dot_chunk(const float (&q)[Row<DT>::kElems], const uint4& d) {
+    float x[Row<DT>::kElems];
+    decode<DT>(d, x);
+    float s = 0.0f;
+#pragma unroll
+    for (int e = 0; e < Row<DT>::kElems; ++e) s = fmaf(q[e], x[e], s);
+    return s;
+}
+
+// ------------------------------------------------------------------------------------
+// Cross-lane reductions.  DPP control words (GFX9 encoding).
+// ------------------------------------------------------------------------------------
+constexpr int kDppQuadXor1 = 0xB1;    // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;    // quad_perm [2,3,0,1]
+constexpr int kDppRowRor4 = 0x124;    // rotate 16-lane row by 4
+constexpr int kDppRowRor8 = 0x128;    // rotate 16-lane row by 8
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i inside each 8-lane half row
+constexpr int kDppRowMirror = 0x140;  // lane i <-> 15-i inside each 16-lane row
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xF, 0xF, true));
+}
+
+// Sum over the kLanes lanes holding one row (aligned groups of 4, 8 or 16 lanes).
+template <int kLanes>
+__device__ __forceinline__ float row_sum(float x) {
+    x += dpp<kDppQuadXor1>(x);
+    x += dpp<kDppQuadXor2>(x);
+    if constexpr (kLanes >= 8) x += dpp<kDppHalfMirror>(x);
+    if constexpr (kLanes >= 16) x += dpp<kDppRowMirror>(x);
+    return x;
+}
+
+// Reduce over the lanes that hold the same channel slice of different rows
+// (lane = row_slot * kLanes + slice): every lane receives the result for its slice.
+template <int kLanes, bool kMax>
+__device__ __forceinline__ float slot_reduce(float x) {
+    auto op = [](float a, float b) { return kMax ? fmaxf(a, b) : a + b; };
+    if constexpr (kLanes == 4) { x = op(x, dpp<kDppRowRor4>(x)); x = op(x, dpp<kDppRowRor8>(x)); }
+    if constexpr (kLanes == 8) { x = op(x, dpp<kDppRowRor8>(x)); }
+    x = op(x, __shfl_xor(x, 16));
+    x = op(x, __shfl_xor(x, 32));
+    return x;
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+    x = fmaxf(x, dpp<kDppQuadXor1>(x));
+    x = fmaxf(x, dpp<kDppQuadXor2>(x));
+    x = fmaxf(x, dpp<kDppHalfMirror>(x));
+    x = fmaxf(x, dpp<kDppRowMirror>(x));
+    x = fmaxf(x, __shfl_xor(x, 16));
+    x = fmaxf(x, __shfl_xor(x, 32));
+    return x;
+}
+
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Attended positions of sequence b: device length clamped to [0, maxT-1], plus one.
+__device__ __forceinline__ int seq_total(const int* cur_len, int lens_per_seq, int b, int maxT) {
+    int cl = cur_len[lens_per_seq ? b : 0];
+    cl = cl < 0 ? 0 : (cl > maxT - 1 ? maxT - 1 : cl);
+    return cl + 1;
+}
+
+// Load this lane's q slice (channels slice*kElems ..) as float, pre-multiplied by
+// scale*log2(e) so dot products come out in base-2 score units.
+template <int DT>
+__device__ __forceinline__ void load_q(const void* qkv, int b, int h, int NH, int slice, float qscale,
+                                       float (&q)[Row<DT>::kElems]) {
+    const size_t q0 = ((size_t)b * 3 * NH + h) * kHeadDim + (size_t)slice * Row<DT>::kElems;
+    if constexpr (Row<DT>::kActF32) {
+        const float* p = reinterpret_cast<const float*>(qkv) + q0;
+#pragma unroll
+        for (int e = 0; e < Row<DT>::kElems; ++e) q[e] = p[e] * qscale;
+    } else {
+        const uint16_t* p = reinterpret_cast<const uint16_t*>(qkv) + q0;
+#pragma unroll
+        for (int e = 0; e < Row<DT>::kElems; ++e) q[e] = bf16_to_f32(p[e]) * qscale;
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void store_out(void* out, size_t i, float v) {
+    if constexpr (Row<DT>::kActF32) reinterpret_cast<float*>(out)[i] = v;
+    else reinterpret_cast<uint16_t*>(out)[i] = f32_to_bf16(v);
+}
+
+// Byte pointers of one (b,h) cache slot, already offset to this lane's 16-byte slice.
+struct Slot {
+    const uint8_t* k;
+    const uint8_t* v;
+    const float* ks;   // row scales (8-bit) or nullptr
+    const float* vs;
+};
+
+template <int DT>
+__device__ __forceinline__ Slot make_slot(const uint8_t* kv, const float* kv_scale, int B, int NH,
+                                          int maxT, int bh, int slice) {
+    const size_t rows = (size_t)B * NH * maxT;
+    const size_t base = (size_t)bh * maxT;
+    Slot s;
+    s.k = kv + base * Row<DT>::kBytes + slice * 16;
+    s.v = kv + (rows + base) * Row<DT>::kBytes + slice * 16;
+    s.ks = Row<DT>::k8bit ? kv_scale + base : nullptr;
+    s.vs = Row<DT>::k8bit ? kv_scale + rows + base : nullptr;
+    return s;
+}
+
+// ------------------------------------------------------------------------------------
+// Online softmax over rows [r0, r1) of a slot by one wave.  Each group of kLanes lanes
+// owns one row per load instruction and keeps its own running (m, l, acc) in base-2
+// units; the groups are combined later.  U row chunks are in flight per lane per tile.
+// ------------------------------------------------------------------------------------
+template <int DT, int U, bool kChecked>
+__device__ __forceinline__ void online_tile(const Slot& sl, int r, int r1, int slot_row,
+                                            const float (&q)[Row<DT>::kElems], float& m, float& l,
+                                            float (&acc)[Row<DT>::kElems]) {
+    using R = Row<DT>;
+    constexpr int kRPL = kRowsPerLoad<DT>;
+    uint4 kd[U], vd[U];
+    float ks[U], vs[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int row = r + u * kRPL + slot_row;
+        const bool ok = !kChecked || row < r1;
+        if (ok) {
+            kd[u] = load16(sl.k + (uint32_t)row * R::kBytes);
+            vd[u] = load16(sl.v + (uint32_t)row * R::kBytes);
+            if constexpr (R::k8bit) { ks[u] = sl.ks[row]; vs[u] = sl.vs[row]; }
+        } else {
+            kd[u] = make_uint4(0u, 0u, 0u, 0u);
+            vd[u] = make_uint4(0u, 0u, 0u, 0u);
+            if constexpr (R::k8bit) { ks[u] = 0.0f; vs[u] = 0.0f; }
+        }
+    }
+    float s[U];
+    float mt = m;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        s[u] = row_sum<R::kLanes>(dot_chunk<DT>(q, kd[u]));
+        if constexpr (R::k8bit) s[u] *= ks[u];
+        if (kChecked && r + u * kRPL + slot_row >= r1) s[u] = -INFINITY;
+        mt = fmaxf(mt, s[u]);
+    }
+    const float corr = exp2_fast(m - mt);
+    l *= corr;
+#pragma unroll
+    for (int e = 0; e < R::kElems; ++e) acc[e] *= corr;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const float p = exp2_fast(s[u] - mt);
+        l += p;
+        const float pv = R::k8bit ? p * vs[u] : p;
+        float x[R::kElems];
+        decode<DT>(vd[u], x);
+#pragma unroll
+        for (int e = 0; e < R::kElems; ++e) acc[e] = fmaf(pv, x[e], acc[e]);
+    }
+    m = mt;
+}
+
+template <int DT>
+__device__ __forceinline__ void online_rows(const Slot& sl, int r0, int r1, int slot_row,
+                                            const float (&q)[Row<DT>::kElems], float& m, float& l,
+                                            float (&acc)[Row<DT>::kElems]) {
+    constexpr int kRPL = kRowsPerLoad<DT>;
+    constexpr int kTile = kRPL * kUnroll<DT>;
+    int r = r0;
+    for (; r + kTile <= r1; r += kTile) online_tile<DT, kUnroll<DT>, false>(sl, r, r1, slot_row, q, m, l, acc);
+    for (; r < r1; r += kRPL) online_tile<DT, 1, true>(sl, r, r1, slot_row, q, m, l, acc);
+}
+
+// ------------------------------------------------------------------------------------
+// fused_single: one workgroup per (b,h), grid B*NH.  Pass 1 writes every score to LDS
+// and finds the exact maximum; pass 2 weights V with exp2(score - max).
+// ------------------------------------------------------------------------------------
+template <int DT, int U, bool kChecked>
+__device__ __forceinline__ void score_tile(const Slot& sl, int r, int total, int slot_row, int slice,
+                                           const float (&q)[Row<DT>::kElems], float* scores, float& mloc) {
+    using R = Row<DT>;
+    constexpr int kRPL = kRowsPerLoad<DT>;
+    uint4 kd[U];
+    float ks[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int row = r + u * kRPL + slot_row;
+        if (!kChecked || row < total) {
+            kd[u] = load16(sl.k + (uint32_t)row * R::kBytes);
+            if constexpr (R::k8bit) ks[u] = sl.ks[row];
+        } else {
+            kd[u] = make_uint4(0u, 0u, 0u, 0u);
+            if constexpr (R::k8bit) ks[u] = 0.0f;
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        float s = row_sum<R::kLanes>(dot_chunk<DT>(q, kd[u]));
+        if constexpr (R::k8bit) s *= ks[u];
+        const int row = r + u * kRPL + slot_row;
+        if (!kChecked || row < total) {
+            mloc = fmaxf(mloc, s);
+            if (slice == 0) scores[row] = s;
+        }
+    }
+}
+
+template <int DT, int U, bool kChecked>
+__device__ __forceinline__ void weight_tile(const Slot& sl, int r, int total, int slot_row, float M,
+                                            const float* scores, float& l, float (&acc)[Row<DT>::kElems]) {
+    using R = Row<DT>;
+    constexpr int kRPL = kRowsPerLoad<DT>;
+    uint4 vd[U];
+    float vs[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int row = r + u * kRPL + slot_row;
+        if (!kChecked || row < total) {
+            vd[u] = load16(sl.v + (uint32_t)row * R::kBytes);
+            if constexpr (R::k8bit) vs[u] = sl.vs[row];
+        } else {
+            vd[u] = make_uint4(0u, 0u, 0u, 0u);
+            if constexpr (R::k8bit) vs[u] = 0.0f;
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int row = r + u * kRPL + slot_row;
+        if (!kChecked || row < total) {
+            const float p = exp2_fast(scores[row] - M);
+            l += p;
+            const float pv = R::k8bit ? p * vs[u] : p;
+            float x[R::kElems];
+            decode<DT>(vd[u], x);
+#pragma unroll
+            for (int e = 0; e < R::kElems; ++e) acc[e] = fmaf(pv, x[e], acc[e]);
+        }
+    }
+}
+
+template <int DT>
+__global__ __launch_bounds__(kBlock) void fused_single_kernel(
+    void* __restrict__ out, const void* __restrict__ qkv, const uint8_t* __restrict__ kv,
+    const float* __restrict__ kv_scale, const int* __restrict__ cur_len, int lens_per_seq,
+    int B, int NH, int maxT, float qscale) {
+    using R = Row<DT>;
+    constexpr int kRPL = kRowsPerLoad<DT>;
+    constexpr int kTile = kRPL * kUnroll<DT>;
+    extern __shared__ float s_scores[];
+    __shared__ float s_max[kWaves];
+    __shared__ float s_l[kWaves];
+    __shared__ float s_acc[kWaves][kHeadDim];
+
+    const int bh = blockIdx.x;
+    const int b = bh / NH, h = bh - b * NH;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int slot_row = lane / R::kLanes, slice = lane % R::kLanes;
+    const int total = seq_total(cur_len, lens_per_seq, b, maxT);
+
+    float q[R::kElems];
+    load_q<DT>(qkv, b, h, NH, slice, qscale, q);
+    const Slot sl = make_slot<DT>(kv, kv_scale, B, NH, maxT, bh, slice);
+
+    // Pass 1: tiles of kTile rows go round-robin to the 4 waves; single-load steps
+    // finish the remainder.
+    float mloc = kStartMax;
+    const int full = total / kTile * kTile;
+    for (int r = wave * kTile; r < full; r += kWaves * kTile)
+        score_tile<DT, kUnroll<DT>, false>(sl, r, total, slot_row, slice, q, s_scores, mloc);
+    for (int r = full + wave * kRPL; r < total; r += kWaves * kRPL)
+        score_tile<DT, 1, true>(sl, r, total, slot_row, slice, q, s_scores, mloc);
+    mloc = wave_max(mloc);
+    if (lane == 0) s_max[wave] = mloc;
+    __syncthreads();
+    float M = s_max[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_max[w]);
+
+    // Pass 2: the same rows, weighted by exp2(score - M).
+    float l = 0.0f, acc[R::kElems];
+#pragma unroll
+    for (int e = 0; e < R::kElems; ++e) acc[e] = 0.0f;
+    for (int r = wave * kTile; r < full; r += kWaves * kTile)
+        weight_tile<DT, kUnroll<DT>, false>(sl, r, total, slot_row, M, s_scores, l, acc);
+    for (int r = full + wave * kRPL; r < total; r += kWaves * kRPL)
+        weight_tile<DT, 1, true>(sl, r, total, slot_row, M, s_scores, l, acc);
+
+    l = slot_reduce<R::kLanes, false>(l);
+#pragma unroll
+    for (int e = 0; e < R::kElems; ++e) acc[e] = slot_reduce<R::kLanes, false>(acc[e]);
+    if (lane == 0) s_l[wave] = l;
+    if (slot_row == 0) {
+#pragma unroll
+        for (int e = 0; e < R::kElems; ++e) s_acc[wave][slice * R::kElems + e] = acc[e];
+    }
+    __syncthreads();
+    if (threadIdx.x < kHeadDim) {
+        const int c = threadIdx.x;
+        float L = 0.0f, A = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) { L += s_l[w]; A += s_acc[w][c]; }
+        store_out<DT>(out, (size_t)bh * kHeadDim + c, A / L);
+    }
+}
+
+// ------------------------------------------------------------------------------------
+// Split kernels.
+// ------------------------------------------------------------------------------------
+enum SplitMode { kPartialsOnly = 0, kLastBlockMerge = 1, kCoopMerge = 2 };
+
+struct SplitArgs {
+    void* out;
+    float* part_out;
+    float* part_lse;
+    float* part_max;
+    unsigned* counters;
+    const void* qkv;
+    const uint8_t* kv;
+    const float* kv_scale;
+    const int* cur_len;
+    int lens_per_seq;
+    int B, NH, maxT;
+    int S;          // segment slots per (b,h): the grid stride and the partial stride
+    int seg_rows;   // > 0: fixed rows per segment; 0: reference partition ceil(total/S)
+    float qscale;   // scale * log2(e)
+};
+
+struct Item {
+    int b, h, s, total, n_seg;
+};
+
+__host__ __device__ __forceinline__ int ceil_div_i(int a, int b) { return (a + b - 1) / b; }
+
+// Map a workgroup index to (b, h, segment).  Uniform lengths (or the reference
+// partition) use the dense grid B*NH*S; ragged lengths with fixed-size segments pack
+// the real segments of all sequences at the front of the grid using a prefix sum over
+// the per-sequence segment counts, computed redundantly by every wave.
+__device__ __forceinline__ bool locate(const SplitArgs& a, int x, Item& it) {
+    if (!a.lens_per_seq || a.seg_rows == 0) {
+        const int bh = x / a.S;
+        it.s = x - bh * a.S;
+        it.b = bh / a.NH;
+        it.h = bh - it.b * a.NH;
+        if (it.b >= a.B) return false;
+        it.total = seq_total(a.cur_len, a.lens_per_seq, it.b, a.maxT);
+        it.n_seg = a.seg_rows > 0 ? ceil_div_i(it.total, a.seg_rows) : a.S;
+        return it.s < it.n_seg;
+    }
+    const int lane = threadIdx.x & (kWave - 1);
+    int base = 0;
+    for (int b0 = 0; b0 < a.B; b0 += kWave) {
+        const int b = b0 + lane;
+        int tot = 0, cnt = 0;
+        if (b < a.B) {
+            tot = seq_total(a.cur_len, 1, b, a.maxT);
+            cnt = a.NH * ceil_div_i(tot, a.seg_rows);
+        }
+        int incl = cnt;
+#pragma unroll
+        for (int d = 1; d < kWave; d <<= 1) {
+            const int v = __shfl_up(incl, d);
+            if (lane >= d) incl += v;
+        }
+        const int pass_total = __shfl(incl, kWave - 1);
+        if (x < base + pass_total) {
+            const unsigned long long hit = __ballot(base + incl > x);
+            const int L = __ffsll((long long)hit) - 1;
+            const int excl = __shfl(incl - cnt, L);
+            it.b = b0 + L;
+            it.total = __shfl(tot, L);
+            it.n_seg = ceil_div_i(it.total, a.seg_rows);
+            const int local = x - base - excl;
+            it.h = local / it.n_seg;
+            it.s = local - it.h * it.n_seg;
+            return true;
+        }
+        base += pass_total;
+    }
+    return false;
+}
+
+// Merge the n_seg partials of (b,h) = bh into out; executed by one full wave, lane c
+// producing channel c.
+template <int DT>
+__device__ __forceinline__ void merge_partials(void* out, const float* part_out, const float* part_lse,
+                                               const float* part_max, int S, int n_seg, int bh, int c) {
+    const size_t p0 = (size_t)bh * S;
+    float M = kEmptyMax;
+    for (int s = 0; s < n_seg; ++s) M = fmaxf(M, part_max[p0 + s]);
+    float O = 0.0f, L = 0.0f;
+    for (int s = 0; s < n_seg; ++s) {
+        const float e = exp2_fast((part_max[p0 + s] - M) * kLog2e);
+        O = fmaf(e, part_out[(p0 + s) * kHeadDim + c], O);
+        L = fmaf(e, part_lse[p0 + s], L);
+    }
+    store_out<DT>(out, (size_t)bh * kHeadDim + c, O / L);
+}
+
+template <int DT, int kMode>
+__global__ __launch_bounds__(kBlock) void split_kernel(SplitArgs a) {
+    using R = Row<DT>;
+    __shared__ float s_m[kWaves];
+    __shared__ float s_l[kWaves];
+    __shared__ float s_acc[kWaves][kHeadDim];
+
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int slot_row = lane / R::kLanes, slice = lane % R::kLanes;
+
+    Item it;
+    const bool active = locate(a, blockIdx.x, it);
+    if constexpr (kMode != kCoopMerge) {
+        if (!active) return;
+    }
+    const int bh = it.b * a.NH + it.h;
+    const size_t pidx = (size_t)bh * a.S + it.s;
+
+    if (active) {
+        int j0, j1;
+        if (a.seg_rows > 0) {
+            j0 = it.s * a.seg_rows;
+            j1 = min(j0 + a.seg_rows, it.total);
+        } else {
+            const int chunk = ceil_div_i(it.total, a.S);
+            j0 = it.s * chunk;
+            j1 = min(j0 + chunk, it.total);
+        }
+        if (j1 <= j0) {
+            // Empty segment (reference partition with total < S): neutral partial.
+            if (wave == 0) {
+                a.part_out[pidx * kHeadDim + lane] = 0.0f;
+                if (lane == 0) { a.part_max[pidx] = kEmptyMax; a.part_lse[pidx] = 0.0f; }
+            }
+        } else {
+            float q[R::kElems];
+            load_q<DT>(a.qkv, it.b, it.h, a.NH, slice, a.qscale, q);
+            const Slot sl = make_slot<DT>(a.kv, a.kv_scale, a.B, a.NH, a.maxT, bh, slice);
+            const int per_wave = ceil_div_i(j1 - j0, kWaves);
+            const int w0 = min(j0 + wave * per_wave, j1);
+            const int w1 = min(w0 + per_wave, j1);
+            float m = kStartMax, l = 0.0f, acc[R::kElems];
+#pragma unroll
+            for (int e = 0; e < R::kElems; ++e) acc[e] = 0.0f;
+            online_rows<DT>(sl, w0, w1, slot_row, q, m, l, acc);
+
+            // Combine the row slots of this wave, then the 4 waves.
+            const float mw = slot_reduce<R::kLanes, true>(m);
+            const float f = exp2_fast(m - mw);
+            l = slot_reduce<R::kLanes, false>(l * f);
+#pragma unroll
+            for (int e = 0; e < R::kElems; ++e) acc[e] = slot_reduce<R::kLanes, false>(acc[e] * f);
+            if (lane == 0) { s_m[wave] = mw; s_l[wave] = l; }
+            if (slot_row == 0) {
+#pragma unroll
+                for (int e = 0; e < R::kElems; ++e) s_acc[wave][slice * R::kElems + e] = acc[e];
+            }
+            __syncthreads();
+            if (wave == 0) {
+                float Mb = s_m[0];
+#pragma unroll
+                for (int w = 1; w < kWaves; ++w) Mb = fmaxf(Mb, s_m[w]);
+                float L = 0.0f, A = 0.0f;
+#pragma unroll
+                for (int w = 0; w < kWaves; ++w) {
+                    const float g = exp2_fast(s_m[w] - Mb);
+                    L = fmaf(g, s_l[w], L);
+                    A = fmaf(g, s_acc[w][lane], A);
+                }
+                a.part_out[pidx * kHeadDim + lane] = A;
+                if (lane == 0) { a.part_max[pidx] = Mb * kLn2; a.part_lse[pidx] = L; }
+            }
+        }
+    }
+
+    if constexpr (kMode == kLastBlockMerge) {
+        // Wave 0 wrote this segment's partial.  Release it at agent scope, count the
+        // segment, and let the last segment of (b,h) to arrive acquire all partials,
+        // merge them and re-arm the counter for the next call.
+        if (wave == 0) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+            __builtin_amdgcn_wave_barrier();
+            unsigned prev = 0;
+            if (lane == 0)
+                prev = __hip_atomic_fetch_add(a.counters + bh, 1u, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+            prev = __shfl(prev, 0);
+            if (prev == (unsigned)(it.n_seg - 1)) {
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+                merge_partials<DT>(a.out, a.part_out, a.part_lse, a.part_max, a.S, it.n_seg, bh, lane);
+                if (lane == 0)
+                    __hip_atomic_store(a.counters + bh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    } else if constexpr (kMode == kCoopMerge) {
+        cooperative_groups::this_grid().sync();
+        if (active && it.s == 0 && wave == 0)
+            merge_partials<DT>(a.out, a.part_out, a.part_lse, a.part_max, a.S, it.n_seg, bh, lane);
+    }
+}
+
+// Stand-alone merge: one wave per (b,h).
+template <int DT>
+__global__ __launch_bounds__(kWave) void merge_kernel(SplitArgs a) {
+    const int bh = blockIdx.x;
+    const int b = bh / a.NH;
+    int n_seg = a.S;
+    if (a.seg_rows > 0) n_seg = ceil_div_i(seq_total(a.cur_len, a.lens_per_seq, b, a.maxT), a.seg_rows);
+    merge_partials<DT>(a.out, a.part_out, a.part_lse, a.part_max, a.S, n_seg, bh, threadIdx.x);
+}
+
+// ------------------------------------------------------------------------------------
+// KV append.
+// ------------------------------------------------------------------------------------
+// F32 / BF16: one thread per 16-byte chunk of the 2*B*NH rows (K rows, then V rows).
+template <int DT>
+__global__ __launch_bounds__(kBlock) void cache_write_kernel(uint8_t* __restrict__ kv, const uint8_t* __restrict__ qkv,
+                                                             const int* __restrict__ cur_len, int lens_per_seq,
+                                                             int B, int NH, int maxT) {
+    constexpr int kChunks = Row<DT>::kBytes / 16;
+    const int t = blockIdx.x * kBlock + threadIdx.x;
+    const int rows = 2 * B * NH;
+    if (t >= rows * kChunks) return;
+    const int row = t / kChunks, c = t - row * kChunks;
+    const int is_v = row >= B * NH;
+    const int kh = row - is_v * B * NH;
+    const int b = kh / NH, h = kh - b * NH;
+    const int cl = seq_total(cur_len, lens_per_seq, b, maxT) - 1;
+    const size_t src = (((size_t)b * 3 + 1 + is_v) * NH + h) * Row<DT>::kBytes + c * 16;
+    const size_t dst = ((size_t)is_v * B * NH * maxT + (size_t)kh * maxT + cl) * Row<DT>::kBytes + c * 16;
+    *reinterpret_cast<uint4*>(kv + dst) = *reinterpret_cast<const uint4*>(qkv + src);
+}
+
+// INT8 / FP8: one wave per row, lane c = channel c.  amax over the row, scale =
+// amax / limit (127 or 448, IEEE division), codes of x / scale, zero codes for a zero row.
+template <int DT>
+__global__ __launch_bounds__(kBlock) void cache_write_w8_kernel(uint8_t* __restrict__ kv, float* __restrict__ kv_scale,
+                                                                const uint16_t* __restrict__ qkv,
+                                                                const int* __restrict__ cur_len, int lens_per_seq,
+                                                                int B, int NH, int maxT) {
+    const int row = blockIdx.x * kWaves + threadIdx.x / kWave;
+    const int c = threadIdx.x & (kWave - 1);
+    if (row >= 2 * B * NH) return;
+    const int is_v = row >= B * NH;
+    const int kh = row - is_v * B * NH;
+    const int b = kh / NH, h = kh - b * NH;
+    const int cl = seq_total(cur_len, lens_per_seq, b, maxT) - 1;
+    const float x = bf16_to_f32(qkv[(((size_t)b * 3 + 1 + is_v) * NH + h) * kHeadDim + c]);
+    const float amax = wave_max(fabsf(x));
+    const float limit = DT == KVATTN_KV_FP8_E4M3 ? 448.0f : 127.0f;
+    const float scale = amax / limit;
+    uint8_t code = 0;
+    if (scale > 0.0f) {
+        const float y = x / scale;
+        if constexpr (DT == KVATTN_KV_FP8_E4M3) {
+            code = f32_to_e4m3_sat(y);
+        } else {
+            int qv = (int)rintf(y);
+            qv = qv < -127 ? -127 : (qv > 127 ? 127 : qv);
+            code = (uint8_t)(int8_t)qv;
+        }
+    }
+    const size_t r = (size_t)is_v * B * NH * maxT + (size_t)kh * maxT + cl;
+    kv[r * kHeadDim + c] = code;
+    if (c == 0) kv_scale[r] = scale;
+}
+
+__device__ int g_cur_len = 0;
+
+// ------------------------------------------------------------------------------------
+// Host side.
+// ------------------------------------------------------------------------------------
+thread_local int t_last_hip_error = 0;
+
+#define KV_HIP(expr)                                            \
+    do {                                                        \
+        hipError_t e_ = (expr);                                 \
+        if (e_ != hipSuccess) {                                 \
+            t_last_hip_error = (int)e_;                         \
+            return KVATTN_ERR_HIP;                              \
+        }                                                       \
+    } while (0)
+
+#define KV_TRY(expr)                      \
+    do {                                  \
+        int st_ = (expr);                 \
+        if (st_ != KVATTN_OK) return st_; \
+    } while (0)
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+bool is_8bit(int dt) { return dt == KVATTN_KV_INT8 || dt == KVATTN_KV_FP8_E4M3; }
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int resolve_len(const int*& p) {
+    if (p) return KVATTN_OK;
+    int dev = 0;
+    KV_HIP(hipGetDevice(&dev));
+    static std::mutex mu;
+    static std::map<int, int*> cache;
+    std::lock_guard<std::mutex> lock(mu);
+    auto itc = cache.find(dev);
+    if (itc == cache.end()) {
+        int* ptr = nullptr;
+        KV_HIP(hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(g_cur_len)));
+        itc = cache.emplace(dev, ptr).first;
+    }
+    p = itc->second;
+    return KVATTN_OK;
+}
+
+int check_common(const void* qkv, const void* kv, const float* kv_scale, int B, int NH, int hs,
+                 int maxT, int kv_dtype) {
+    if (hs != kHeadDim) return KVATTN_ERR_HEAD_DIM;
+    if (B < 1 || NH < 1 || maxT < 1 || maxT > kMaxT) return KVATTN_ERR_SHAPE;
+    if ((long long)B * NH > (1ll << 24)) return KVATTN_ERR_SHAPE;
+    if (kv_dtype < KVATTN_KV_F32 || kv_dtype > KVATTN_KV_FP8_E4M3) return KVATTN_ERR_DTYPE;
+    if (!qkv || !kv) return KVATTN_ERR_NULL_POINTER;
+    if (is_8bit(kv_dtype) && !kv_scale) return KVATTN_ERR_DTYPE;
+    if (!aligned16(qkv) || !aligned16(kv)) return KVATTN_ERR_MISALIGNED;
+    if (is_8bit(kv_dtype) && ((uintptr_t)kv_scale & 3u)) return KVATTN_ERR_MISALIGNED;
+    return KVATTN_OK;
+}
+
+float qscale_for(int hs) { return (1.0f / sqrtf((float)hs)) * kLog2e; }
+
+template <typename F>
+int dispatch_dtype(int dt, F&& f) {
+    switch (dt) {
+        case KVATTN_KV_F32: return f(std::integral_constant<int, KVATTN_KV_F32>{});
+        case KVATTN_KV_BF16: return f(std::integral_constant<int, KVATTN_KV_BF16>{});
+        case KVATTN_KV_INT8: return f(std::integral_constant<int, KVATTN_KV_INT8>{});
+        case KVATTN_KV_FP8_E4M3: return f(std::integral_constant<int, KVATTN_KV_FP8_E4M3>{});
+        default: return KVATTN_ERR_DTYPE;
+    }
+}
+
+int launch_fused_single(void* out, const void* qkv, const void* kv, const float* kv_scale, int B, int NH,
+                        int maxT, const int* cur_len, int lens_per_seq, int kv_dtype, hipStream_t stream) {
+    const size_t lds = (size_t)maxT * sizeof(float);
+    if (lds > kFusedMaxLds) return KVATTN_ERR_LDS;
+    const float qs = qscale_for(kHeadDim);
+    return dispatch_dtype(kv_dtype, [&](auto dtc) -> int {
+        constexpr int DT = decltype(dtc)::value;
+        hipLaunchKernelGGL((fused_single_kernel<DT>), dim3(B * NH), dim3(kBlock), lds, stream, out, qkv,
+                           (const uint8_t*)kv, kv_scale, cur_len, lens_per_seq, B, NH, maxT, qs);
+        KV_HIP(hipGetLastError());
+        return KVATTN_OK;
+    });
+}
+
+template <int DT>
+void* split_fn(int mode) {
+    switch (mode) {
+        case kPartialsOnly: return (void*)&split_kernel<DT, kPartialsOnly>;
+        case kLastBlockMerge: return (void*)&split_kernel<DT, kLastBlockMerge>;
+        default: return (void*)&split_kernel<DT, kCoopMerge>;
+    }
+}
+
+int launch_split(const SplitArgs& a, int kv_dtype, int mode, hipStream_t stream) {
+    const dim3 grid((unsigned)a.B * a.NH * a.S), block(kBlock);
+    return dispatch_dtype(kv_dtype, [&](auto dtc) -> int {
+        constexpr int DT = decltype(dtc)::value;
+        if (mode == kPartialsOnly)
+            hipLaunchKernelGGL((split_kernel<DT, kPartialsOnly>), grid, block, 0, stream, a);
+        else
+            hipLaunchKernelGGL((split_kernel<DT, kLastBlockMerge>), grid, block, 0, stream, a);
+        KV_HIP(hipGetLastError());
+        return KVATTN_OK;
+    });
+}
+
+int launch_merge(const SplitArgs& a, int kv_dtype, hipStream_t stream) {
+    return dispatch_dtype(kv_dtype, [&](auto dtc) -> int {
+        constexpr int DT = decltype(dtc)::value;
+        hipLaunchKernelGGL((merge_kernel<DT>), dim3(a.B * a.NH), dim3(kWave), 0, stream, a);
+        KV_HIP(hipGetLastError());
+        return KVATTN_OK;
+    });
+}
+
+int stream_capturing(hipStream_t stream, bool& capturing) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    KV_HIP(hipStreamIsCapturing(stream, &st));
+    capturing = st != hipStreamCaptureStatusNone;
+    return KVATTN_OK;
+}
+
+int launch_coop(const SplitArgs& a, int kv_dtype, hipStream_t stream) {
+    bool capturing = false;
+    KV_TRY(stream_capturing(stream, capturing));
+    if (capturing) return KVATTN_ERR_CAPTURE;
+    int dev = 0, cus = 0, coop = 0;
+    KV_HIP(hipGetDevice(&dev));
+    KV_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    KV_HIP(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev));
+    if (!coop) return KVATTN_ERR_COOP_TOO_LARGE;
+    const long long blocks = (long long)a.B * a.NH * a.S;
+    return dispatch_dtype(kv_dtype, [&](auto dtc) -> int {
+        constexpr int DT = decltype(dtc)::value;
+        const void* fn = (const void*)&split_kernel<DT, kCoopMerge>;
+        int per_cu = 0;
+        KV_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kBlock, 0));
+        if (blocks > (long long)per_cu * cus) return KVATTN_ERR_COOP_TOO_LARGE;
+        SplitArgs args = a;
+        void* params[] = {&args};
+        KV_HIP(hipLaunchCooperativeKernel(fn, dim3((unsigned)blocks), dim3(kBlock), params, 0, stream));
+        return KVATTN_OK;
+    });
+}
+
+// hipGraph holding the split and merge kernel nodes, built once per argument set.
+struct GraphKey {
+    int dev, dt;
+    const void *out, *qkv, *kv, *ks, *len, *po, *pl, *pm;
+    int lens_per_seq, B, NH, maxT, S, seg_rows;
+    bool operator<(const GraphKey& o) const {
+        return std::tie(dev, dt, out, qkv, kv, ks, len, po, pl, pm, lens_per_seq, B, NH, maxT, S, seg_rows) <
+               std::tie(o.dev, o.dt, o.out, o.qkv, o.kv, o.ks, o.len, o.po, o.pl, o.pm, o.lens_per_seq, o.B, o.NH,
+                        o.maxT, o.S, o.seg_rows);
+    }
+};
+
+int launch_graph_pair(const SplitArgs& a, int kv_dtype, hipStream_t stream) {
+    bool capturing = false;
+    KV_TRY(stream_capturing(stream, capturing));
+    if (capturing) {
+        // Inside a caller's capture the two kernels become nodes of the caller's graph.
+        KV_TRY(launch_split(a, kv_dtype, kPartialsOnly, stream));
+        return launch_merge(a, kv_dtype, stream);
+    }
+    int dev = 0;
+    KV_HIP(hipGetDevice(&dev));
+    GraphKey key{dev, kv_dtype, a.out, a.qkv, a.kv, a.kv_scale, a.cur_len, a.part_out, a.part_lse, a.part_max,
+                 a.lens_per_seq, a.B, a.NH, a.maxT, a.S, a.seg_rows};
+    static std::mutex mu;
+    static std::map<GraphKey, hipGraphExec_t> cache;
+    std::lock_guard<std::mutex> lock(mu);
+    auto itc = cache.find(key);
+    if (itc == cache.end()) {
+        if (cache.size() >= 256) {
+            for (auto& kvp : cache) (void)hipGraphExecDestroy(kvp.second);
+            cache.clear();
+        }
+        void* fsplit = nullptr;
+        void* fmerge = nullptr;
+        dispatch_dtype(kv_dtype, [&](auto dtc) -> int {
+            constexpr int DT = decltype(dtc)::value;
+            fsplit = (void*)&split_kernel<DT, kPartialsOnly>;
+            fmerge = (void*)&merge_kernel<DT>;
+            return KVATTN_OK;
+        });
+        SplitArgs args = a;
+        void* params[] = {&args};
+        hipGraph_t g = nullptr;
+        KV_HIP(hipGraphCreate(&g, 0));
+        hipKernelNodeParams ps{};
+        ps.func = fsplit;
+        ps.gridDim = dim3((unsigned)a.B * a.NH * a.S);
+        ps.blockDim = dim3(kBlock);
+        ps.sharedMemBytes = 0;
+        ps.kernelParams = params;
+        ps.extra = nullptr;
+        hipGraphNode_t nsplit = nullptr, nmerge = nullptr;
+        hipError_t e = hipGraphAddKernelNode(&nsplit, g, nullptr, 0, &ps);
+        if (e == hipSuccess) {
+            hipKernelNodeParams pm = ps;
+            pm.func = fmerge;
+            pm.gridDim = dim3((unsigned)a.B * a.NH);
+            pm.blockDim = dim3(kWave);
+            e = hipGraphAddKernelNode(&nmerge, g, &nsplit, 1, &pm);
+        }
+        hipGraphExec_t exec = nullptr;
+        if (e == hipSuccess) e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        if (e != hipSuccess) {
+            t_last_hip_error = (int)e;
+            return KVATTN_ERR_HIP;
+        }
+        itc = cache.emplace(key, exec).first;
+    }
+    KV_HIP(hipGraphLaunch(itc->second, stream));
+    return KVATTN_OK;
+}
+
+// Workspace: [counters B*NH u32][part_max][part_lse][part_out], each 256-byte aligned.
+struct Workspace {
+    unsigned* counters;
+    float* part_max;
+    float* part_lse;
+    float* part_out;
+    size_t bytes;
+};
+
+Workspace carve(void* base, int B, int NH, int S) {
+    const size_t bh = (size_t)B * NH;
+    const size_t nc = align_up(bh * sizeof(unsigned), 256);
+    const size_t nm = align_up(bh * S * sizeof(float), 256);
+    const size_t no = align_up(bh * S * kHeadDim * sizeof(float), 256);
+    Workspace w;
+    uint8_t* p = (uint8_t*)base;
+    w.counters = (unsigned*)p;
+    w.part_max = (float*)(p + nc);
+    w.part_lse = (float*)(p + nc + nm);
+    w.part_out = (float*)(p + nc + 2 * nm);
+    w.bytes = nc + 2 * nm + no;
+    return w;
+}
+
+// S > 0: reference partition, S slots.  S < 0: -S rows per segment.  S == 0: sized for
+// the smallest automatic segment length.
+int segment_slots(int maxT, int S, int& slots, int& seg_rows) {
+    if (S > 0) {
+        if (S > kMaxSegments) return KVATTN_ERR_SPLIT;
+        slots = S;
+        seg_rows = 0;
+        return KVATTN_OK;
+    }
+    seg_rows = S < 0 ? -S : kMinSegRows;
+    if (seg_rows < 1) return KVATTN_ERR_SPLIT;
+    slots = ceil_div_i(maxT, seg_rows);
+    if (slots > kMaxSegments) return KVATTN_ERR_SPLIT;
+    return KVATTN_OK;
+}
+
+// Automatic rows per segment: enough segments to give every CU a couple of
+// workgroups, never shorter than kMinSegRows rows, at most 1024.
+int auto_seg_rows(int B, int NH, int total_hint) {
+    const long long work = (long long)B * NH * total_hint;
+    long long rows = (work + 511) / 512;
+    int r = kMinSegRows;
+    while (r < rows && r < 1024) r <<= 1;
+    return r;
+}
+
+constexpr int kFusedMaxRows = 256;   // AUTO: fused_single up to this many positions
+
+int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scale, int B, int NH, int hs,
+                int maxT, const int* d_cur_len, int lens_per_seq, int len_hint, void* workspace,
+                size_t workspace_bytes, int S, int strategy, int kv_dtype, void* stream_v) {
+    KV_TRY(check_common(qkv, kv, kv_scale, B, NH, hs, maxT, kv_dtype));
+    if (!out) return KVATTN_ERR_NULL_POINTER;
+    if (!aligned16(out)) return KVATTN_ERR_MISALIGNED;
+    if (strategy < KVATTN_AUTO || strategy > KVATTN_SPLIT_LASTBLOCK) return KVATTN_ERR_STRATEGY;
+    if (len_hint >= maxT || len_hint < -1) return KVATTN_ERR_LENGTH;
+    KV_TRY(resolve_len(d_cur_len));
+    hipStream_t stream = (hipStream_t)stream_v;
+    const int total_hint = (len_hint < 0 ? maxT - 1 : len_hint) + 1;
+
+    if (strategy == KVATTN_AUTO) {
+        const bool fits = (size_t)maxT * sizeof(float) <= kFusedMaxLds;
+        strategy = (fits && total_hint <= kFusedMaxRows) ? KVATTN_FUSED_SINGLE : KVATTN_SPLIT_LASTBLOCK;
+    }
+    if (strategy == KVATTN_FUSED_SINGLE)
+        return launch_fused_single(out, qkv, kv, kv_scale, B, NH, maxT, d_cur_len, lens_per_seq, kv_dtype, stream);
+
+    int slots = 0, seg_rows = 0;
+    KV_TRY(segment_slots(maxT, S, slots, seg_rows));
+    if (S == 0) {
+        seg_rows = auto_seg_rows(B, NH, total_hint);
+        slots = ceil_div_i(maxT, seg_rows);
+    }
+    if ((long long)B * NH * slots >= (1ll << 31)) return KVATTN_ERR_SHAPE;
+    if (!workspace) return KVATTN_ERR_WORKSPACE;
+    if (!aligned16(workspace)) return KVATTN_ERR_MISALIGNED;
+    const Workspace w = carve(workspace, B, NH, slots);
+    if (w.bytes > workspace_bytes) return KVATTN_ERR_WORKSPACE;
+
+    SplitArgs a{};
+    a.out = out;
+    a.part_out = w.part_out;
+    a.part_lse = w.part_lse;
+    a.part_max = w.part_max;
+    a.counters = w.counters;
+    a.qkv = qkv;
+    a.kv = (const uint8_t*)kv;
+    a.kv_scale = kv_scale;
+    a.cur_len = d_cur_len;
+    a.lens_per_seq = lens_per_seq ? 1 : 0;
+    a.B = B;
+    a.NH = NH;
+    a.maxT = maxT;
+    a.S = slots;
+    a.seg_rows = seg_rows;
+    a.qscale = qscale_for(hs);
+
+    switch (strategy) {
+        case KVATTN_SPLIT_MERGE:
+            KV_TRY(launch_split(a, kv_dtype, kPartialsOnly, stream));
+            return launch_merge(a, kv_dtype, stream);
+        case KVATTN_SPLIT_LASTBLOCK: return launch_split(a, kv_dtype, kLastBlockMerge, stream);
+        case KVATTN_SINGLE_LAUNCH_COOP: return launch_coop(a, kv_dtype, stream);
+        case KVATTN_SINGLE_LAUNCH_GRAPH: return launch_graph_pair(a, kv_dtype, stream);
+        default: return KVATTN_ERR_STRATEGY;
+    }
+}
+
+SplitArgs caller_partials(void* out, const void* qkv, const void* kv, const float* kv_scale, int B, int NH,
+                          int maxT, const int* cur_len, int lens_per_seq, float* part_out, float* part_lse,
+                          float* part_max, int S) {
+    SplitArgs a{};
+    a.out = out;
+    a.part_out = part_out;
+    a.part_lse = part_lse;
+    a.part_max = part_max;
+    a.counters = nullptr;
+    a.qkv = qkv;
+    a.kv = (const uint8_t*)kv;
+    a.kv_scale = kv_scale;
+    a.cur_len = cur_len;
+    a.lens_per_seq = lens_per_seq ? 1 : 0;
+    a.B = B;
+    a.NH = NH;
+    a.maxT = maxT;
+    a.S = S;
+    a.seg_rows = 0;
+    a.qscale = qscale_for(kHeadDim);
+    return a;
+}
+
+int check_partials(const float* po, const float* pl, const float* pm, int S) {
+    if (!po || !pl || !pm) return KVATTN_ERR_NULL_POINTER;
+    if (!aligned16(po) || ((uintptr_t)pl & 3u) || ((uintptr_t)pm & 3u)) return KVATTN_ERR_MISALIGNED;
+    if (S < 1 || S > kMaxSegments) return KVATTN_ERR_SPLIT;
+    return KVATTN_OK;
+}
+
+}  // namespace
+
+// ======================================================================================
+// C ABI
+// ======================================================================================
+extern "C" {
+
+const char* kvattn_strerror(int status) {
+    switch (status) {
+        case KVATTN_OK: return "ok";
+        case KVATTN_ERR_NULL_POINTER: return "a required pointer is NULL";
+        case KVATTN_ERR_MISALIGNED: return "a buffer is not 16-byte aligned";
+        case KVATTN_ERR_HEAD_DIM: return "head size must be 64";
+        case KVATTN_ERR_SHAPE: return "B, NH or maxT out of range";
+        case KVATTN_ERR_DTYPE: return "unknown kv dtype or missing kv_scale for an 8-bit cache";
+        case KVATTN_ERR_STRATEGY: return "unknown strategy";
+        case KVATTN_ERR_WORKSPACE: return "workspace missing or too small";
+        case KVATTN_ERR_SPLIT: return "segment count or segment length out of range";
+        case KVATTN_ERR_COOP_TOO_LARGE: return "cooperative grid exceeds co-resident capacity";
+        case KVATTN_ERR_LDS: return "fused_single scores for maxT exceed the LDS budget";
+        case KVATTN_ERR_CAPTURE: return "cooperative launch is not allowed inside stream capture";
+        case KVATTN_ERR_LENGTH: return "length hint outside [-1, maxT-1]";
+        case KVATTN_ERR_HIP: return "HIP runtime error";
+        default: return "unknown status";
+    }
+}
+
+int kvattn_last_hip_error(void) { return t_last_hip_error; }
+
+int kvattn_cur_len_symbol(int** d_cur_len) {
+    if (!d_cur_len) return KVATTN_ERR_NULL_POINTER;
+    const int* p = nullptr;
+    KV_TRY(resolve_len(p));
+    *d_cur_len = const_cast<int*>(p);
+    return KVATTN_OK;
+}
+
+int kvattn_set_cur_len(int cur_len) {
+    KV_HIP(hipMemcpyToSymbol(HIP_SYMBOL(g_cur_len), &cur_len, sizeof(int), 0, hipMemcpyHostToDevice));
+    return KVATTN_OK;
+}
+
+int kvattn_cache_write(void* kv_cache, float* kv_scale, const void* qkv, int B, int NH, int hs, int maxT,
+                       const int* d_cur_len, int lens_per_seq, int kv_dtype, void* stream_v) {
+    KV_TRY(check_common(qkv, kv_cache, kv_scale, B, NH, hs, maxT, kv_dtype));
+    KV_TRY(resolve_len(d_cur_len));
+    hipStream_t stream = (hipStream_t)stream_v;
+    const int lps = lens_per_seq ? 1 : 0;
+    return dispatch_dtype(kv_dtype, [&](auto dtc) -> int {
+        constexpr int DT = decltype(dtc)::value;
+        if constexpr (Row<DT>::k8bit) {
+            const int rows = 2 * B * NH;
+            hipLaunchKernelGGL((cache_write_w8_kernel<DT>), dim3((rows + kWaves - 1) / kWaves), dim3(kBlock), 0,
+                               stream, (uint8_t*)kv_cache, kv_scale, (const uint16_t*)qkv, d_cur_len, lps, B, NH,
+                               maxT);
+        } else {
+            const int chunks = 2 * B * NH * (Row<DT>::kBytes / 16);
+            hipLaunchKernelGGL((cache_write_kernel<DT>), dim3((chunks + kBlock - 1) / kBlock), dim3(kBlock), 0,
+                               stream, (uint8_t*)kv_cache, (const uint8_t*)qkv, d_cur_len, lps, B, NH, maxT);
+        }
+        KV_HIP(hipGetLastError());
+        return KVATTN_OK;
+    });
+}
+
+int kvattn_forward_small(void* out, const void* qkv, const void* kv_cache, const float* kv_scale, int B, int NH,
+                         int hs, int maxT, const int* d_cur_len, int lens_per_seq, int kv_dtype, void* stream) {
+    KV_TRY(check_common(qkv, kv_cache, kv_scale, B, NH, hs, maxT, kv_dtype));
+    if (!out) return KVATTN_ERR_NULL_POINTER;
+    if (!aligned16(out)) return KVATTN_ERR_MISALIGNED;
+    KV_TRY(resolve_len(d_cur_len));
+    return launch_fused_single(out, qkv, kv_cache, kv_scale, B, NH, maxT, d_cur_len, lens_per_seq, kv_dtype,
+                               (hipStream_t)stream);
+}
+
+int kvattn_forward_large(void* out, const void* qkv, const void* kv_cache, const float* kv_scale, int B, int NH,
+                         int hs, int maxT, const int* d_cur_len, int lens_per_seq, float* part_out,
+                         float* part_lse, float* part_max, int S, int kv_dtype, void* stream_v) {
+    KV_TRY(check_common(qkv, kv_cache, kv_scale, B, NH, hs, maxT, kv_dtype));
+    if (!out) return KVATTN_ERR_NULL_POINTER;
+    if (!aligned16(out)) return KVATTN_ERR_MISALIGNED;
+    KV_TRY(check_partials(part_out, part_lse, part_max, S));
+    KV_TRY(resolve_len(d_cur_len));
+    hipStream_t stream = (hipStream_t)stream_v;
+    const SplitArgs a = caller_partials(out, qkv, kv_cache, kv_scale, B, NH, maxT, d_cur_len, lens_per_seq,
+                                        part_out, part_lse, part_max, S);
+    bool capturing = false;
+    KV_TRY(stream_capturing(stream, capturing));
+    if (B == 1 && !capturing) {
+        const int st = launch_coop(a, kv_dtype, stream);
+        if (st != KVATTN_ERR_COOP_TOO_LARGE) return st;
+    }
+    KV_TRY(launch_split(a, kv_dtype, kPartialsOnly, stream));
+    return launch_merge(a, kv_dtype, stream);
+}
+
+int kvattn_split(float* part_out, float* part_lse, float* part_max, const void* qkv, const void* kv_cache,
+                 const float* kv_scale, int B, int NH, int hs, int maxT, const int* d_cur_len, int lens_per_seq,
+                 int S, int kv_dtype, void* stream) {
+    KV_TRY(check_common(qkv, kv_cache, kv_scale, B, NH, hs, maxT, kv_dtype));
+    KV_TRY(check_partials(part_out, part_lse, part_max, S));
+    KV_TRY(resolve_len(d_cur_len));
+    const SplitArgs a = caller_partials(nullptr, qkv, kv_cache, kv_scale, B, NH, maxT, d_cur_len, lens_per_seq,
+                                        part_out, part_lse, part_max, S);
+    return launch_split(a, kv_dtype, kPartialsOnly, (hipStream_t)stream);
+}
+
+int kvattn_merge(void* out, const float* part_out, const float* part_lse, const float* part_max, int B, int NH,
+                 int hs, int S, int kv_dtype, void* stream) {
+    if (hs != kHeadDim) return KVATTN_ERR_HEAD_DIM;
+    if (B < 1 || NH < 1 || (long long)B * NH > (1ll << 24)) return KVATTN_ERR_SHAPE;
+    if (kv_dtype < KVATTN_KV_F32 || kv_dtype > KVATTN_KV_FP8_E4M3) return KVATTN_ERR_DTYPE;
+    if (!out) return KVATTN_ERR_NULL_POINTER;
+    if (!aligned16(out)) return KVATTN_ERR_MISALIGNED;
+    KV_TRY(check_partials(part_out, part_lse, part_max, S));
+    SplitArgs a = caller_partials(out, nullptr, nullptr, nullptr, B, NH, 1, nullptr, 0,
+                                  const_cast<float*>(part_out), const_cast<float*>(part_lse),
+                                  const_cast<float*>(part_max), S);
+    return launch_merge(a, kv_dtype, (hipStream_t)stream);
+}
+
+size_t kvattn_workspace_bytes(int B, int NH, int hs, int maxT, int S) {
+    if (hs != kHeadDim || B < 1 || NH < 1 || maxT < 1 || maxT > kMaxT) return 0;
+    int slots = 0, seg_rows = 0;
+    if (segment_slots(maxT, S, slots, seg_rows) != KVATTN_OK) return 0;
+    return carve(nullptr, B, NH, slots).bytes;
+}
+
+int kvattn_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
+    if (!workspace) return KVATTN_ERR_NULL_POINTER;
+    KV_HIP(hipMemsetAsync(workspace, 0, workspace_bytes, (hipStream_t)stream));
+    return KVATTN_OK;
+}
+
+int kvattn_decode(void* out, const void* qkv, const void* kv_cache, const float* kv_scale, int B, int NH, int hs,
+                  int maxT, const int* d_cur_len, int lens_per_seq, int len_hint, void* workspace,
+                  size_t workspace_bytes, int S, int strategy, int kv_dtype, void* stream) {
+    return decode_impl(out, qkv, kv_cache, kv_scale, B, NH, hs, maxT, d_cur_len, lens_per_seq, len_hint,
+                       workspace, workspace_bytes, S, strategy, kv_dtype, stream);
+}
+
+}  // extern "C"

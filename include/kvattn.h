@@ -1,0 +1,169 @@
+/* kvattn.h -- C ABI of the MI355X (gfx950) decode-phase KV-cache attention library.
+ *
+ * Drop-in for the attention call inside a GPT-2 decode step: the same q / K-cache /
+ * V-cache / out pointer layouts as the reference engine, the same [NH, maxT, hs] cache
+ * slot per (batch, head), a device-resident current length (so captured graphs stay
+ * valid while the length grows), and the FP32 / BF16 / INT8 / FP8-E4M3 KV switch, here a
+ * run-time argument instead of a compile-time macro.
+ *
+ * Layouts (reference names; element type below):
+ *   qkv       [B][3][NH][hs]             Q, K, V of the current token
+ *   kv_cache  [2][B][NH][maxT][hs]       K block then V block; K(b,h,j) at
+ *                                        ((b*NH+h)*maxT + j)*hs, V adds B*NH*maxT*hs
+ *   kv_scale  [2][B][NH][maxT] float     per-row scales, 8-bit caches only
+ *   out       [B][NH][hs]
+ *   part_out  [B][NH][S][hs] float, part_max / part_lse [B][NH][S] float
+ * Element types: kv_dtype F32 -> qkv, kv_cache, out are float.  BF16 -> bfloat16.
+ * INT8 / FP8_E4M3 -> kv_cache holds one byte per element, qkv and out are bfloat16.
+ *
+ * Lengths: the number of attended positions of sequence b is cur_len + 1 where cur_len
+ * is read ON THE DEVICE when the kernels run: from d_cur_len[0] for every sequence, or
+ * from d_cur_len[b] when lens_per_seq != 0 (ragged batches).  d_cur_len == NULL means
+ * the library's own device-resident length, see kvattn_cur_len_symbol().  Device lengths
+ * are clamped into [0, maxT-1]; the host never reads them.
+ *
+ * Every entry point only enqueues work on `stream` (a hipStream_t; NULL = the null
+ * stream), returns a kvattn_status and never exits the process.  All except the
+ * cooperative strategy are legal inside hipStreamBeginCapture / hipStreamEndCapture.
+ * Only hs == 64 is supported (one 64-lane wavefront spans one head row).
+ */
+#ifndef KVATTN_H
+#define KVATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum kvattn_status {
+    KVATTN_OK = 0,
+    KVATTN_ERR_NULL_POINTER = 1,    /* a required pointer is NULL */
+    KVATTN_ERR_MISALIGNED = 2,      /* qkv / kv_cache / out / workspace not 16-byte aligned */
+    KVATTN_ERR_HEAD_DIM = 3,        /* hs != 64 */
+    KVATTN_ERR_SHAPE = 4,           /* B, NH or maxT < 1, or a size that overflows */
+    KVATTN_ERR_DTYPE = 5,           /* unknown kv_dtype, or kv_scale missing for 8-bit */
+    KVATTN_ERR_STRATEGY = 6,        /* unknown strategy */
+    KVATTN_ERR_WORKSPACE = 7,       /* workspace missing or smaller than required */
+    KVATTN_ERR_SPLIT = 8,           /* S or seg_rows out of range */
+    KVATTN_ERR_COOP_TOO_LARGE = 9,  /* cooperative grid exceeds co-resident capacity */
+    KVATTN_ERR_LDS = 10,            /* fused_single scores for maxT do not fit in LDS */
+    KVATTN_ERR_CAPTURE = 11,        /* cooperative launch requested inside stream capture */
+    KVATTN_ERR_LENGTH = 12,         /* host length hint outside [0, maxT-1] */
+    KVATTN_ERR_HIP = 13             /* a HIP runtime call failed; see kvattn_last_hip_error */
+} kvattn_status;
+
+typedef enum kvattn_dtype {
+    KVATTN_KV_F32 = 0,       /* reference ENABLE_FP32 build (Makefile:78-79) */
+    KVATTN_KV_BF16 = 1,      /* reference default BF16 build (Makefile:88-89) */
+    KVATTN_KV_INT8 = 2,      /* reference USE_KV_W8 + USE_INT8 (Makefile:80-82,100-106) */
+    KVATTN_KV_FP8_E4M3 = 3   /* reference USE_KV_W8 + USE_FP8 (Makefile:83-85,100-106) */
+} kvattn_dtype;
+
+typedef enum kvattn_strategy {
+    KVATTN_AUTO = 0,                /* fused_single for short contexts, else split with
+                                       in-kernel merge; chosen from len_hint */
+    KVATTN_FUSED_SINGLE = 1,        /* one workgroup per (b,h), scores staged in LDS */
+    KVATTN_SPLIT_MERGE = 2,         /* flash-decoding: split kernel + merge kernel */
+    KVATTN_SINGLE_LAUNCH_COOP = 3,  /* split + grid barrier + merge, cooperative launch */
+    KVATTN_SINGLE_LAUNCH_GRAPH = 4, /* split + merge pair replayed as one hipGraph launch */
+    KVATTN_SPLIT_LASTBLOCK = 5      /* split kernel whose last finishing segment of each
+                                       (b,h) merges: one ordinary launch, capturable */
+} kvattn_strategy;
+
+/* Human-readable text of a status code. */
+const char* kvattn_strerror(int status);
+
+/* The hipError_t of the most recent failing HIP call on this thread (0 if none). */
+int kvattn_last_hip_error(void);
+
+/* Device address of the library's device-resident length for the current device.
+ * Replaces cudaGetSymbolAddress(&d_cur_len_ptr, g_cur_len)
+ * (inference_gpt2_opt.cu:252-254; g_cur_len at Inference_gpt2/attention_kvcache.cuh:35-40). */
+int kvattn_cur_len_symbol(int** d_cur_len);
+
+/* Blocking write of the library's device-resident length.
+ * Replaces cudaMemcpyToSymbol(g_cur_len, &cur_len, sizeof(int))
+ * (inference_gpt2_opt.cu:409,548). */
+int kvattn_set_cur_len(int cur_len);
+
+/* Append the current token's K and V (from qkv) into column cur_len of every (b,h) slot.
+ * F32/BF16 copy the elements; INT8/FP8 quantise each 64-element row with
+ * scale = amax/127 (INT8) or amax/448 (FP8), store the codes and the FP32 scale.
+ * Replaces kv_cache_write_kernel (Inference_gpt2/attention_kvcache.cuh:46-64) and
+ * kv_cache_write_kernel_w8 (Inference_gpt2/attention_kvcache_w8.cuh:115-155), launched at
+ * inference_gpt2_opt.cu:302-303 and :329.  kv_scale must be NULL for F32/BF16. */
+int kvattn_cache_write(void* kv_cache, float* kv_scale, const void* qkv,
+                       int B, int NH, int hs, int maxT,
+                       const int* d_cur_len, int lens_per_seq,
+                       int kv_dtype, void* stream);
+
+/* Short-context path: one workgroup per (b,h), scores staged in LDS.
+ * Replaces attention_forward_kv_small (Inference_gpt2/attention_kvcache.cuh:453-459) and
+ * attention_forward_kv_small_w8 (Inference_gpt2/attention_kvcache_w8.cuh:529-536). */
+int kvattn_forward_small(void* out, const void* qkv, const void* kv_cache,
+                         const float* kv_scale, int B, int NH, int hs, int maxT,
+                         const int* d_cur_len, int lens_per_seq,
+                         int kv_dtype, void* stream);
+
+/* Long-context path with caller-owned partials of S segments per (b,h).  As in the
+ * reference, B == 1 uses the cooperative single launch and B > 1 the split + merge pair.
+ * Replaces attention_forward_kv_large (Inference_gpt2/attention_kvcache.cuh:464-487) and
+ * attention_forward_kv_large_w8 (Inference_gpt2/attention_kvcache_w8.cuh:541-566). */
+int kvattn_forward_large(void* out, const void* qkv, const void* kv_cache,
+                         const float* kv_scale, int B, int NH, int hs, int maxT,
+                         const int* d_cur_len, int lens_per_seq,
+                         float* part_out, float* part_lse, float* part_max, int S,
+                         int kv_dtype, void* stream);
+
+/* Split phase alone: segment s of (b,h) covers [s*chunk, min((s+1)*chunk, total)) with
+ * chunk = ceil(total/S); an empty segment writes (max=-FLT_MAX, lse=0, out=0).
+ * Replaces the attention_kv_split_kernel[_w8] launches used under graph capture
+ * (inference_gpt2_opt.cu:310-312,338-339; kernels at attention_kvcache.cuh:185-288 and
+ * attention_kvcache_w8.cuh:260-363). */
+int kvattn_split(float* part_out, float* part_lse, float* part_max,
+                 const void* qkv, const void* kv_cache, const float* kv_scale,
+                 int B, int NH, int hs, int maxT,
+                 const int* d_cur_len, int lens_per_seq, int S,
+                 int kv_dtype, void* stream);
+
+/* Merge phase alone: out = sum_s e_s*part_out_s / sum_s e_s*part_lse_s with
+ * e_s = exp(part_max_s - max_s part_max_s).  `out` is float when kv_dtype is F32, else
+ * bfloat16.  Replaces the attention_kv_merge_kernel[_w8] launches
+ * (inference_gpt2_opt.cu:313-314,340-341; kernels at attention_kvcache.cuh:298-318 and
+ * attention_kvcache_w8.cuh:374-396). */
+int kvattn_merge(void* out, const float* part_out, const float* part_lse,
+                 const float* part_max, int B, int NH, int hs, int S,
+                 int kv_dtype, void* stream);
+
+/* Bytes of workspace kvattn_decode needs for (B, NH, hs, maxT, S).  S > 0 sizes for
+ * exactly S segments per (b,h); S == 0 sizes for every automatic choice. */
+size_t kvattn_workspace_bytes(int B, int NH, int hs, int maxT, int S);
+
+/* Zero the workspace's merge counters.  Call once after allocating a workspace and
+ * before the first kvattn_decode on it (outside any graph capture); the kernels leave the
+ * counters at zero after every call. */
+int kvattn_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
+
+/* One decode-attention call with an explicit strategy, the unified entry the per-layer
+ * attention block of forward_kv_graph_ready (inference_gpt2_opt.cu:298-347) maps onto.
+ *   strategy   kvattn_strategy; AUTO picks from len_hint (the host's view of cur_len,
+ *              used for the choice only; -1 = unknown, treated as maxT-1).
+ *   S          segments per (b,h) for the split strategies: S > 0 uses the reference
+ *              partition chunk = ceil(total/S); S == 0 lets the library pick a fixed
+ *              number of rows per segment and the per-sequence count from each length.
+ *   workspace  device memory of kvattn_workspace_bytes(B, NH, hs, maxT, S) bytes,
+ *              initialised once with kvattn_workspace_init; may be NULL for
+ *              FUSED_SINGLE.  Calls sharing a workspace must be ordered (one stream).
+ */
+int kvattn_decode(void* out, const void* qkv, const void* kv_cache, const float* kv_scale,
+                  int B, int NH, int hs, int maxT,
+                  const int* d_cur_len, int lens_per_seq, int len_hint,
+                  void* workspace, size_t workspace_bytes,
+                  int S, int strategy, int kv_dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KVATTN_H */

@@ -1,0 +1,114 @@
+"""CPU checks of the C ABI: the library loads, exports every symbol include/kvattn.h
+declares, and rejects bad arguments with status codes before touching a GPU."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "kvattn.h")
+
+
+def _kv():
+    from cuda_gpt2_inference_amd import kvattn
+    return kvattn
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(kvattn_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    kvattn = _kv()
+    lib = kvattn.lib()
+    declared = header_functions()
+    assert len(declared) >= 12
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in kvattn.h but not exported"
+    assert set(declared) == set(kvattn.SIGNATURES), "ctypes signatures out of sync with kvattn.h"
+
+
+def test_symbols_are_c_linkage():
+    """extern "C": exported names are unmangled (dlsym by plain name works)."""
+    so = ctypes.CDLL(_kv().LIB_PATH)
+    for name in header_functions():
+        assert getattr(so, name) is not None
+
+
+def test_strerror_covers_every_status():
+    kvattn = _kv()
+    seen = set()
+    for st in range(0, 14):
+        msg = kvattn.strerror(st)
+        assert msg and msg != "unknown status"
+        seen.add(msg)
+    assert len(seen) == 14
+    assert kvattn.strerror(99) == "unknown status"
+
+
+def test_workspace_bytes():
+    kvattn = _kv()
+    # counters (B*NH u32), part_max, part_lse (B*NH*S f32), part_out (B*NH*S*64 f32),
+    # every region rounded up to 256 bytes.
+    def expect(B, NH, S):
+        up = lambda x: (x + 255) // 256 * 256  # noqa: E731
+        return up(B * NH * 4) + 2 * up(B * NH * S * 4) + up(B * NH * S * 64 * 4)
+    assert kvattn.workspace_bytes(1, 12, 64, 1024, 8) == expect(1, 12, 8)
+    assert kvattn.workspace_bytes(64, 12, 64, 8192, 0) == expect(64, 12, 8192 // 64)
+    assert kvattn.workspace_bytes(2, 3, 64, 1000, -100) == expect(2, 3, 10)
+    assert kvattn.workspace_bytes(1, 12, 32, 1024, 8) == 0      # hs != 64
+    assert kvattn.workspace_bytes(0, 12, 64, 1024, 8) == 0      # B < 1
+
+
+ALIGNED = 1 << 20   # a fake, 16-byte aligned address; never dereferenced by these calls
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(hs=32), 3),                       # KVATTN_ERR_HEAD_DIM
+    (dict(B=0), 4),                         # KVATTN_ERR_SHAPE
+    (dict(maxT=0), 4),
+    (dict(kv_dtype=7), 5),                  # KVATTN_ERR_DTYPE
+    (dict(kv_dtype=2, kv_scale=None), 5),   # 8-bit without scales
+    (dict(qkv=None), 1),                    # KVATTN_ERR_NULL_POINTER
+    (dict(out=None), 1),
+    (dict(kv=ALIGNED + 8), 2),              # KVATTN_ERR_MISALIGNED
+    (dict(strategy=9), 6),                  # KVATTN_ERR_STRATEGY
+    (dict(len_hint=5000), 12),              # KVATTN_ERR_LENGTH
+])
+def test_decode_argument_errors(kw, status):
+    kvattn = _kv()
+    a = dict(out=ALIGNED, qkv=ALIGNED, kv=ALIGNED, kv_scale=ALIGNED, B=1, NH=12, hs=64, maxT=1024,
+             kv_dtype=1, strategy=0, len_hint=-1)
+    a.update(kw)
+    st = kvattn.lib().kvattn_decode(a["out"], a["qkv"], a["kv"], a["kv_scale"], a["B"], a["NH"], a["hs"],
+                                    a["maxT"], None, 0, a["len_hint"], None, 0, 0, a["strategy"],
+                                    a["kv_dtype"], None)
+    assert st == status, kvattn.strerror(st)
+
+
+def test_other_entry_point_errors():
+    kvattn = _kv()
+    L = kvattn.lib()
+    assert L.kvattn_cache_write(ALIGNED, None, ALIGNED, 1, 12, 48, 1024, None, 0, 1, None) == kvattn.ERR_HEAD_DIM
+    assert L.kvattn_cache_write(ALIGNED, None, ALIGNED, 1, 12, 64, 1024, None, 0, 3, None) == kvattn.ERR_DTYPE
+    assert L.kvattn_forward_small(None, ALIGNED, ALIGNED, None, 1, 12, 64, 1024, None, 0, 1, None) == \
+        kvattn.ERR_NULL_POINTER
+    assert L.kvattn_forward_large(ALIGNED, ALIGNED, ALIGNED, None, 1, 12, 64, 1024, None, 0, ALIGNED, ALIGNED,
+                                  ALIGNED, 0, 1, None) == kvattn.ERR_SPLIT
+    assert L.kvattn_split(ALIGNED, None, ALIGNED, ALIGNED, ALIGNED, None, 1, 12, 64, 1024, None, 0, 8, 1,
+                          None) == kvattn.ERR_NULL_POINTER
+    assert L.kvattn_merge(ALIGNED, ALIGNED, ALIGNED, ALIGNED, 1, 12, 64, 1 << 20, 1, None) == kvattn.ERR_SPLIT
+    assert L.kvattn_merge(ALIGNED + 4, ALIGNED, ALIGNED, ALIGNED, 1, 12, 64, 8, 1, None) == kvattn.ERR_MISALIGNED
+    assert L.kvattn_cur_len_symbol(None) == kvattn.ERR_NULL_POINTER
+    assert L.kvattn_workspace_init(None, 0, None) == kvattn.ERR_NULL_POINTER
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    kvattn = _kv()
+    monkeypatch.setattr(kvattn, "_LIB", None)
+    monkeypatch.setattr(kvattn, "LIB_PATH", str(tmp_path / "libkvattn.so"))
+    with pytest.raises(kvattn.KvAttnError):
+        kvattn.lib()

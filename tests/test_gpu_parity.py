@@ -1,0 +1,379 @@
+"""GPU parity of the HIP decode attention against the CPU oracle (runs on an MI355X).
+
+Tolerances (stated per dtype in kvcases.TOL): FP32 1e-5, BF16 1e-2, 8-bit 2e-2, as
+norm-wise relative error per (b,h) and max-abs error relative to max|ref|.  Cache appends
+and 8-bit codes/scales are compared bit for bit.
+"""
+import numpy as np
+import pytest
+
+from kvcases import HS, TOL, assert_close, make_case, out_tensor, to_device
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+ALL_DT = ["f32", "bf16", "int8", "fp8"]
+SPLIT_STRATS = ["split_merge", "lastblock", "graph", "coop"]
+
+
+def _kv():
+    from cuda_gpt2_inference_amd import kvattn
+    return kvattn
+
+
+def _run(case, dev, strategy, S=0, len_hint=-1, ws_S=None):
+    import torch
+    kvattn = _kv()
+    qkv, cache, scale, cur = to_device(case, dev)
+    out = out_tensor(case, dev)
+    ws = kvattn.Workspace(case.B, case.NH, case.maxT, S if ws_S is None else ws_S)
+    kvattn.decode(out, qkv, cache, case.B, case.NH, HS, case.maxT, kv_dtype=case.dtype, kv_scale=scale,
+                  cur_len=cur, lens_per_seq=True, len_hint=len_hint, S=S, strategy=strategy, **ws.kwargs())
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+# ---------------------------------------------------------------------------------
+# KV append
+# ---------------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_append_copy_bitexact(dev, dtype):
+    import torch
+    kvattn = _kv()
+    B, NH, maxT = 3, 5, 40
+    case = make_case(dtype, B, NH, maxT, [0, 17, 39], seed=11)
+    qkv, cache, _, cur = to_device(case, dev)
+    kvattn.kv_cache_write(cache, qkv, B, NH, HS, maxT, kv_dtype=dtype, cur_len=cur, lens_per_seq=True)
+    torch.cuda.synchronize()
+    ref = case.cache_raw.copy()
+    oracle.cache_write(ref, case.qkv_raw, case.cur_lens, B, NH, HS, maxT)
+    got = cache.cpu().numpy() if dtype == "f32" else cache.view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got.view(np.uint8), ref.view(np.uint8))
+
+
+@pytest.mark.parametrize("dtype", ["int8", "fp8"])
+def test_append_w8_codes_bitexact(dev, dtype):
+    """Fill a whole 8-bit cache by one append per position; codes and scales bit-exact.
+    Source values N(0,1) with 1% outliers x8, plus an all-zero row (scale 0, zero codes)."""
+    import torch
+    kvattn = _kv()
+    B, NH, maxT = 2, 3, 96
+    fmt = oracle.W8_INT8 if dtype == "int8" else oracle.W8_FP8_E4M3
+    vals = oracle.gen_normal(21, maxT * B * 3 * NH * HS).reshape(maxT, B, 3, NH, HS)
+    rng = np.random.RandomState(5)
+    vals = np.where(rng.random_sample(vals.shape) < 0.01, vals * 8.0, vals).astype(np.float32)
+    vals[7, 1, 1, 2, :] = 0.0            # zero K row at position 7 of (b=1, h=2)
+    vals[9, 0, 2, 0, :5] = 448.0 * 3     # large values (FP8 saturation region after scaling)
+    bits = oracle.bf16_round(vals)
+    src = oracle.bf16_decode(bits)
+    codes = torch.zeros(2 * B * NH * maxT * HS, dtype=torch.uint8, device=dev)
+    scales = torch.full((2 * B * NH * maxT,), -1.0, dtype=torch.float32, device=dev)
+    ref_codes = np.zeros(2 * B * NH * maxT * HS, dtype=np.uint8)
+    ref_scales = np.full(2 * B * NH * maxT, -1.0, dtype=np.float32)
+    cur = torch.zeros(1, dtype=torch.int32, device=dev)
+    for j in range(maxT):
+        qkv = torch.from_numpy(bits[j].reshape(-1).view(np.int16)).to(dev).view(torch.bfloat16)
+        cur.fill_(j)
+        kvattn.kv_cache_write(codes, qkv, B, NH, HS, maxT, kv_dtype=dtype, kv_scale=scales, cur_len=cur)
+        oracle.cache_write_w8(ref_codes, ref_scales, src[j].reshape(-1), [j] * B, B, NH, HS, maxT, fmt)
+    torch.cuda.synchronize()
+    got_codes = codes.cpu().numpy()
+    got_scales = scales.cpu().numpy()
+    assert np.array_equal(got_scales.view(np.uint32), ref_scales.view(np.uint32))
+    assert np.array_equal(got_codes, ref_codes)
+    assert ref_scales.reshape(2, B, NH, maxT)[0, 1, 2, 7] == 0.0
+
+
+def test_fp8_hardware_decode_matches_ocp_table(dev):
+    """Every finite E4M3 code through the kernel's hardware conversion: V rows hold codes
+    0..255 (NaN codes replaced by 0), scale 1, one attended position -> out = decode(code)
+    exactly (E4M3 values are exact in bf16)."""
+    import torch
+    kvattn = _kv()
+    B, NH, maxT = 1, 4, 1
+    codes = np.arange(256, dtype=np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0
+    cache = np.zeros(2 * B * NH * maxT * HS, dtype=np.uint8)
+    cache[B * NH * maxT * HS:] = codes
+    scales = np.ones(2 * B * NH * maxT, dtype=np.float32)
+    qkv = np.zeros(B * 3 * NH * HS, dtype=np.uint16)
+    out = torch.empty(B * NH * HS, dtype=torch.bfloat16, device=dev)
+    kvattn.attention_forward_kv_small(out, torch.from_numpy(qkv.view(np.int16)).to(dev).view(torch.bfloat16),
+                                      torch.from_numpy(cache).to(dev), B, NH, HS, maxT, kv_dtype="fp8",
+                                      kv_scale=torch.from_numpy(scales).to(dev),
+                                      cur_len=torch.zeros(1, dtype=torch.int32, device=dev))
+    torch.cuda.synchronize()
+    expect = np.array([oracle.fp8_to_f32(int(c)) for c in codes], dtype=np.float32)
+    assert np.array_equal(out.float().cpu().numpy(), expect)
+
+
+# ---------------------------------------------------------------------------------
+# FP32 fused_single at the GPT-2 single-layer shape and the reference lab's inputs
+# ---------------------------------------------------------------------------------
+def test_c1_fp32_fused_single(dev):
+    case = make_case("f32", 1, 12, 256, 255, seed=1)
+    got = _run(case, dev, "fused_single")
+    assert_close(got, case.reference(), "f32", "C1 fused_single")
+
+
+@pytest.mark.parametrize("strategy", ["fused_single"] + SPLIT_STRATS + ["auto"])
+def test_reference_lab_inputs_fp32(dev, strategy):
+    """srand(0) inputs of attention_kvcache/attention_kvcache.cu:952,979-980 (B=1, NH=12,
+    maxT=1024), at the lab's check lengths {1,64,256,512,1024} (:1014).  The lab passes at
+    1e-4 absolute (:1038); the bar here is 1e-5 relative plus 1e-4 absolute."""
+    base = make_case("f32", 1, 12, 1024, 0, seed=0, source="lab")
+    for total in (1, 64, 256, 512, 1024):
+        base.cur_lens[:] = total - 1
+        S = max(4, min(32, (total + 127) // 128)) if strategy in SPLIT_STRATS else 0
+        got = _run(base, dev, strategy, S=S, len_hint=total - 1)
+        ref = base.reference()
+        assert_close(got, ref, "f32", f"lab {strategy} T={total}")
+        assert np.abs(got - ref.reshape(-1)).max() <= 1e-4
+
+
+# ---------------------------------------------------------------------------------
+# Strategies x dtypes
+# ---------------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", ALL_DT)
+@pytest.mark.parametrize("strategy", ["fused_single"] + SPLIT_STRATS)
+def test_strategy_dtype_matrix(dev, dtype, strategy):
+    case = make_case(dtype, 2, 3, 300, [299, 130], seed=3)
+    ref = case.reference()
+    for S in ([0, 8, 64] if strategy in SPLIT_STRATS else [0]):
+        if strategy == "coop" and S == 0:
+            continue
+        got = _run(case, dev, strategy, S=S)
+        assert_close(got, ref, dtype, f"{strategy} {dtype} S={S}")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_empty_segments_total_below_S(dev, dtype):
+    """total < S: the reference partition leaves empty segments (sentinel partials)."""
+    case = make_case(dtype, 1, 4, 64, [2], seed=4)
+    for strategy in SPLIT_STRATS:
+        got = _run(case, dev, strategy, S=8)
+        assert_close(got, case.reference(), dtype, f"{strategy} total=3 S=8")
+
+
+def test_split_partials_match_oracle(dev):
+    """kvattn_split partials (reference format: natural-log max, exp-sum, unnormalised
+    weighted V sum) against the oracle's split restatement, including empty segments."""
+    import torch
+    kvattn = _kv()
+    B, NH, maxT, S = 2, 3, 100, 16
+    case = make_case("f32", B, NH, maxT, [99, 9], seed=8)
+    qkv, cache, _, cur = to_device(case, dev)
+    po = torch.empty(B * NH * S * HS, dtype=torch.float32, device=dev)
+    pl = torch.empty(B * NH * S, dtype=torch.float32, device=dev)
+    pm = torch.empty(B * NH * S, dtype=torch.float32, device=dev)
+    kvattn.attention_kv_split(po, pl, pm, qkv, cache, B, NH, HS, maxT, S, kv_dtype="f32", cur_len=cur,
+                              lens_per_seq=True)
+    torch.cuda.synchronize()
+    rpo, rpl, rpm = oracle.split_partials(case.qkv_host, case.cache_host, case.totals, B, NH, HS, maxT, S)
+    gpo, gpl, gpm = (t.cpu().numpy().reshape(x.shape) for t, x in ((po, rpo), (pl, rpl), (pm, rpm)))
+    empty = rpl == 0.0
+    assert np.array_equal(empty, gpl == 0.0)
+    assert np.all(gpm[empty] == np.float32(-3.4028234663852886e38))
+    assert np.all(gpo[empty] == 0.0)
+    ne = ~empty
+    assert np.allclose(gpm[ne], rpm[ne], rtol=1e-5, atol=1e-5)
+    assert np.allclose(gpl[ne], rpl[ne], rtol=1e-5)
+    assert np.allclose(gpo[ne], rpo[ne], rtol=1e-5, atol=1e-5 * np.abs(rpo).max())
+
+
+def test_merge_of_oracle_partials(dev):
+    import torch
+    kvattn = _kv()
+    B, NH, maxT, S = 1, 12, 200, 7
+    case = make_case("f32", B, NH, maxT, [199], seed=9)
+    rpo, rpl, rpm = oracle.split_partials(case.qkv_host, case.cache_host, case.totals, B, NH, HS, maxT, S)
+    out = torch.empty(B * NH * HS, dtype=torch.float32, device=dev)
+    kvattn.attention_kv_merge(out, torch.from_numpy(rpo.reshape(-1)).to(dev),
+                              torch.from_numpy(rpl.reshape(-1)).to(dev),
+                              torch.from_numpy(rpm.reshape(-1)).to(dev), B, NH, HS, S, kv_dtype="f32")
+    torch.cuda.synchronize()
+    ref = oracle.merge(rpo, rpl, rpm, B, NH, HS, S)
+    assert_close(out.cpu().numpy(), ref, "f32", "merge")
+
+
+@pytest.mark.parametrize("B", [1, 2])
+def test_forward_large_reference_semantics(dev, B):
+    """attention_forward_kv_large: B == 1 -> cooperative, B > 1 -> split + merge, both
+    with caller-owned partials of S = 8 segments (inference_gpt2_opt.cu:711-716)."""
+    import torch
+    kvattn = _kv()
+    NH, maxT, S = 12, 1024, 8
+    for dtype in ALL_DT:
+        case = make_case(dtype, B, NH, maxT, [1023] * B, seed=12)
+        qkv, cache, scale, cur = to_device(case, dev)
+        out = out_tensor(case, dev)
+        po = torch.empty(B * NH * S * HS, dtype=torch.float32, device=dev)
+        pl = torch.empty(B * NH * S, dtype=torch.float32, device=dev)
+        pm = torch.empty(B * NH * S, dtype=torch.float32, device=dev)
+        kvattn.attention_forward_kv_large(out, qkv, cache, B, NH, HS, maxT, po, pl, pm, S, kv_dtype=dtype,
+                                          kv_scale=scale, cur_len=cur)
+        torch.cuda.synchronize()
+        assert_close(out.float().cpu().numpy(), case.reference(), dtype, f"forward_large {dtype} B={B}")
+
+
+# ---------------------------------------------------------------------------------
+# The configurations of the benchmark
+# ---------------------------------------------------------------------------------
+def test_c2_bf16_sweep_auto(dev):
+    """BF16, B=1, NH=12, maxT=1024: AUTO across the fused_single / split switch."""
+    case = make_case("bf16", 1, 12, 1024, 0, seed=2)
+    for total in (1, 2, 7, 63, 64, 65, 149, 150, 151, 255, 256, 257, 511, 700, 1000, 1023, 1024):
+        case.cur_lens[:] = total - 1
+        got = _run(case, dev, "auto", len_hint=total - 1)
+        assert_close(got, case.reference(), "bf16", f"C2 auto T={total}")
+
+
+def test_c3_int8_outliers_8way(dev):
+    case = make_case("int8", 1, 12, 1024, 1023, seed=3, outliers=0.01)
+    for strategy in ("split_merge", "lastblock"):
+        got = _run(case, dev, strategy, S=8)
+        assert_close(got, case.reference(), "int8", f"C3 {strategy}")
+
+
+@pytest.mark.parametrize("total", [512, 1024])
+def test_c4_fp8_single_launch(dev, total):
+    case = make_case("fp8", 1, 12, 1024, total - 1, seed=4)
+    for strategy in ("coop", "graph", "lastblock"):
+        got = _run(case, dev, strategy, S=8)
+        assert_close(got, case.reference(), "fp8", f"C4 {strategy} T={total}")
+
+
+def test_c5_ragged_64_sequences(dev):
+    """64 sequences x NH=12, BF16, maxT=8192, lengths ~ U[1,8192] from a seed (~1.6 GB
+    cache).  Inputs come from torch's seeded generator on the device; 24 (b,h) slots are
+    copied back and checked against the oracle; every slot is checked for the
+    size-independent bound min_j V <= out <= max_j V and all strategies must agree."""
+    import torch
+    kvattn = _kv()
+    B, NH, maxT = 64, 12, 8192
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    lens = torch.randint(1, maxT + 1, (B,), generator=g, device=dev, dtype=torch.int32)
+    cur = (lens - 1).contiguous()
+    cache = torch.randn(2 * B * NH * maxT * HS, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    qkv = torch.randn(B * 3 * NH * HS, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    outs = {}
+    for strategy in ("auto", "split_merge", "lastblock"):
+        out = torch.empty(B * NH * HS, dtype=torch.bfloat16, device=dev)
+        ws = kvattn.Workspace(B, NH, maxT, 0)
+        kvattn.decode(out, qkv, cache, B, NH, HS, maxT, kv_dtype="bf16", cur_len=cur, lens_per_seq=True,
+                      strategy=strategy, **ws.kwargs())
+        torch.cuda.synchronize()
+        outs[strategy] = out.float()
+    lens_h = lens.cpu().numpy()
+    q_h = qkv.float().cpu().numpy()
+    rng = np.random.RandomState(0)
+    picks = [(int(b), int(h)) for b, h in zip(rng.randint(0, B, 24), rng.randint(0, NH, 24))]
+    picks += [(int(np.argmax(lens_h)), 0), (int(np.argmin(lens_h)), NH - 1)]
+    kv5 = cache.view(2, B, NH, maxT, HS)
+    for b, h in picks:
+        T = int(lens_h[b])
+        k = kv5[0, b, h, :T].float().cpu().numpy()
+        v = kv5[1, b, h, :T].float().cpu().numpy()
+        q1 = np.zeros((1, 3, 1, HS), np.float32)
+        q1[0, 0, 0] = q_h.reshape(B, 3, NH, HS)[b, 0, h]
+        c1 = np.stack([k, v]).reshape(-1)
+        ref = oracle.attention_f32(q1.reshape(-1), c1, T, 1, 1, HS, T)
+        for name, o in outs.items():
+            got = o.view(B, NH, HS)[b, h].cpu().numpy()
+            assert_close(got, ref, "bf16", f"C5 {name} b={b} h={h} T={T}")
+    # size-independent checks on every slot
+    pos = torch.arange(maxT, device=dev).view(1, 1, maxT, 1)
+    valid = pos < lens.view(B, 1, 1, 1)
+    vv = kv5[1].float()
+    vmin = torch.where(valid, vv, torch.full_like(vv, float("inf"))).amin(dim=2)
+    vmax = torch.where(valid, vv, torch.full_like(vv, float("-inf"))).amax(dim=2)
+    for name, o in outs.items():
+        o3 = o.view(B, NH, HS)
+        slack = 1e-2 * (vmax - vmin).abs() + 1e-3
+        assert bool(((o3 >= vmin - slack) & (o3 <= vmax + slack)).all()), f"C5 {name} outside V hull"
+        d = (o3 - outs["split_merge"].view(B, NH, HS)).norm(dim=2) / outs["split_merge"].view(B, NH, HS).norm(dim=2)
+        assert float(d.max()) <= 1e-2, f"C5 {name} disagrees with split_merge ({float(d.max()):.3e})"
+
+
+# ---------------------------------------------------------------------------------
+# Graph capture with a device-resident length
+# ---------------------------------------------------------------------------------
+def test_graph_capture_replay_tracks_device_length(dev):
+    """Capture append + decode (AUTO, picked at capture time as split) into a torch CUDA
+    graph once, then replay it while the device length grows; each replay is checked
+    against the oracle (the reference's graph mode, inference_gpt2_opt.cu:420-450,544-579)."""
+    import torch
+    kvattn = _kv()
+    B, NH, maxT = 1, 12, 512
+    case = make_case("bf16", B, NH, maxT, 0, seed=13)
+    qkv, cache, scale, cur = to_device(case, dev)
+    out = out_tensor(case, dev)
+    ws = kvattn.Workspace(B, NH, maxT, 0)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            kvattn.decode(out, qkv, cache, B, NH, HS, maxT, kv_dtype="bf16", cur_len=cur, len_hint=400,
+                          strategy="auto", **ws.kwargs())
+    for total in (300, 301, 450, 512, 200):
+        cur.fill_(total - 1)
+        g.replay()
+        torch.cuda.synchronize()
+        case.cur_lens[:] = total - 1
+        assert_close(out.float().cpu().numpy(), case.reference(), "bf16", f"graph replay T={total}")
+        out.fill_(float("nan"))
+
+
+def test_coop_refused_inside_capture(dev):
+    import torch
+    kvattn = _kv()
+    case = make_case("f32", 1, 2, 64, 63, seed=1)
+    qkv, cache, _, cur = to_device(case, dev)
+    out = out_tensor(case, dev)
+    ws = kvattn.Workspace(1, 2, 64, 8)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    err = None
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            try:
+                kvattn.decode(out, qkv, cache, 1, 2, HS, 64, kv_dtype="f32", cur_len=cur, S=8,
+                              strategy="coop", **ws.kwargs())
+            except kvattn.KvAttnError as e:
+                err = e
+    assert err is not None and err.status == kvattn.ERR_CAPTURE
+
+
+def test_library_length_symbol(dev):
+    """NULL length pointer -> the library's device-resident length (g_cur_len)."""
+    import torch
+    kvattn = _kv()
+    case = make_case("bf16", 1, 12, 128, 0, seed=6)
+    qkv, cache, _, _ = to_device(case, dev)
+    out = out_tensor(case, dev)
+    assert kvattn.cur_len_symbol() != 0
+    for total in (1, 77, 128):
+        kvattn.set_cur_len(total - 1)
+        kvattn.attention_forward_kv_small(out, qkv, cache, 1, 12, HS, 128, kv_dtype="bf16")
+        torch.cuda.synchronize()
+        case.cur_lens[:] = total - 1
+        assert_close(out.float().cpu().numpy(), case.reference(), "bf16", f"g_cur_len T={total}")
+
+
+def test_device_length_out_of_range_is_clamped(dev):
+    import torch
+    case = make_case("f32", 1, 2, 32, 31, seed=2)
+    qkv, cache, _, cur = to_device(case, dev)
+    for bad in (40, 1 << 30):
+        cur.fill_(bad)
+        for strategy in ("fused_single", "lastblock"):
+            from cuda_gpt2_inference_amd import kvattn
+            out = out_tensor(case, dev)
+            ws = kvattn.Workspace(1, 2, 32, 0)
+            kvattn.decode(out, qkv, cache, 1, 2, HS, 32, kv_dtype="f32", cur_len=cur, strategy=strategy,
+                          **ws.kwargs())
+            torch.cuda.synchronize()
+            assert_close(out.cpu().numpy(), case.reference(), "f32", f"clamped {bad} {strategy}")
