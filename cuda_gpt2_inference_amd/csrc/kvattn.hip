@@ -49,6 +49,10 @@ constexpr int kMinSegRows = 64;         // smallest automatic segment length
 constexpr int kMaxSegments = 1 << 16;   // upper bound on segments per (b,h)
 constexpr int kMaxT = 1 << 23;          // keeps per-slot byte offsets inside 32 bits
 constexpr size_t kFusedMaxLds = 64 * 1024;  // dynamic LDS of fused_single (scores)
+#ifndef KVATTN_FUSED_THREADS
+#define KVATTN_FUSED_THREADS 1024
+#endif
+constexpr int kFusedThreads = KVATTN_FUSED_THREADS;  // fused_single workgroup size
 
 // ------------------------------------------------------------------------------------
 // Per-dtype row geometry.
@@ -72,7 +76,13 @@ template <> struct Row<KVATTN_KV_FP8_E4M3> {
 };
 template <int DT> constexpr int kRowsPerLoad = kWave / Row<DT>::kLanes;
 // Row chunks per lane and tile in the unrolled main loops (8-bit rows are 4x denser).
-template <int DT> constexpr int kUnroll = Row<DT>::k8bit ? 4 : 8;
+#ifndef KVATTN_UNROLL_WIDE
+#define KVATTN_UNROLL_WIDE 8
+#endif
+#ifndef KVATTN_UNROLL_BYTE
+#define KVATTN_UNROLL_BYTE 4
+#endif
+template <int DT> constexpr int kUnroll = Row<DT>::k8bit ? KVATTN_UNROLL_BYTE : KVATTN_UNROLL_WIDE;
 
 // ------------------------------------------------------------------------------------
 // Element helpers.
@@ -108,8 +118,18 @@ __device__ __forceinline__ uint8_t f32_to_e4m3_sat(float y) {
     return (uint8_t)(sign | code);
 }
 
+// 16-byte row-chunk load; KVATTN_NT_LOADS=1 marks K/V loads non-temporal (streamed once).
+#ifndef KVATTN_NT_LOADS
+#define KVATTN_NT_LOADS 1
+#endif
 __device__ __forceinline__ uint4 load16(const uint8_t* p) {
+#if KVATTN_NT_LOADS
+    typedef unsigned v4u __attribute__((ext_vector_type(4)));
+    const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+#else
     return *reinterpret_cast<const uint4*>(p);
+#endif
 }
 
 // Decode one lane's 16-byte chunk of a row into kElems floats.
@@ -173,6 +193,23 @@ __device__ __forceinline__ float row_sum(float x) {
     return x;
 }
 
+// op(x, x of lane ^ 16) and op(x, x of lane ^ 32) with the gfx950 row-swap permutes:
+// permlane16_swap / permlane32_swap of x with itself return x with 16-lane rows (resp.
+// 32-lane halves) exchanged in one of the two results, so op over both outputs is op
+// over the lane pair.
+template <bool kMax>
+__device__ __forceinline__ float op_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float a = __uint_as_float(r[0]), b = __uint_as_float(r[1]);
+    return kMax ? fmaxf(a, b) : a + b;
+}
+template <bool kMax>
+__device__ __forceinline__ float op_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float a = __uint_as_float(r[0]), b = __uint_as_float(r[1]);
+    return kMax ? fmaxf(a, b) : a + b;
+}
+
 // Reduce over the lanes that hold the same channel slice of different rows
 // (lane = row_slot * kLanes + slice): every lane receives the result for its slice.
 template <int kLanes, bool kMax>
@@ -180,8 +217,8 @@ __device__ __forceinline__ float slot_reduce(float x) {
     auto op = [](float a, float b) { return kMax ? fmaxf(a, b) : a + b; };
     if constexpr (kLanes == 4) { x = op(x, dpp<kDppRowRor4>(x)); x = op(x, dpp<kDppRowRor8>(x)); }
     if constexpr (kLanes == 8) { x = op(x, dpp<kDppRowRor8>(x)); }
-    x = op(x, __shfl_xor(x, 16));
-    x = op(x, __shfl_xor(x, 32));
+    x = op_xor16<kMax>(x);
+    x = op_xor32<kMax>(x);
     return x;
 }
 
@@ -190,8 +227,18 @@ __device__ __forceinline__ float wave_max(float x) {
     x = fmaxf(x, dpp<kDppQuadXor2>(x));
     x = fmaxf(x, dpp<kDppHalfMirror>(x));
     x = fmaxf(x, dpp<kDppRowMirror>(x));
-    x = fmaxf(x, __shfl_xor(x, 16));
-    x = fmaxf(x, __shfl_xor(x, 32));
+    x = op_xor16<true>(x);
+    x = op_xor32<true>(x);
+    return x;
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+    x += dpp<kDppQuadXor1>(x);
+    x += dpp<kDppQuadXor2>(x);
+    x += dpp<kDppHalfMirror>(x);
+    x += dpp<kDppRowMirror>(x);
+    x = op_xor16<false>(x);
+    x = op_xor32<false>(x);
     return x;
 }
 
@@ -204,20 +251,42 @@ __device__ __forceinline__ int seq_total(const int* cur_len, int lens_per_seq, i
     return cl + 1;
 }
 
-// Load this lane's q slice (channels slice*kElems ..) as float, pre-multiplied by
-// scale*log2(e) so dot products come out in base-2 score units.
+// This lane's q slice (channels slice*kElems ..) as raw bytes: 16 bytes, or 32 for the
+// 8-bit caches whose lanes cover 16 bf16 channels.  Converting is deferred until the first
+// K/V tile has been requested so that the q load and the K/V loads overlap.
+template <int DT> struct QRaw {
+    uint4 w[Row<DT>::k8bit ? 2 : 1];
+};
+
 template <int DT>
-__device__ __forceinline__ void load_q(const void* qkv, int b, int h, int NH, int slice, float qscale,
-                                       float (&q)[Row<DT>::kElems]) {
-    const size_t q0 = ((size_t)b * 3 * NH + h) * kHeadDim + (size_t)slice * Row<DT>::kElems;
+__device__ __forceinline__ QRaw<DT> load_q(const void* qkv, int b, int h, int NH, int slice) {
+    constexpr int kActBytes = Row<DT>::kActF32 ? 4 : 2;
+    const size_t q0 = (((size_t)b * 3 * NH + h) * kHeadDim + (size_t)slice * Row<DT>::kElems) * kActBytes;
+    const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(qkv) + q0);
+    QRaw<DT> r;
+#pragma unroll
+    for (int i = 0; i < (Row<DT>::k8bit ? 2 : 1); ++i) r.w[i] = p[i];
+    return r;
+}
+
+// q as float, multiplied by scale*log2(e) so dot products come out in base-2 units.
+template <int DT>
+__device__ __forceinline__ void convert_q(const QRaw<DT>& r, float qscale, float (&q)[Row<DT>::kElems]) {
     if constexpr (Row<DT>::kActF32) {
-        const float* p = reinterpret_cast<const float*>(qkv) + q0;
-#pragma unroll
-        for (int e = 0; e < Row<DT>::kElems; ++e) q[e] = p[e] * qscale;
+        q[0] = __uint_as_float(r.w[0].x) * qscale;
+        q[1] = __uint_as_float(r.w[0].y) * qscale;
+        q[2] = __uint_as_float(r.w[0].z) * qscale;
+        q[3] = __uint_as_float(r.w[0].w) * qscale;
     } else {
-        const uint16_t* p = reinterpret_cast<const uint16_t*>(qkv) + q0;
 #pragma unroll
-        for (int e = 0; e < Row<DT>::kElems; ++e) q[e] = bf16_to_f32(p[e]) * qscale;
+        for (int i = 0; i < (Row<DT>::k8bit ? 2 : 1); ++i) {
+            const uint32_t w[4] = {r.w[i].x, r.w[i].y, r.w[i].z, r.w[i].w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                q[8 * i + 2 * k] = bf16_lo(w[k]) * qscale;
+                q[8 * i + 2 * k + 1] = bf16_hi(w[k]) * qscale;
+            }
+        }
     }
 }
 
@@ -251,36 +320,46 @@ __device__ __forceinline__ Slot make_slot(const uint8_t* kv, const float* kv_sca
 // ------------------------------------------------------------------------------------
 // Online softmax over rows [r0, r1) of a slot by one wave.  Each group of kLanes lanes
 // owns one row per load instruction and keeps its own running (m, l, acc) in base-2
-// units; the groups are combined later.  U row chunks are in flight per lane per tile.
+// units; the groups are combined later.  A tile holds U K and U V row chunks per lane,
+// all requested before any of them is used.
 // ------------------------------------------------------------------------------------
+template <int DT, int U>
+struct Tile {
+    uint4 k[U], v[U];
+    float ks[U], vs[U];
+};
+
 template <int DT, int U, bool kChecked>
-__device__ __forceinline__ void online_tile(const Slot& sl, int r, int r1, int slot_row,
-                                            const float (&q)[Row<DT>::kElems], float& m, float& l,
-                                            float (&acc)[Row<DT>::kElems]) {
+__device__ __forceinline__ void load_tile(Tile<DT, U>& t, const Slot& sl, int r, int r1, int slot_row) {
     using R = Row<DT>;
     constexpr int kRPL = kRowsPerLoad<DT>;
-    uint4 kd[U], vd[U];
-    float ks[U], vs[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int row = r + u * kRPL + slot_row;
-        const bool ok = !kChecked || row < r1;
-        if (ok) {
-            kd[u] = load16(sl.k + (uint32_t)row * R::kBytes);
-            vd[u] = load16(sl.v + (uint32_t)row * R::kBytes);
-            if constexpr (R::k8bit) { ks[u] = sl.ks[row]; vs[u] = sl.vs[row]; }
+        if (!kChecked || row < r1) {
+            t.k[u] = load16(sl.k + (uint32_t)row * R::kBytes);
+            t.v[u] = load16(sl.v + (uint32_t)row * R::kBytes);
+            if constexpr (R::k8bit) { t.ks[u] = sl.ks[row]; t.vs[u] = sl.vs[row]; }
         } else {
-            kd[u] = make_uint4(0u, 0u, 0u, 0u);
-            vd[u] = make_uint4(0u, 0u, 0u, 0u);
-            if constexpr (R::k8bit) { ks[u] = 0.0f; vs[u] = 0.0f; }
+            t.k[u] = make_uint4(0u, 0u, 0u, 0u);
+            t.v[u] = make_uint4(0u, 0u, 0u, 0u);
+            if constexpr (R::k8bit) { t.ks[u] = 0.0f; t.vs[u] = 0.0f; }
         }
     }
+}
+
+template <int DT, int U, bool kChecked>
+__device__ __forceinline__ void consume_tile(const Tile<DT, U>& t, int r, int r1, int slot_row,
+                                             const float (&q)[Row<DT>::kElems], float& m, float& l,
+                                             float (&acc)[Row<DT>::kElems]) {
+    using R = Row<DT>;
+    constexpr int kRPL = kRowsPerLoad<DT>;
     float s[U];
     float mt = m;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        s[u] = row_sum<R::kLanes>(dot_chunk<DT>(q, kd[u]));
-        if constexpr (R::k8bit) s[u] *= ks[u];
+        s[u] = row_sum<R::kLanes>(dot_chunk<DT>(q, t.k[u]));
+        if constexpr (R::k8bit) s[u] *= t.ks[u];
         if (kChecked && r + u * kRPL + slot_row >= r1) s[u] = -INFINITY;
         mt = fmaxf(mt, s[u]);
     }
@@ -292,24 +371,48 @@ __device__ __forceinline__ void online_tile(const Slot& sl, int r, int r1, int s
     for (int u = 0; u < U; ++u) {
         const float p = exp2_fast(s[u] - mt);
         l += p;
-        const float pv = R::k8bit ? p * vs[u] : p;
+        const float pv = R::k8bit ? p * t.vs[u] : p;
         float x[R::kElems];
-        decode<DT>(vd[u], x);
+        decode<DT>(t.v[u], x);
 #pragma unroll
         for (int e = 0; e < R::kElems; ++e) acc[e] = fmaf(pv, x[e], acc[e]);
     }
     m = mt;
 }
 
+// Where this lane's q slice lives; the load is issued after the first tile's K/V loads so
+// that nothing depending on q can be scheduled ahead of them.
+struct QSrc {
+    const void* qkv;
+    int b, h, NH, slice;
+};
+
 template <int DT>
-__device__ __forceinline__ void online_rows(const Slot& sl, int r0, int r1, int slot_row,
-                                            const float (&q)[Row<DT>::kElems], float& m, float& l,
-                                            float (&acc)[Row<DT>::kElems]) {
-    constexpr int kRPL = kRowsPerLoad<DT>;
-    constexpr int kTile = kRPL * kUnroll<DT>;
+__device__ __forceinline__ void online_rows(const Slot& sl, int r0, int r1, int slot_row, const QSrc& qs,
+                                            float qscale, float& m, float& l, float (&acc)[Row<DT>::kElems]) {
+    constexpr int kU = kUnroll<DT>;
+    constexpr int kTile = kRowsPerLoad<DT> * kU;
+    if (r0 >= r1) return;
+    Tile<DT, kU> t;
+    float q[Row<DT>::kElems];
     int r = r0;
-    for (; r + kTile <= r1; r += kTile) online_tile<DT, kUnroll<DT>, false>(sl, r, r1, slot_row, q, m, l, acc);
-    for (; r < r1; r += kRPL) online_tile<DT, 1, true>(sl, r, r1, slot_row, q, m, l, acc);
+    if (r + kTile > r1) {
+        load_tile<DT, kU, true>(t, sl, r, r1, slot_row);
+        convert_q<DT>(load_q<DT>(qs.qkv, qs.b, qs.h, qs.NH, qs.slice), qscale, q);
+        consume_tile<DT, kU, true>(t, r, r1, slot_row, q, m, l, acc);
+        return;
+    }
+    load_tile<DT, kU, false>(t, sl, r, r1, slot_row);
+    convert_q<DT>(load_q<DT>(qs.qkv, qs.b, qs.h, qs.NH, qs.slice), qscale, q);
+    consume_tile<DT, kU, false>(t, r, r1, slot_row, q, m, l, acc);
+    for (r += kTile; r + kTile <= r1; r += kTile) {
+        load_tile<DT, kU, false>(t, sl, r, r1, slot_row);
+        consume_tile<DT, kU, false>(t, r, r1, slot_row, q, m, l, acc);
+    }
+    if (r < r1) {
+        load_tile<DT, kU, true>(t, sl, r, r1, slot_row);
+        consume_tile<DT, kU, true>(t, r, r1, slot_row, q, m, l, acc);
+    }
 }
 
 // ------------------------------------------------------------------------------------
@@ -379,18 +482,20 @@ __device__ __forceinline__ void weight_tile(const Slot& sl, int r, int total, in
     }
 }
 
-template <int DT>
-__global__ __launch_bounds__(kBlock) void fused_single_kernel(
+template <int DT, int kThreads>
+__global__ __launch_bounds__(kThreads) void fused_single_kernel(
     void* __restrict__ out, const void* __restrict__ qkv, const uint8_t* __restrict__ kv,
     const float* __restrict__ kv_scale, const int* __restrict__ cur_len, int lens_per_seq,
     int B, int NH, int maxT, float qscale) {
     using R = Row<DT>;
+    constexpr int kW = kThreads / kWave;
+    constexpr int kU = kUnroll<DT>;
     constexpr int kRPL = kRowsPerLoad<DT>;
-    constexpr int kTile = kRPL * kUnroll<DT>;
+    constexpr int kTile = kRPL * kU;
     extern __shared__ float s_scores[];
-    __shared__ float s_max[kWaves];
-    __shared__ float s_l[kWaves];
-    __shared__ float s_acc[kWaves][kHeadDim];
+    __shared__ float s_max[kW];
+    __shared__ float s_l[kW];
+    __shared__ float s_acc[kW][kHeadDim];
 
     const int bh = blockIdx.x;
     const int b = bh / NH, h = bh - b * NH;
@@ -398,33 +503,67 @@ __global__ __launch_bounds__(kBlock) void fused_single_kernel(
     const int slot_row = lane / R::kLanes, slice = lane % R::kLanes;
     const int total = seq_total(cur_len, lens_per_seq, b, maxT);
 
-    float q[R::kElems];
-    load_q<DT>(qkv, b, h, NH, slice, qscale, q);
     const Slot sl = make_slot<DT>(kv, kv_scale, B, NH, maxT, bh, slice);
+    float q[R::kElems];
 
-    // Pass 1: tiles of kTile rows go round-robin to the 4 waves; single-load steps
-    // finish the remainder.
-    float mloc = kStartMax;
-    const int full = total / kTile * kTile;
-    for (int r = wave * kTile; r < full; r += kWaves * kTile)
-        score_tile<DT, kUnroll<DT>, false>(sl, r, total, slot_row, slice, q, s_scores, mloc);
-    for (int r = full + wave * kRPL; r < total; r += kWaves * kRPL)
-        score_tile<DT, 1, true>(sl, r, total, slot_row, slice, q, s_scores, mloc);
-    mloc = wave_max(mloc);
-    if (lane == 0) s_max[wave] = mloc;
-    __syncthreads();
-    float M = s_max[0];
-#pragma unroll
-    for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_max[w]);
-
-    // Pass 2: the same rows, weighted by exp2(score - M).
     float l = 0.0f, acc[R::kElems];
 #pragma unroll
     for (int e = 0; e < R::kElems; ++e) acc[e] = 0.0f;
-    for (int r = wave * kTile; r < full; r += kWaves * kTile)
-        weight_tile<DT, kUnroll<DT>, false>(sl, r, total, slot_row, M, s_scores, l, acc);
-    for (int r = full + wave * kRPL; r < total; r += kWaves * kRPL)
-        weight_tile<DT, 1, true>(sl, r, total, slot_row, M, s_scores, l, acc);
+
+    if (total <= kW * kTile) {
+        // Every wave owns at most one tile: its K and V rows are requested together, the
+        // scores stay in registers and only the workgroup maximum passes through LDS.
+        const int r = wave * kTile;
+        Tile<DT, kU> t;
+        load_tile<DT, kU, true>(t, sl, r, total, slot_row);
+        convert_q<DT>(load_q<DT>(qkv, b, h, NH, slice), qscale, q);
+        float s[kU];
+        float mloc = kStartMax;
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            s[u] = row_sum<R::kLanes>(dot_chunk<DT>(q, t.k[u]));
+            if constexpr (R::k8bit) s[u] *= t.ks[u];
+            if (r + u * kRPL + slot_row < total) mloc = fmaxf(mloc, s[u]);
+            else s[u] = -INFINITY;
+        }
+        mloc = wave_max(mloc);
+        if (lane == 0) s_max[wave] = mloc;
+        __syncthreads();
+        float M = s_max[0];
+#pragma unroll
+        for (int w = 1; w < kW; ++w) M = fmaxf(M, s_max[w]);
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const float p = exp2_fast(s[u] - M);
+            l += p;
+            const float pv = R::k8bit ? p * t.vs[u] : p;
+            float x[R::kElems];
+            decode<DT>(t.v[u], x);
+#pragma unroll
+            for (int e = 0; e < R::kElems; ++e) acc[e] = fmaf(pv, x[e], acc[e]);
+        }
+    } else {
+        // Scores staged in LDS.  Pass 1: tiles of kTile rows go round-robin to the waves,
+        // every score is written to LDS and the exact maximum is found.
+        convert_q<DT>(load_q<DT>(qkv, b, h, NH, slice), qscale, q);
+        float mloc = kStartMax;
+        const int full = total / kTile * kTile;
+        for (int r = wave * kTile; r < full; r += kW * kTile)
+            score_tile<DT, kU, false>(sl, r, total, slot_row, slice, q, s_scores, mloc);
+        for (int r = full + wave * kTile; r < total; r += kW * kTile)
+            score_tile<DT, kU, true>(sl, r, total, slot_row, slice, q, s_scores, mloc);
+        mloc = wave_max(mloc);
+        if (lane == 0) s_max[wave] = mloc;
+        __syncthreads();
+        float M = s_max[0];
+#pragma unroll
+        for (int w = 1; w < kW; ++w) M = fmaxf(M, s_max[w]);
+        // Pass 2: V rows weighted by exp2(score - M).
+        for (int r = wave * kTile; r < full; r += kW * kTile)
+            weight_tile<DT, kU, false>(sl, r, total, slot_row, M, s_scores, l, acc);
+        for (int r = full + wave * kTile; r < total; r += kW * kTile)
+            weight_tile<DT, kU, true>(sl, r, total, slot_row, M, s_scores, l, acc);
+    }
 
     l = slot_reduce<R::kLanes, false>(l);
 #pragma unroll
@@ -439,7 +578,7 @@ __global__ __launch_bounds__(kBlock) void fused_single_kernel(
         const int c = threadIdx.x;
         float L = 0.0f, A = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) { L += s_l[w]; A += s_acc[w][c]; }
+        for (int w = 0; w < kW; ++w) { L += s_l[w]; A += s_acc[w][c]; }
         store_out<DT>(out, (size_t)bh * kHeadDim + c, A / L);
     }
 }
@@ -520,19 +659,63 @@ __device__ __forceinline__ bool locate(const SplitArgs& a, int x, Item& it) {
     return false;
 }
 
+// Partials of the in-kernel merge travel between workgroups that may sit on different
+// XCDs (each with its own L2).  They are written and read as agent-scope relaxed atomics,
+// which the gfx950 code generator emits as write-through / coherent stores and loads
+// (sc1), so no L2 write-back or invalidate is needed: a writer waits until its stores are
+// acknowledged (vmcnt 0) before it bumps the (b,h) counter, and the workgroup that takes
+// the counter to n_seg reads the partials afterwards.
+template <bool kCoherent>
+__device__ __forceinline__ void put(float* p, float v) {
+    if constexpr (kCoherent) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else *p = v;
+}
+template <bool kCoherent>
+__device__ __forceinline__ float get(const float* p) {
+    if constexpr (kCoherent) return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else return *p;
+}
+// s_waitcnt vmcnt(0) (GFX9 encoding: expcnt and lgkmcnt fields left at their maximum),
+// fenced against compiler reordering on both sides.
+__device__ __forceinline__ void wait_vm_stores() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // Merge the n_seg partials of (b,h) = bh into out; executed by one full wave, lane c
-// producing channel c.
-template <int DT>
+// producing channel c.  Lane s holds the max and exp-sum of segment s (64 segments per
+// round), and the weighted V partials are requested 16 segments at a time together with
+// them, so up to 16 segments merge in a single memory round trip.
+template <int DT, bool kCoherent>
 __device__ __forceinline__ void merge_partials(void* out, const float* part_out, const float* part_lse,
                                                const float* part_max, int S, int n_seg, int bh, int c) {
+    constexpr int kBatch = 16;
     const size_t p0 = (size_t)bh * S;
-    float M = kEmptyMax;
-    for (int s = 0; s < n_seg; ++s) M = fmaxf(M, part_max[p0 + s]);
-    float O = 0.0f, L = 0.0f;
-    for (int s = 0; s < n_seg; ++s) {
-        const float e = exp2_fast((part_max[p0 + s] - M) * kLog2e);
-        O = fmaf(e, part_out[(p0 + s) * kHeadDim + c], O);
-        L = fmaf(e, part_lse[p0 + s], L);
+    float M = kEmptyMax, L = 0.0f, O = 0.0f;
+    for (int s0 = 0; s0 < n_seg; s0 += kWave) {
+        const int n = min(kWave, n_seg - s0);
+        const float pm = c < n ? get<kCoherent>(part_max + p0 + s0 + c) : kEmptyMax;
+        const float pl = c < n ? get<kCoherent>(part_lse + p0 + s0 + c) : 0.0f;
+        float e = 0.0f;
+        for (int k = 0; k < n; k += kBatch) {
+            float v[kBatch];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u)
+                v[u] = (k + u < n) ? get<kCoherent>(part_out + (p0 + s0 + k + u) * kHeadDim + c) : 0.0f;
+            if (k == 0) {
+                // Rescale what earlier rounds accumulated to the new running maximum.
+                const float Mn = fmaxf(M, wave_max(pm));
+                const float f = exp2_fast((M - Mn) * kLog2e);
+                O *= f;
+                L = L * f + wave_sum(exp2_fast((pm - Mn) * kLog2e) * pl);
+                e = exp2_fast((pm - Mn) * kLog2e);
+                M = Mn;
+            }
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u)
+                O = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), k + u)), v[u], O);
+        }
     }
     store_out<DT>(out, (size_t)bh * kHeadDim + c, O / L);
 }
@@ -554,6 +737,7 @@ __global__ __launch_bounds__(kBlock) void split_kernel(SplitArgs a) {
     }
     const int bh = it.b * a.NH + it.h;
     const size_t pidx = (size_t)bh * a.S + it.s;
+    constexpr bool kCoh = kMode == kLastBlockMerge;
 
     if (active) {
         int j0, j1;
@@ -568,12 +752,11 @@ __global__ __launch_bounds__(kBlock) void split_kernel(SplitArgs a) {
         if (j1 <= j0) {
             // Empty segment (reference partition with total < S): neutral partial.
             if (wave == 0) {
-                a.part_out[pidx * kHeadDim + lane] = 0.0f;
-                if (lane == 0) { a.part_max[pidx] = kEmptyMax; a.part_lse[pidx] = 0.0f; }
+                put<kCoh>(a.part_out + pidx * kHeadDim + lane, 0.0f);
+                if (lane == 0) { put<kCoh>(a.part_max + pidx, kEmptyMax); put<kCoh>(a.part_lse + pidx, 0.0f); }
             }
         } else {
-            float q[R::kElems];
-            load_q<DT>(a.qkv, it.b, it.h, a.NH, slice, a.qscale, q);
+            const QSrc qs{a.qkv, it.b, it.h, a.NH, slice};
             const Slot sl = make_slot<DT>(a.kv, a.kv_scale, a.B, a.NH, a.maxT, bh, slice);
             const int per_wave = ceil_div_i(j1 - j0, kWaves);
             const int w0 = min(j0 + wave * per_wave, j1);
@@ -581,7 +764,7 @@ __global__ __launch_bounds__(kBlock) void split_kernel(SplitArgs a) {
             float m = kStartMax, l = 0.0f, acc[R::kElems];
 #pragma unroll
             for (int e = 0; e < R::kElems; ++e) acc[e] = 0.0f;
-            online_rows<DT>(sl, w0, w1, slot_row, q, m, l, acc);
+            online_rows<DT>(sl, w0, w1, slot_row, qs, a.qscale, m, l, acc);
 
             // Combine the row slots of this wave, then the 4 waves.
             const float mw = slot_reduce<R::kLanes, true>(m);
@@ -606,27 +789,27 @@ __global__ __launch_bounds__(kBlock) void split_kernel(SplitArgs a) {
                     L = fmaf(g, s_l[w], L);
                     A = fmaf(g, s_acc[w][lane], A);
                 }
-                a.part_out[pidx * kHeadDim + lane] = A;
-                if (lane == 0) { a.part_max[pidx] = Mb * kLn2; a.part_lse[pidx] = L; }
+                put<kCoh>(a.part_out + pidx * kHeadDim + lane, A);
+                if (lane == 0) { put<kCoh>(a.part_max + pidx, Mb * kLn2); put<kCoh>(a.part_lse + pidx, L); }
             }
         }
     }
 
     if constexpr (kMode == kLastBlockMerge) {
-        // Wave 0 wrote this segment's partial.  Release it at agent scope, count the
-        // segment, and let the last segment of (b,h) to arrive acquire all partials,
-        // merge them and re-arm the counter for the next call.
+        // Wave 0 wrote this segment's partial with coherent stores.  Once they are
+        // acknowledged it counts the segment; the wave that brings the (b,h) counter to
+        // n_seg reads every partial with coherent loads, merges them and re-arms the
+        // counter for the next call.
         if (wave == 0) {
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-            __builtin_amdgcn_wave_barrier();
+            wait_vm_stores();
             unsigned prev = 0;
             if (lane == 0)
                 prev = __hip_atomic_fetch_add(a.counters + bh, 1u, __ATOMIC_RELAXED,
                                               __HIP_MEMORY_SCOPE_AGENT);
             prev = __shfl(prev, 0);
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
             if (prev == (unsigned)(it.n_seg - 1)) {
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-                merge_partials<DT>(a.out, a.part_out, a.part_lse, a.part_max, a.S, it.n_seg, bh, lane);
+                merge_partials<DT, true>(a.out, a.part_out, a.part_lse, a.part_max, a.S, it.n_seg, bh, lane);
                 if (lane == 0)
                     __hip_atomic_store(a.counters + bh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
@@ -634,7 +817,7 @@ __global__ __launch_bounds__(kBlock) void split_kernel(SplitArgs a) {
     } else if constexpr (kMode == kCoopMerge) {
         cooperative_groups::this_grid().sync();
         if (active && it.s == 0 && wave == 0)
-            merge_partials<DT>(a.out, a.part_out, a.part_lse, a.part_max, a.S, it.n_seg, bh, lane);
+            merge_partials<DT, false>(a.out, a.part_out, a.part_lse, a.part_max, a.S, it.n_seg, bh, lane);
     }
 }
 
@@ -645,7 +828,7 @@ __global__ __launch_bounds__(kWave) void merge_kernel(SplitArgs a) {
     const int b = bh / a.NH;
     int n_seg = a.S;
     if (a.seg_rows > 0) n_seg = ceil_div_i(seq_total(a.cur_len, a.lens_per_seq, b, a.maxT), a.seg_rows);
-    merge_partials<DT>(a.out, a.part_out, a.part_lse, a.part_max, a.S, n_seg, bh, threadIdx.x);
+    merge_partials<DT, false>(a.out, a.part_out, a.part_lse, a.part_max, a.S, n_seg, bh, threadIdx.x);
 }
 
 // ------------------------------------------------------------------------------------
@@ -781,7 +964,7 @@ int launch_fused_single(void* out, const void* qkv, const void* kv, const float*
     const float qs = qscale_for(kHeadDim);
     return dispatch_dtype(kv_dtype, [&](auto dtc) -> int {
         constexpr int DT = decltype(dtc)::value;
-        hipLaunchKernelGGL((fused_single_kernel<DT>), dim3(B * NH), dim3(kBlock), lds, stream, out, qkv,
+        hipLaunchKernelGGL((fused_single_kernel<DT, kFusedThreads>), dim3(B * NH), dim3(kFusedThreads), lds, stream, out, qkv,
                            (const uint8_t*)kv, kv_scale, cur_len, lens_per_seq, B, NH, maxT, qs);
         KV_HIP(hipGetLastError());
         return KVATTN_OK;
@@ -963,17 +1146,20 @@ int segment_slots(int maxT, int S, int& slots, int& seg_rows) {
     return KVATTN_OK;
 }
 
-// Automatic rows per segment: enough segments to give every CU a couple of
-// workgroups, never shorter than kMinSegRows rows, at most 1024.
-int auto_seg_rows(int B, int NH, int total_hint) {
-    const long long work = (long long)B * NH * total_hint;
-    long long rows = (work + 511) / 512;
+// Automatic rows per segment: about four segments for the host's length hint, between
+// kMinSegRows and 512 rows.  Small problems (a GPT-2 layer at B=1: 12 heads x 1024
+// positions) then launch ~48 workgroups whose single in-kernel merge round is short;
+// large ones stream 512-row segments, long enough to amortise a partial and short
+// enough to balance ragged lengths across 256 CUs.
+int auto_seg_rows(int total_hint) {
+    const int want = (total_hint + 3) / 4;
     int r = kMinSegRows;
-    while (r < rows && r < 1024) r <<= 1;
+    while (r < want && r < 512) r <<= 1;
     return r;
 }
 
-constexpr int kFusedMaxRows = 256;   // AUTO: fused_single up to this many positions
+constexpr int kFusedMaxRows = 256;        // AUTO: fused_single up to this many positions
+constexpr long long kStreamRows = 1 << 19; // AUTO: split + merge kernel from this many rows
 
 int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scale, int B, int NH, int hs,
                 int maxT, const int* d_cur_len, int lens_per_seq, int len_hint, void* workspace,
@@ -988,8 +1174,13 @@ int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scal
     const int total_hint = (len_hint < 0 ? maxT - 1 : len_hint) + 1;
 
     if (strategy == KVATTN_AUTO) {
+        // Short contexts: one workgroup per (b,h).  Otherwise split; a single launch with
+        // the in-kernel merge while the whole call is latency bound, and split + merge
+        // kernel once the call streams enough rows to be bandwidth bound.
         const bool fits = (size_t)maxT * sizeof(float) <= kFusedMaxLds;
-        strategy = (fits && total_hint <= kFusedMaxRows) ? KVATTN_FUSED_SINGLE : KVATTN_SPLIT_LASTBLOCK;
+        if (fits && total_hint <= kFusedMaxRows) strategy = KVATTN_FUSED_SINGLE;
+        else if ((long long)B * NH * total_hint >= kStreamRows) strategy = KVATTN_SPLIT_MERGE;
+        else strategy = KVATTN_SPLIT_LASTBLOCK;
     }
     if (strategy == KVATTN_FUSED_SINGLE)
         return launch_fused_single(out, qkv, kv, kv_scale, B, NH, maxT, d_cur_len, lens_per_seq, kv_dtype, stream);
@@ -997,7 +1188,7 @@ int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scal
     int slots = 0, seg_rows = 0;
     KV_TRY(segment_slots(maxT, S, slots, seg_rows));
     if (S == 0) {
-        seg_rows = auto_seg_rows(B, NH, total_hint);
+        seg_rows = auto_seg_rows(total_hint);
         slots = ceil_div_i(maxT, seg_rows);
     }
     if ((long long)B * NH * slots >= (1ll << 31)) return KVATTN_ERR_SHAPE;

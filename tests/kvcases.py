@@ -45,7 +45,7 @@ def bf16_bits(x: np.ndarray) -> np.ndarray:
 def make_case(dtype: str, B: int, NH: int, maxT: int, cur_lens, seed: int = 0, outliers: float = 0.0,
               source: str = "normal") -> Case:
     """Seeded inputs: q, K, V ~ N(0,1) (or the reference lab's uniform stream)."""
-    cur_lens = np.ascontiguousarray(np.broadcast_to(np.asarray(cur_lens, dtype=np.int32), (B,)))
+    cur_lens = np.array(np.broadcast_to(np.asarray(cur_lens, dtype=np.int32), (B,)), dtype=np.int32)
     n_qkv = B * 3 * NH * HS
     n_cache = 2 * B * NH * maxT * HS
     if source == "lab":
