@@ -5,16 +5,26 @@ Workload of the headline number (value): GPT-2 124M 12-layer decode-attention st
 a BF16 KV cache, B=1, NH=12, hd=64, T=1024 attended positions (cur_len=1023).  A step is
 one decode token: 12 attention calls, one per layer, each over that layer's own cache
 (12 x 3 MiB).  The 12 calls are captured once in a HIP graph and replayed, as the
-reference engine replays its whole-step graph; value = microseconds per attention call.
+reference engine replays its whole-step graph; value = microseconds per attention call
+(the graph runs the 12 kernels back to back, so this is the kernel's own duration plus
+the dispatch gap between graph nodes).
 
-Also reported in the same JSON line:
-  roofline      the dominant kernel (split with in-kernel merge, BF16) at T=1024
-  cpu_baseline  single-threaded restatement of the reference CPU attention on the same
-                shape (the oracle; a reported baseline, not the target)
+Also in the same JSON line:
+  roofline      the dominant kernel of that workload (the split kernel with in-kernel
+                merge, BF16): algorithmic bytes per launch / measured time per launch;
+                `traffic` is the HBM bytes per launch measured with rocprofv3 FETCH_SIZE +
+                WRITE_SIZE (profiles/pmc_traffic.md), null if that summary is absent
+  cpu_baseline  single-threaded restatement of the reference CPU attention
+                (attention_kv_cpu) on the same shape; a reported baseline, not the target
   extra         eager per-call time, and the scaled-up ragged configuration: 64
-                sequences x NH=12, BF16, lengths ~ U[1, 8192] (~0.8 GB of KV read per call)
+                sequences x NH=12, BF16, lengths ~ U[1, 8192] (~0.8 GB of KV per call),
+                which streams from HBM and carries the >=70 % of peak target
 
-Inputs are synthetic (seeded N(0,1)), resident in HBM before timing starts.
+Inputs are synthetic (seeded N(0,1)) and resident in HBM before any timed region.
+
+Modes: default = the measurement above.  `--mode pmc` runs the workloads a few times
+without timing, for `rocprofv3 --pmc FETCH_SIZE|WRITE_SIZE -- python3 bench.py --mode pmc`;
+it first copies 256 MiB device to device as the counters' calibration dispatch.
 """
 from __future__ import annotations
 
@@ -23,7 +33,6 @@ import json
 import os
 import platform
 import sys
-import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 if ROOT not in sys.path:
@@ -32,6 +41,7 @@ if ROOT not in sys.path:
 HBM_PEAK_GBS = 8000.0
 HD = 64
 METRIC = "µs per decode-attention call + achieved HBM GB/s (% of peak), T=1024"
+TRAFFIC_MD = os.path.join(ROOT, "profiles", "pmc_traffic.md")
 
 
 def parse():
@@ -39,6 +49,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200, help="timed decode steps (12 calls each)")
     p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--mode", choices=["full", "pmc"], default="full")
     p.add_argument("--strategy", default="auto")
     p.add_argument("--S", type=int, default=0, help="0 auto, >0 reference partition, <0 rows/segment")
     p.add_argument("--c5-reps", type=int, default=50)
@@ -55,111 +66,123 @@ def bytes_per_call(lengths, NH, kv_bytes, act_bytes, B):
     return int(sum(2 * NH * L * HD * kv_bytes for L in lengths) + B * NH * HD * 2 * act_bytes)
 
 
-def bench_c2(args, torch, kvattn, dev):
+def timed(torch, fn, reps):
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps   # ms per fn()
+
+
+class C2:
+    """12 layers x (B=1, NH=12, maxT=1024) BF16 caches, T=1024."""
     L, B, NH, maxT, T = 12, 1, 12, 1024, 1024
-    g = torch.Generator(device=dev)
-    g.manual_seed(2)
-    caches = [torch.randn(2 * B * NH * maxT * HD, generator=g, device=dev, dtype=torch.float32)
-              .to(torch.bfloat16) for _ in range(L)]
-    qkvs = [torch.randn(B * 3 * NH * HD, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
-            for _ in range(L)]
-    outs = [torch.empty(B * NH * HD, device=dev, dtype=torch.bfloat16) for _ in range(L)]
-    cur = torch.tensor([T - 1], dtype=torch.int32, device=dev)
-    ws = kvattn.Workspace(B, NH, maxT, args.S)
 
-    def step():
-        for l in range(L):
-            kvattn.decode(outs[l], qkvs[l], caches[l], B, NH, HD, maxT, kv_dtype="bf16", cur_len=cur,
-                          len_hint=T - 1, S=args.S, strategy=args.strategy, **ws.kwargs())
+    def __init__(self, args, torch, kvattn, dev):
+        self.torch, self.kvattn, self.args = torch, kvattn, args
+        g = torch.Generator(device=dev)
+        g.manual_seed(2)
+        n_cache = 2 * self.B * self.NH * self.maxT * HD
+        self.caches = [torch.randn(n_cache, generator=g, device=dev).to(torch.bfloat16) for _ in range(self.L)]
+        self.qkvs = [torch.randn(self.B * 3 * self.NH * HD, generator=g, device=dev).to(torch.bfloat16)
+                     for _ in range(self.L)]
+        self.outs = [torch.empty(self.B * self.NH * HD, device=dev, dtype=torch.bfloat16) for _ in range(self.L)]
+        self.cur = torch.tensor([self.T - 1], dtype=torch.int32, device=dev)
+        self.ws = kvattn.Workspace(self.B, self.NH, self.maxT, args.S)
+        self.plan = kvattn.plan(self.B, self.NH, HD, self.maxT, kv_dtype="bf16", len_hint=self.T - 1, S=args.S,
+                                strategy=args.strategy)
 
-    # eager
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(args.steps):
-        step()
-    e1.record()
-    torch.cuda.synchronize()
-    eager_ms_step = e0.elapsed_time(e1) / args.steps
+    def step(self):
+        for l in range(self.L):
+            self.kvattn.decode(self.outs[l], self.qkvs[l], self.caches[l], self.B, self.NH, HD, self.maxT,
+                               kv_dtype="bf16", cur_len=self.cur, len_hint=self.T - 1, S=self.args.S,
+                               strategy=self.args.strategy, **self.ws.kwargs())
 
-    # graph: the 12 calls captured once, replayed per step
-    s = torch.cuda.Stream()
-    graph = torch.cuda.CUDAGraph()
-    torch.cuda.synchronize()
-    with torch.cuda.stream(s):
-        with torch.cuda.graph(graph, stream=s):
-            step()
-    for _ in range(args.warmup):
-        graph.replay()
-    torch.cuda.synchronize()
-    e0.record()
-    for _ in range(args.steps):
-        graph.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    graph_ms_step = e0.elapsed_time(e1) / args.steps
+    def measure(self):
+        torch, a = self.torch, self.args
+        for _ in range(a.warmup):
+            self.step()
+        eager_ms = timed(torch, self.step, a.steps)
+        s = torch.cuda.Stream()
+        graph = torch.cuda.CUDAGraph()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(graph, stream=s):
+                self.step()
+        for _ in range(a.warmup):
+            graph.replay()
+        graph_ms = timed(torch, graph.replay, a.steps)
+        return graph_ms, eager_ms
 
-    # parity spot check of the last layer against a float64 torch reference on the CPU
-    cs = caches[-1].float().view(2, B, NH, maxT, HD)[:, 0, :, :T].cpu().double()
-    q = qkvs[-1].float().view(B, 3, NH, HD)[0, 0].cpu().double()
-    sc = torch.einsum("hd,htd->ht", q, cs[0]) / (HD ** 0.5)
-    ref = torch.einsum("ht,htd->hd", torch.softmax(sc, dim=1), cs[1])
-    got = outs[-1].float().view(NH, HD).cpu().double()
-    rel = float(((got - ref).norm(dim=1) / ref.norm(dim=1)).max())
-    return {
-        "layers": L, "B": B, "NH": NH, "T": T, "maxT": maxT,
-        "graph_ms_step": graph_ms_step, "eager_ms_step": eager_ms_step,
-        "bytes_per_call": bytes_per_call([T], NH, 2, 2, B),
-        "rel_err_vs_f64": rel,
-        "caches": caches, "qkvs": qkvs,
-    }
+    def check(self):
+        """Last layer against a float64 reference computed on the CPU."""
+        torch = self.torch
+        B, NH, T, maxT = self.B, self.NH, self.T, self.maxT
+        cs = self.caches[-1].float().view(2, B, NH, maxT, HD)[:, 0, :, :T].cpu().double()
+        q = self.qkvs[-1].float().view(B, 3, NH, HD)[0, 0].cpu().double()
+        sc = (cs[0] @ q.unsqueeze(-1)).squeeze(-1) / (HD ** 0.5)
+        ref = (torch.softmax(sc, dim=1).unsqueeze(1) @ cs[1]).squeeze(1)
+        got = self.outs[-1].float().view(NH, HD).cpu().double()
+        return float(((got - ref).norm(dim=1) / ref.norm(dim=1)).max())
 
 
-def bench_c5(args, torch, kvattn, dev):
+class C5:
+    """64 sequences x NH=12, BF16, maxT=8192, lengths ~ U[1, 8192] from seed 5."""
     B, NH, maxT = 64, 12, 8192
-    g = torch.Generator(device=dev)
-    g.manual_seed(5)
-    lens = torch.randint(1, maxT + 1, (B,), generator=g, device=dev, dtype=torch.int32)
-    cur = (lens - 1).contiguous()
-    cache = torch.empty(2 * B * NH * maxT * HD, device=dev, dtype=torch.bfloat16)
-    chunk = 1 << 26
-    for i in range(0, cache.numel(), chunk):
-        n = min(chunk, cache.numel() - i)
-        cache[i:i + n] = torch.randn(n, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
-    qkv = torch.randn(B * 3 * NH * HD, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
-    out = torch.empty(B * NH * HD, device=dev, dtype=torch.bfloat16)
-    ws = kvattn.Workspace(B, NH, maxT, args.c5_S)
 
-    def call():
-        kvattn.decode(out, qkv, cache, B, NH, HD, maxT, kv_dtype="bf16", cur_len=cur, lens_per_seq=True,
-                      S=args.c5_S, strategy=args.c5_strategy, **ws.kwargs())
+    def __init__(self, args, torch, kvattn, dev):
+        self.torch, self.kvattn, self.args = torch, kvattn, args
+        g = torch.Generator(device=dev)
+        g.manual_seed(5)
+        self.lens = torch.randint(1, self.maxT + 1, (self.B,), generator=g, device=dev, dtype=torch.int32)
+        self.cur = (self.lens - 1).contiguous()
+        self.cache = torch.empty(2 * self.B * self.NH * self.maxT * HD, device=dev, dtype=torch.bfloat16)
+        chunk = 1 << 26
+        for i in range(0, self.cache.numel(), chunk):
+            n = min(chunk, self.cache.numel() - i)
+            self.cache[i:i + n] = torch.randn(n, generator=g, device=dev).to(torch.bfloat16)
+        self.qkv = torch.randn(self.B * 3 * self.NH * HD, generator=g, device=dev).to(torch.bfloat16)
+        self.out = torch.empty(self.B * self.NH * HD, device=dev, dtype=torch.bfloat16)
+        self.ws = kvattn.Workspace(self.B, self.NH, self.maxT, args.c5_S)
+        self.plan = kvattn.plan(self.B, self.NH, HD, self.maxT, kv_dtype="bf16", S=args.c5_S,
+                                strategy=args.c5_strategy)
 
-    for _ in range(5):
-        call()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(args.c5_reps):
-        call()
-    e1.record()
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1000.0 / args.c5_reps
-    lh = [int(x) for x in lens.cpu().tolist()]
-    nbytes = bytes_per_call(lh, NH, 2, 2, B)
-    gbs = nbytes / (us * 1e-6) / 1e9
-    return {"workload": "64 seqs x NH=12 x hd=64, BF16 KV, lengths U[1,8192] (seed 5)",
-            "sum_len": sum(lh), "bytes_per_call": nbytes, "us_per_call": us, "GBps": gbs,
-            "frac_of_hbm_peak": gbs / HBM_PEAK_GBS, "strategy": args.c5_strategy, "S": args.c5_S}
+    def call(self):
+        self.kvattn.decode(self.out, self.qkv, self.cache, self.B, self.NH, HD, self.maxT, kv_dtype="bf16",
+                           cur_len=self.cur, lens_per_seq=True, S=self.args.c5_S, strategy=self.args.c5_strategy,
+                           **self.ws.kwargs())
+
+    def measure(self):
+        for _ in range(5):
+            self.call()
+        us = timed(self.torch, self.call, self.args.c5_reps) * 1000.0
+        lh = [int(x) for x in self.lens.cpu().tolist()]
+        nbytes = bytes_per_call(lh, self.NH, 2, 2, self.B)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        return {"workload": "64 seqs x NH=12 x hd=64, BF16 KV, maxT=8192, lengths U[1,8192] (seed 5)",
+                "sum_len": sum(lh), "bytes_per_call": nbytes, "us_per_call": round(us, 3),
+                "GBps": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                "strategy": self.kvattn.STRATEGY_NAMES[self.plan[0]], "segments_per_head": self.plan[1],
+                "rows_per_segment": self.plan[2]}
 
 
-def cpu_baseline(seconds, torch, c2):
+def kernel_key(plan, B, NH):
+    """rocprof summary key of the split kernel a plan launches (BF16 = dtype 1)."""
+    st, slots, _ = plan
+    mode = {2: 0, 4: 0, 5: 1, 3: 2}.get(st)
+    if mode is None:
+        return None
+    return f"split_kernel<1, {mode}> grid={B * NH * slots * 256}"
+
+
+def cpu_baseline(seconds, c2):
     from oracle import oracle
-    import numpy as np
-    B, NH, maxT, T = 1, 12, 1024, 1024
-    cache = c2["caches"][0].float().cpu().numpy()
-    qkv = c2["qkvs"][0].float().cpu().numpy()
+    B, NH, maxT, T = c2.B, c2.NH, c2.maxT, c2.T
+    cache = c2.caches[0].float().cpu().numpy()
+    qkv = c2.qkvs[0].float().cpu().numpy()
     t1 = oracle.time_attention_f32(qkv, cache, T, B, NH, HD, maxT, 1)
     reps = max(3, int(seconds * 1e6 / max(t1, 1.0)))
     med = oracle.time_attention_f32(qkv, cache, T, B, NH, HD, maxT, reps)
@@ -172,10 +195,29 @@ def cpu_baseline(seconds, torch, c2):
                     break
     except OSError:
         pass
-    return {"value": med, "unit": "us/call", "cores": 1, "kind": "port",
-            "sample": f"attention_kv_cpu restated (oracle, FP32, single thread), B=1 NH=12 hd=64 T=1024 "
-                      f"(bf16 cache decoded to FP32), median of {reps} calls",
-            "host_cpu": cpu, "host_nproc": os.cpu_count(), "reps": reps}
+    return {"value": round(med, 2), "unit": "us/call", "cores": 1, "kind": "port",
+            "sample": f"attention_kv_cpu restated in C (oracle, FP32, one thread): B=1 NH=12 hd=64 T=1024, "
+                      f"bf16 cache decoded to FP32 outside the timed region, median of {reps} calls (~{seconds:.0f} s)",
+            "host_cpu": cpu, "host_nproc": os.cpu_count()}
+
+
+def pmc_pass(args, torch, kvattn, dev):
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    src.fill_(7)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    c2 = C2(args, torch, kvattn, dev)
+    for _ in range(3):
+        c2.step()
+    torch.cuda.synchronize()
+    if not args.no_c5:
+        c5 = C5(args, torch, kvattn, dev)
+        for _ in range(3):
+            c5.call()
+        torch.cuda.synchronize()
+    print("pmc pass done")
 
 
 def main():
@@ -192,13 +234,29 @@ def main():
     kvattn.lib()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.mode == "pmc":
+        pmc_pass(args, torch, kvattn, dev)
+        return
 
-    c2 = bench_c2(args, torch, kvattn, dev)
-    us_call = c2["graph_ms_step"] * 1000.0 / c2["layers"]
-    eager_us_call = c2["eager_ms_step"] * 1000.0 / c2["layers"]
-    achieved = c2["bytes_per_call"] / (us_call * 1e-6) / 1e9
-    c5 = None if args.no_c5 else bench_c5(args, torch, kvattn, dev)
-    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds, torch, c2)
+    from cuda_gpt2_inference_amd.rocprof_summary import read_traffic
+    traffic = read_traffic(TRAFFIC_MD)
+
+    c2 = C2(args, torch, kvattn, dev)
+    graph_ms, eager_ms = c2.measure()
+    rel = c2.check()
+    us_call = graph_ms * 1000.0 / c2.L
+    nbytes = bytes_per_call([c2.T], c2.NH, 2, 2, c2.B)
+    achieved = nbytes / (us_call * 1e-6) / 1e9
+    key2 = kernel_key(c2.plan, c2.B, c2.NH)
+
+    c5 = None
+    if not args.no_c5:
+        c5o = C5(args, torch, kvattn, dev)
+        c5 = c5o.measure()
+        k5 = kernel_key(c5o.plan, c5o.B, c5o.NH)
+        c5["kernel"] = k5
+        c5["traffic_bytes_split_kernel"] = traffic.get(k5)
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds, c2)
 
     line = {
         "metric": METRIC,
@@ -207,7 +265,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(c2["graph_ms_step"], 6),
+        "ms_per_step": round(graph_ms, 6),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
@@ -216,14 +274,15 @@ def main():
         "config": {"workload": "GPT-2 124M 12-layer decode-attention stack, BF16 KV cache, B=1, NH=12, hd=64, "
                                "T=1024 (cur_len=1023); one step = 12 calls replayed as a HIP graph",
                    "batch": 1, "heads": 12, "head_dim": 64, "context": 1024, "layers": 12,
-                   "kv_dtype": "bf16", "accumulate": "f32", "strategy": args.strategy, "S": args.S},
+                   "kv_dtype": "bf16", "accumulate": "f32",
+                   "strategy": kvattn.STRATEGY_NAMES[c2.plan[0]], "segments_per_head": c2.plan[1],
+                   "rows_per_segment": c2.plan[2]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None,
-                     "kernel": "split_kernel<BF16, last-block merge>",
-                     "bytes_per_launch": c2["bytes_per_call"], "us_per_launch": round(us_call, 4)},
+                     "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic.get(key2),
+                     "kernel": key2, "bytes_per_launch": nbytes, "us_per_launch": round(us_call, 4)},
         "cpu_baseline": cpu,
-        "extra": {"eager_us_per_call": round(eager_us_call, 4),
-                  "rel_err_vs_f64": c2["rel_err_vs_f64"],
+        "extra": {"eager_us_per_call": round(eager_ms * 1000.0 / c2.L, 4),
+                  "rel_err_vs_f64": rel,
                   "gpu_vs_cpu_speedup": (round(cpu["value"] / us_call, 1) if cpu else None),
                   "c5": c5, "gpu": torch.cuda.get_device_name(dev), "host": platform.node()},
     }

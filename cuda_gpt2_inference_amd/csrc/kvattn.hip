@@ -1161,18 +1161,16 @@ int auto_seg_rows(int total_hint) {
 constexpr int kFusedMaxRows = 256;        // AUTO: fused_single up to this many positions
 constexpr long long kStreamRows = 1 << 19; // AUTO: split + merge kernel from this many rows
 
-int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scale, int B, int NH, int hs,
-                int maxT, const int* d_cur_len, int lens_per_seq, int len_hint, void* workspace,
-                size_t workspace_bytes, int S, int strategy, int kv_dtype, void* stream_v) {
-    KV_TRY(check_common(qkv, kv, kv_scale, B, NH, hs, maxT, kv_dtype));
-    if (!out) return KVATTN_ERR_NULL_POINTER;
-    if (!aligned16(out)) return KVATTN_ERR_MISALIGNED;
+// Resolve AUTO and the segmentation.  S > 0: reference partition with S slots; S < 0:
+// -S rows per segment; S == 0: automatic rows per segment from the length hint.
+struct Plan {
+    int strategy, slots, seg_rows;
+};
+
+int make_plan(int B, int NH, int maxT, int len_hint, int S, int strategy, Plan& p) {
     if (strategy < KVATTN_AUTO || strategy > KVATTN_SPLIT_LASTBLOCK) return KVATTN_ERR_STRATEGY;
     if (len_hint >= maxT || len_hint < -1) return KVATTN_ERR_LENGTH;
-    KV_TRY(resolve_len(d_cur_len));
-    hipStream_t stream = (hipStream_t)stream_v;
     const int total_hint = (len_hint < 0 ? maxT - 1 : len_hint) + 1;
-
     if (strategy == KVATTN_AUTO) {
         // Short contexts: one workgroup per (b,h).  Otherwise split; a single launch with
         // the in-kernel merge while the whole call is latency bound, and split + merge
@@ -1182,19 +1180,38 @@ int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scal
         else if ((long long)B * NH * total_hint >= kStreamRows) strategy = KVATTN_SPLIT_MERGE;
         else strategy = KVATTN_SPLIT_LASTBLOCK;
     }
-    if (strategy == KVATTN_FUSED_SINGLE)
+    p.strategy = strategy;
+    if (strategy == KVATTN_FUSED_SINGLE) {
+        p.slots = 1;
+        p.seg_rows = 0;
+        return KVATTN_OK;
+    }
+    KV_TRY(segment_slots(maxT, S, p.slots, p.seg_rows));
+    if (S == 0) {
+        p.seg_rows = auto_seg_rows(total_hint);
+        p.slots = ceil_div_i(maxT, p.seg_rows);
+    }
+    if ((long long)B * NH * p.slots >= (1ll << 31)) return KVATTN_ERR_SHAPE;
+    return KVATTN_OK;
+}
+
+int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scale, int B, int NH, int hs,
+                int maxT, const int* d_cur_len, int lens_per_seq, int len_hint, void* workspace,
+                size_t workspace_bytes, int S, int strategy, int kv_dtype, void* stream_v) {
+    KV_TRY(check_common(qkv, kv, kv_scale, B, NH, hs, maxT, kv_dtype));
+    if (!out) return KVATTN_ERR_NULL_POINTER;
+    if (!aligned16(out)) return KVATTN_ERR_MISALIGNED;
+    Plan plan{};
+    KV_TRY(make_plan(B, NH, maxT, len_hint, S, strategy, plan));
+    KV_TRY(resolve_len(d_cur_len));
+    hipStream_t stream = (hipStream_t)stream_v;
+
+    if (plan.strategy == KVATTN_FUSED_SINGLE)
         return launch_fused_single(out, qkv, kv, kv_scale, B, NH, maxT, d_cur_len, lens_per_seq, kv_dtype, stream);
 
-    int slots = 0, seg_rows = 0;
-    KV_TRY(segment_slots(maxT, S, slots, seg_rows));
-    if (S == 0) {
-        seg_rows = auto_seg_rows(total_hint);
-        slots = ceil_div_i(maxT, seg_rows);
-    }
-    if ((long long)B * NH * slots >= (1ll << 31)) return KVATTN_ERR_SHAPE;
     if (!workspace) return KVATTN_ERR_WORKSPACE;
     if (!aligned16(workspace)) return KVATTN_ERR_MISALIGNED;
-    const Workspace w = carve(workspace, B, NH, slots);
+    const Workspace w = carve(workspace, B, NH, plan.slots);
     if (w.bytes > workspace_bytes) return KVATTN_ERR_WORKSPACE;
 
     SplitArgs a{};
@@ -1211,11 +1228,11 @@ int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scal
     a.B = B;
     a.NH = NH;
     a.maxT = maxT;
-    a.S = slots;
-    a.seg_rows = seg_rows;
+    a.S = plan.slots;
+    a.seg_rows = plan.seg_rows;
     a.qscale = qscale_for(hs);
 
-    switch (strategy) {
+    switch (plan.strategy) {
         case KVATTN_SPLIT_MERGE:
             KV_TRY(launch_split(a, kv_dtype, kPartialsOnly, stream));
             return launch_merge(a, kv_dtype, stream);
@@ -1387,6 +1404,20 @@ size_t kvattn_workspace_bytes(int B, int NH, int hs, int maxT, int S) {
 int kvattn_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
     if (!workspace) return KVATTN_ERR_NULL_POINTER;
     KV_HIP(hipMemsetAsync(workspace, 0, workspace_bytes, (hipStream_t)stream));
+    return KVATTN_OK;
+}
+
+int kvattn_plan(int B, int NH, int hs, int maxT, int len_hint, int S, int strategy, int kv_dtype,
+                int* strategy_out, int* segments_out, int* seg_rows_out) {
+    if (hs != kHeadDim) return KVATTN_ERR_HEAD_DIM;
+    if (B < 1 || NH < 1 || maxT < 1 || maxT > kMaxT || (long long)B * NH > (1ll << 24)) return KVATTN_ERR_SHAPE;
+    if (kv_dtype < KVATTN_KV_F32 || kv_dtype > KVATTN_KV_FP8_E4M3) return KVATTN_ERR_DTYPE;
+    if (!strategy_out || !segments_out || !seg_rows_out) return KVATTN_ERR_NULL_POINTER;
+    Plan p{};
+    KV_TRY(make_plan(B, NH, maxT, len_hint, S, strategy, p));
+    *strategy_out = p.strategy;
+    *segments_out = p.slots;
+    *seg_rows_out = p.seg_rows;
     return KVATTN_OK;
 }
 

@@ -81,6 +81,8 @@ SIGNATURES = {
     "kvattn_merge": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "kvattn_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
     "kvattn_workspace_init": (_i, [_vp, _sz, _vp]),
+    "kvattn_plan": (_i, [_i, _i, _i, _i, _i, _i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i),
+                         ctypes.POINTER(_i)]),
     "kvattn_decode": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp, _sz, _i, _i, _i, _vp]),
 }
 
@@ -210,6 +212,18 @@ def workspace_bytes(B, NH, hs, maxT, S=0) -> int:
 
 def workspace_init(workspace, nbytes, stream=None) -> None:
     _check(lib().kvattn_workspace_init(_ptr(workspace), nbytes, _stream(stream)), "kvattn_workspace_init")
+
+
+def plan(B, NH, hs, maxT, *, kv_dtype, len_hint=-1, S=0, strategy="auto"):
+    """(strategy code, segment slots per (b,h), rows per segment) kvattn_decode would use."""
+    st, seg, rows = _i(), _i(), _i()
+    _check(lib().kvattn_plan(B, NH, hs, maxT, int(len_hint), int(S), strategy_code(strategy),
+                             kv_dtype_code(kv_dtype), ctypes.byref(st), ctypes.byref(seg), ctypes.byref(rows)),
+           "kvattn_plan")
+    return st.value, seg.value, rows.value
+
+
+STRATEGY_NAMES = {v: k for k, v in STRATEGIES.items()}
 
 
 def decode(out, qkv, kv_cache, B, NH, hs, maxT, *, kv_dtype, kv_scale=None, cur_len=None,

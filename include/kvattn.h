@@ -146,6 +146,15 @@ size_t kvattn_workspace_bytes(int B, int NH, int hs, int maxT, int S);
  * counters at zero after every call. */
 int kvattn_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
 
+/* The launch plan kvattn_decode would use for these arguments, without launching:
+ * *strategy_out = the resolved kvattn_strategy (AUTO resolved), *segments_out = segment
+ * slots per (b,h) (1 for FUSED_SINGLE), *seg_rows_out = rows per segment (0 when the
+ * reference partition ceil(total/S) is used).  No reference counterpart: it exposes the
+ * AUTO choice, which the reference makes inline in its caller (inference_gpt2_opt.cu:247,
+ * 304,331: fused_single below a length threshold, split + merge above it). */
+int kvattn_plan(int B, int NH, int hs, int maxT, int len_hint, int S, int strategy, int kv_dtype,
+                int* strategy_out, int* segments_out, int* seg_rows_out);
+
 /* One decode-attention call with an explicit strategy, the unified entry the per-layer
  * attention block of forward_kv_graph_ready (inference_gpt2_opt.cu:298-347) maps onto.
  *   strategy   kvattn_strategy; AUTO picks from len_hint (the host's view of cur_len,
