@@ -58,6 +58,7 @@ def parse():
     p.add_argument("--no-c5", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--no-configs", action="store_true", help="skip the other GPT-2-shaped configurations")
     return p.parse_args()
 
 
@@ -169,6 +170,78 @@ class C5:
                 "rows_per_segment": self.plan[2]}
 
 
+def small_config(torch, kvattn, dev, dtype, NH, maxT, T, strategy, S, reps=200):
+    """One (B=1) decode-attention call on a warm cache: microseconds per call, measured over
+    `reps` back-to-back calls replayed from a HIP graph (eager for the cooperative launch,
+    which cannot be captured)."""
+    B = 1
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    n = 2 * B * NH * maxT * HD
+    scale = None
+    if dtype == "f32":
+        cache = torch.randn(n, generator=g, device=dev)
+        qkv = torch.randn(B * 3 * NH * HD, generator=g, device=dev)
+        out = torch.empty(B * NH * HD, device=dev)
+    else:
+        qkv = torch.randn(B * 3 * NH * HD, generator=g, device=dev).to(torch.bfloat16)
+        out = torch.empty(B * NH * HD, device=dev, dtype=torch.bfloat16)
+        if dtype == "bf16":
+            cache = torch.randn(n, generator=g, device=dev).to(torch.bfloat16)
+        else:
+            codes = torch.randint(0, 256, (n,), generator=g, device=dev, dtype=torch.int32)
+            if dtype == "fp8":
+                codes = codes & 0x77          # finite E4M3 codes only (no NaN patterns)
+            cache = codes.to(torch.uint8)
+            scale = torch.rand(2 * B * NH * maxT, generator=g, device=dev) * 0.01 + 1e-3
+    cur = torch.tensor([T - 1], dtype=torch.int32, device=dev)
+    ws = kvattn.Workspace(B, NH, maxT, S)
+    plan = kvattn.plan(B, NH, HD, maxT, kv_dtype=dtype, len_hint=T - 1, S=S, strategy=strategy)
+
+    def call():
+        kvattn.decode(out, qkv, cache, B, NH, HD, maxT, kv_dtype=dtype, kv_scale=scale, cur_len=cur,
+                      len_hint=T - 1, S=S, strategy=strategy, **ws.kwargs())
+
+    for _ in range(10):
+        call()
+    eager_us = timed(torch, call, reps) * 1000.0
+    graph_us = None
+    if strategy != "coop":
+        s = torch.cuda.Stream()
+        graph = torch.cuda.CUDAGraph()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(graph, stream=s):
+                for _ in range(10):
+                    call()
+        graph.replay()
+        graph_us = timed(torch, graph.replay, max(1, reps // 10)) * 100.0
+    kv_bytes = {"f32": 4, "bf16": 2, "int8": 1, "fp8": 1}[dtype]
+    act = 4 if dtype == "f32" else 2
+    nbytes = bytes_per_call([T], NH, kv_bytes, act, B) + (2 * NH * T * 4 if scale is not None else 0)
+    us = graph_us if graph_us is not None else eager_us
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"dtype": dtype, "B": B, "NH": NH, "T": T, "maxT": maxT,
+            "strategy": kvattn.STRATEGY_NAMES[plan[0]], "segments_per_head": plan[1], "rows_per_segment": plan[2],
+            "bytes_per_call": nbytes, "us_per_call_graph": None if graph_us is None else round(graph_us, 3),
+            "us_per_call_eager": round(eager_us, 3), "GBps": round(gbs, 1),
+            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def other_configs(torch, kvattn, dev):
+    """The remaining GPT-2-shaped configurations, single layer, warm cache."""
+    return {
+        "c1_f32_fused_single_T256": small_config(torch, kvattn, dev, "f32", 12, 256, 256, "fused_single", 0),
+        "c3_int8_T1024_split_merge_S8": small_config(torch, kvattn, dev, "int8", 12, 1024, 1024, "split_merge", 8),
+        "c3_int8_T1024_lastblock_S8": small_config(torch, kvattn, dev, "int8", 12, 1024, 1024, "lastblock", 8),
+        "c4_fp8_T512_coop_S8": small_config(torch, kvattn, dev, "fp8", 12, 1024, 512, "coop", 8, reps=50),
+        "c4_fp8_T512_graph_S8": small_config(torch, kvattn, dev, "fp8", 12, 1024, 512, "graph", 8),
+        "c4_fp8_T1024_coop_S8": small_config(torch, kvattn, dev, "fp8", 12, 1024, 1024, "coop", 8, reps=50),
+        "c4_fp8_T1024_graph_S8": small_config(torch, kvattn, dev, "fp8", 12, 1024, 1024, "graph", 8),
+        "c4_fp8_T1024_lastblock_S8": small_config(torch, kvattn, dev, "fp8", 12, 1024, 1024, "lastblock", 8),
+    }
+
+
 def kernel_key(plan, B, NH):
     """rocprof summary key of the split kernel a plan launches (BF16 = dtype 1)."""
     st, slots, _ = plan
@@ -256,6 +329,7 @@ def main():
         k5 = kernel_key(c5o.plan, c5o.B, c5o.NH)
         c5["kernel"] = k5
         c5["traffic_bytes_split_kernel"] = traffic.get(k5)
+    configs = None if args.no_configs else other_configs(torch, kvattn, dev)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds, c2)
 
     line = {
@@ -284,7 +358,8 @@ def main():
         "extra": {"eager_us_per_call": round(eager_ms * 1000.0 / c2.L, 4),
                   "rel_err_vs_f64": rel,
                   "gpu_vs_cpu_speedup": (round(cpu["value"] / us_call, 1) if cpu else None),
-                  "c5": c5, "gpu": torch.cuda.get_device_name(dev), "host": platform.node()},
+                  "c5": c5, "configs": configs, "gpu": torch.cuda.get_device_name(dev),
+                  "host": platform.node()},
     }
     print(json.dumps(line))
 
