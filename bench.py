@@ -243,12 +243,22 @@ def other_configs(torch, kvattn, dev):
 
 
 def kernel_key(plan, B, NH):
-    """rocprof summary key of the split kernel a plan launches (BF16 = dtype 1)."""
+    """(name prefix, grid suffix) of the split kernel a plan launches (BF16 = dtype 1), as
+    keyed in the rocprof summaries: `split_kernel<1, MODE, WAVES, TILE> grid=WORKITEMS`."""
     st, slots, _ = plan
     mode = {2: 0, 4: 0, 5: 1, 3: 2}.get(st)
     if mode is None:
         return None
-    return f"split_kernel<1, {mode}> grid={B * NH * slots * 256}"
+    return f"split_kernel<1, {mode},", f"grid={B * NH * slots * 256}"
+
+
+def lookup(traffic, key):
+    if key is None:
+        return None, None
+    for k, v in traffic.items():
+        if k.startswith(key[0]) and k.endswith(key[1]):
+            return k, v
+    return f"{key[0]} ...> {key[1]}", None
 
 
 def cpu_baseline(seconds, c2):
@@ -320,15 +330,15 @@ def main():
     us_call = graph_ms * 1000.0 / c2.L
     nbytes = bytes_per_call([c2.T], c2.NH, 2, 2, c2.B)
     achieved = nbytes / (us_call * 1e-6) / 1e9
-    key2 = kernel_key(c2.plan, c2.B, c2.NH)
+    key2, traffic2 = lookup(traffic, kernel_key(c2.plan, c2.B, c2.NH))
 
     c5 = None
     if not args.no_c5:
         c5o = C5(args, torch, kvattn, dev)
         c5 = c5o.measure()
-        k5 = kernel_key(c5o.plan, c5o.B, c5o.NH)
+        k5, t5 = lookup(traffic, kernel_key(c5o.plan, c5o.B, c5o.NH))
         c5["kernel"] = k5
-        c5["traffic_bytes_split_kernel"] = traffic.get(k5)
+        c5["traffic_bytes_split_kernel"] = t5
     configs = None if args.no_configs else other_configs(torch, kvattn, dev)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds, c2)
 
@@ -352,7 +362,7 @@ def main():
                    "strategy": kvattn.STRATEGY_NAMES[c2.plan[0]], "segments_per_head": c2.plan[1],
                    "rows_per_segment": c2.plan[2]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic.get(key2),
+                     "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic2,
                      "kernel": key2, "bytes_per_launch": nbytes, "us_per_launch": round(us_call, 4)},
         "cpu_baseline": cpu,
         "extra": {"eager_us_per_call": round(eager_ms * 1000.0 / c2.L, 4),

@@ -49,10 +49,6 @@ constexpr int kMinSegRows = 64;         // smallest automatic segment length
 constexpr int kMaxSegments = 1 << 16;   // upper bound on segments per (b,h)
 constexpr int kMaxT = 1 << 23;          // keeps per-slot byte offsets inside 32 bits
 constexpr size_t kFusedMaxLds = 64 * 1024;  // dynamic LDS of fused_single (scores)
-#ifndef KVATTN_FUSED_THREADS
-#define KVATTN_FUSED_THREADS 1024
-#endif
-constexpr int kFusedThreads = KVATTN_FUSED_THREADS;  // fused_single workgroup size
 
 // ------------------------------------------------------------------------------------
 // Per-dtype row geometry.
@@ -83,6 +79,16 @@ template <int DT> constexpr int kRowsPerLoad = kWave / Row<DT>::kLanes;
 #define KVATTN_UNROLL_BYTE 4
 #endif
 template <int DT> constexpr int kUnroll = Row<DT>::k8bit ? KVATTN_UNROLL_BYTE : KVATTN_UNROLL_WIDE;
+// Latency-bound calls use 16-wave workgroups with 16 rows per wave per tile, so that each
+// wave's dependent chain (dot, row reduction, exp, weighted sum) is short.
+#ifndef KVATTN_LAT_WAVES
+#define KVATTN_LAT_WAVES 4
+#endif
+#ifndef KVATTN_LAT_ROWS
+#define KVATTN_LAT_ROWS 64
+#endif
+template <int DT> constexpr int kUnrollLat = KVATTN_LAT_ROWS / kRowsPerLoad<DT> > 0 ? KVATTN_LAT_ROWS / kRowsPerLoad<DT> : 1;
+constexpr int kWavesLat = KVATTN_LAT_WAVES;
 
 // ------------------------------------------------------------------------------------
 // Element helpers.
@@ -380,32 +386,22 @@ __device__ __forceinline__ void consume_tile(const Tile<DT, U>& t, int r, int r1
     m = mt;
 }
 
-// Where this lane's q slice lives; the load is issued after the first tile's K/V loads so
-// that nothing depending on q can be scheduled ahead of them.
-struct QSrc {
-    const void* qkv;
-    int b, h, NH, slice;
-};
-
-template <int DT>
-__device__ __forceinline__ void online_rows(const Slot& sl, int r0, int r1, int slot_row, const QSrc& qs,
-                                            float qscale, float& m, float& l, float (&acc)[Row<DT>::kElems]) {
-    constexpr int kU = kUnroll<DT>;
+// Online softmax over rows [r0, r1) of a slot by one wave, given the first tile (rows
+// [r0, r0 + kTile) clipped to a bound >= r1) and this lane's q slice already requested;
+// rows of that tile at or beyond r1 are masked.  The q slice is requested after the tile's
+// K/V loads, so nothing that depends on q is scheduled ahead of them.
+template <int DT, int kU>
+__device__ __forceinline__ void online_rows_from(const Tile<DT, kU>& t0, const QRaw<DT>& qr,
+                                                 const Slot& sl, int r0, int r1, int slot_row, float qscale,
+                                                 float& m, float& l, float (&acc)[Row<DT>::kElems]) {
     constexpr int kTile = kRowsPerLoad<DT> * kU;
     if (r0 >= r1) return;
-    Tile<DT, kU> t;
     float q[Row<DT>::kElems];
-    int r = r0;
-    if (r + kTile > r1) {
-        load_tile<DT, kU, true>(t, sl, r, r1, slot_row);
-        convert_q<DT>(load_q<DT>(qs.qkv, qs.b, qs.h, qs.NH, qs.slice), qscale, q);
-        consume_tile<DT, kU, true>(t, r, r1, slot_row, q, m, l, acc);
-        return;
-    }
-    load_tile<DT, kU, false>(t, sl, r, r1, slot_row);
-    convert_q<DT>(load_q<DT>(qs.qkv, qs.b, qs.h, qs.NH, qs.slice), qscale, q);
-    consume_tile<DT, kU, false>(t, r, r1, slot_row, q, m, l, acc);
-    for (r += kTile; r + kTile <= r1; r += kTile) {
+    convert_q<DT>(qr, qscale, q);
+    consume_tile<DT, kU, true>(t0, r0, r1, slot_row, q, m, l, acc);
+    Tile<DT, kU> t;
+    int r = r0 + kTile;
+    for (; r + kTile <= r1; r += kTile) {
         load_tile<DT, kU, false>(t, sl, r, r1, slot_row);
         consume_tile<DT, kU, false>(t, r, r1, slot_row, q, m, l, acc);
     }
@@ -482,14 +478,13 @@ __device__ __forceinline__ void weight_tile(const Slot& sl, int r, int total, in
     }
 }
 
-template <int DT, int kThreads>
+template <int DT, int kThreads, int kU>
 __global__ __launch_bounds__(kThreads) void fused_single_kernel(
     void* __restrict__ out, const void* __restrict__ qkv, const uint8_t* __restrict__ kv,
     const float* __restrict__ kv_scale, const int* __restrict__ cur_len, int lens_per_seq,
-    int B, int NH, int maxT, float qscale) {
+    int B, int NH, int maxT, int spec_rows, float qscale) {
     using R = Row<DT>;
     constexpr int kW = kThreads / kWave;
-    constexpr int kU = kUnroll<DT>;
     constexpr int kRPL = kRowsPerLoad<DT>;
     constexpr int kTile = kRPL * kU;
     extern __shared__ float s_scores[];
@@ -501,9 +496,18 @@ __global__ __launch_bounds__(kThreads) void fused_single_kernel(
     const int b = bh / NH, h = bh - b * NH;
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int slot_row = lane / R::kLanes, slice = lane % R::kLanes;
-    const int total = seq_total(cur_len, lens_per_seq, b, maxT);
-
     const Slot sl = make_slot<DT>(kv, kv_scale, B, NH, maxT, bh, slice);
+    // When the host's length hint fits the one-tile-per-wave shape, the tile and q are
+    // requested before the device length is read (rows at or beyond it are masked later).
+    const int spec_lim = min(spec_rows, maxT);
+    const bool spec = spec_lim > 0 && spec_lim <= kW * kTile;
+    Tile<DT, kU> t;
+    QRaw<DT> qr;
+    if (spec) {
+        load_tile<DT, kU, true>(t, sl, wave * kTile, spec_lim, slot_row);
+        qr = load_q<DT>(qkv, b, h, NH, slice);
+    }
+    const int total = seq_total(cur_len, lens_per_seq, b, maxT);
     float q[R::kElems];
 
     float l = 0.0f, acc[R::kElems];
@@ -514,9 +518,11 @@ __global__ __launch_bounds__(kThreads) void fused_single_kernel(
         // Every wave owns at most one tile: its K and V rows are requested together, the
         // scores stay in registers and only the workgroup maximum passes through LDS.
         const int r = wave * kTile;
-        Tile<DT, kU> t;
-        load_tile<DT, kU, true>(t, sl, r, total, slot_row);
-        convert_q<DT>(load_q<DT>(qkv, b, h, NH, slice), qscale, q);
+        if (!spec || total > spec_lim) {
+            load_tile<DT, kU, true>(t, sl, r, total, slot_row);
+            qr = load_q<DT>(qkv, b, h, NH, slice);
+        }
+        convert_q<DT>(qr, qscale, q);
         float s[kU];
         float mloc = kStartMax;
 #pragma unroll
@@ -602,6 +608,7 @@ struct SplitArgs {
     int B, NH, maxT;
     int S;          // segment slots per (b,h): the grid stride and the partial stride
     int seg_rows;   // > 0: fixed rows per segment; 0: reference partition ceil(total/S)
+    int spec_rows;  // the host's view of the attended length (0: unknown); see split_kernel
     float qscale;   // scale * log2(e)
 };
 
@@ -720,15 +727,47 @@ __device__ __forceinline__ void merge_partials(void* out, const float* part_out,
     store_out<DT>(out, (size_t)bh * kHeadDim + c, O / L);
 }
 
-template <int DT, int kMode>
-__global__ __launch_bounds__(kBlock) void split_kernel(SplitArgs a) {
+// Workgroups of the streaming shape a CU should hold at once (bounds the register budget).
+#ifndef KVATTN_STREAM_MIN_BLOCKS
+#define KVATTN_STREAM_MIN_BLOCKS 1
+#endif
+
+template <int DT, int kMode, int kW, int kU>
+__global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS : 1) void split_kernel(SplitArgs a) {
     using R = Row<DT>;
-    __shared__ float s_m[kWaves];
-    __shared__ float s_l[kWaves];
-    __shared__ float s_acc[kWaves][kHeadDim];
+    __shared__ float s_m[kW];
+    __shared__ float s_l[kW];
+    __shared__ float s_acc[kW][kHeadDim];
 
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int slot_row = lane / R::kLanes, slice = lane % R::kLanes;
+
+    // Uniform lengths with fixed-size segments: (b, h, s) and the segment's nominal rows
+    // [j0, min(j0 + seg_rows, maxT)) follow from blockIdx alone, and the nominal range
+    // always contains the true one [j0, min(j0 + seg_rows, total)).  When the host's length
+    // hint says the segment is in use, each wave requests its first tile of the nominal
+    // range, and its q slice, before reading the device length, so the three memory
+    // round trips overlap; rows beyond the true length are masked afterwards.  Otherwise
+    // the same first tile is requested once the length is known.
+    Tile<DT, kU> t0;
+    QRaw<DT> q0;
+    bool spec = false;
+    int w0 = 0, w1 = 0;
+    if (!a.lens_per_seq && a.seg_rows > 0) {
+        const int bh0 = blockIdx.x / a.S;
+        const int j0 = (blockIdx.x - bh0 * a.S) * a.seg_rows;
+        const int nend = min(j0 + a.seg_rows, a.maxT);
+        if (j0 < a.spec_rows && j0 < nend) {
+            const int per = ceil_div_i(nend - j0, kW);
+            w0 = min(j0 + wave * per, nend);
+            w1 = min(w0 + per, nend);
+            const int b0 = bh0 / a.NH;
+            const Slot sl0 = make_slot<DT>(a.kv, a.kv_scale, a.B, a.NH, a.maxT, bh0, slice);
+            load_tile<DT, kU, true>(t0, sl0, w0, w1, slot_row);
+            q0 = load_q<DT>(a.qkv, b0, bh0 - b0 * a.NH, a.NH, slice);
+            spec = true;
+        }
+    }
 
     Item it;
     const bool active = locate(a, blockIdx.x, it);
@@ -756,15 +795,20 @@ __global__ __launch_bounds__(kBlock) void split_kernel(SplitArgs a) {
                 if (lane == 0) { put<kCoh>(a.part_max + pidx, kEmptyMax); put<kCoh>(a.part_lse + pidx, 0.0f); }
             }
         } else {
-            const QSrc qs{a.qkv, it.b, it.h, a.NH, slice};
             const Slot sl = make_slot<DT>(a.kv, a.kv_scale, a.B, a.NH, a.maxT, bh, slice);
-            const int per_wave = ceil_div_i(j1 - j0, kWaves);
-            const int w0 = min(j0 + wave * per_wave, j1);
-            const int w1 = min(w0 + per_wave, j1);
+            if (spec) {
+                w1 = min(w1, j1);
+            } else {
+                const int per_wave = ceil_div_i(j1 - j0, kW);
+                w0 = min(j0 + wave * per_wave, j1);
+                w1 = min(w0 + per_wave, j1);
+                load_tile<DT, kU, true>(t0, sl, w0, w1, slot_row);
+                q0 = load_q<DT>(a.qkv, it.b, it.h, a.NH, slice);
+            }
             float m = kStartMax, l = 0.0f, acc[R::kElems];
 #pragma unroll
             for (int e = 0; e < R::kElems; ++e) acc[e] = 0.0f;
-            online_rows<DT>(sl, w0, w1, slot_row, qs, a.qscale, m, l, acc);
+            online_rows_from<DT, kU>(t0, q0, sl, w0, w1, slot_row, a.qscale, m, l, acc);
 
             // Combine the row slots of this wave, then the 4 waves.
             const float mw = slot_reduce<R::kLanes, true>(m);
@@ -781,10 +825,10 @@ __global__ __launch_bounds__(kBlock) void split_kernel(SplitArgs a) {
             if (wave == 0) {
                 float Mb = s_m[0];
 #pragma unroll
-                for (int w = 1; w < kWaves; ++w) Mb = fmaxf(Mb, s_m[w]);
+                for (int w = 1; w < kW; ++w) Mb = fmaxf(Mb, s_m[w]);
                 float L = 0.0f, A = 0.0f;
 #pragma unroll
-                for (int w = 0; w < kWaves; ++w) {
+                for (int w = 0; w < kW; ++w) {
                     const float g = exp2_fast(s_m[w] - Mb);
                     L = fmaf(g, s_l[w], L);
                     A = fmaf(g, s_acc[w][lane], A);
@@ -958,39 +1002,56 @@ int dispatch_dtype(int dt, F&& f) {
 }
 
 int launch_fused_single(void* out, const void* qkv, const void* kv, const float* kv_scale, int B, int NH,
-                        int maxT, const int* cur_len, int lens_per_seq, int kv_dtype, hipStream_t stream) {
+                        int maxT, const int* cur_len, int lens_per_seq, int spec_rows, int kv_dtype,
+                        hipStream_t stream) {
     const size_t lds = (size_t)maxT * sizeof(float);
     if (lds > kFusedMaxLds) return KVATTN_ERR_LDS;
     const float qs = qscale_for(kHeadDim);
     return dispatch_dtype(kv_dtype, [&](auto dtc) -> int {
         constexpr int DT = decltype(dtc)::value;
-        hipLaunchKernelGGL((fused_single_kernel<DT, kFusedThreads>), dim3(B * NH), dim3(kFusedThreads), lds, stream, out, qkv,
-                           (const uint8_t*)kv, kv_scale, cur_len, lens_per_seq, B, NH, maxT, qs);
+        constexpr int kThreads = kWavesLat * kWave;
+        hipLaunchKernelGGL((fused_single_kernel<DT, kThreads, kUnrollLat<DT>>), dim3(B * NH), dim3(kThreads), lds,
+                           stream, out, qkv,
+                           (const uint8_t*)kv, kv_scale, cur_len, lens_per_seq, B, NH, maxT, spec_rows, qs);
         KV_HIP(hipGetLastError());
         return KVATTN_OK;
     });
 }
 
+// Split kernel instance for a mode and a shape: 16-wave workgroups with short tiles for
+// latency-bound calls (`lat`), 4-wave workgroups with deep tiles for streaming calls.
 template <int DT>
-void* split_fn(int mode) {
-    switch (mode) {
-        case kPartialsOnly: return (void*)&split_kernel<DT, kPartialsOnly>;
-        case kLastBlockMerge: return (void*)&split_kernel<DT, kLastBlockMerge>;
-        default: return (void*)&split_kernel<DT, kCoopMerge>;
+const void* split_ptr(int mode, bool lat) {
+    if (lat) {
+        constexpr int W = kWavesLat, U = kUnrollLat<DT>;
+        if (mode == kPartialsOnly) return (const void*)&split_kernel<DT, kPartialsOnly, W, U>;
+        if (mode == kLastBlockMerge) return (const void*)&split_kernel<DT, kLastBlockMerge, W, U>;
+        return (const void*)&split_kernel<DT, kCoopMerge, W, U>;
     }
+    constexpr int W = kWaves, U = kUnroll<DT>;
+    if (mode == kPartialsOnly) return (const void*)&split_kernel<DT, kPartialsOnly, W, U>;
+    if (mode == kLastBlockMerge) return (const void*)&split_kernel<DT, kLastBlockMerge, W, U>;
+    return (const void*)&split_kernel<DT, kCoopMerge, W, U>;
 }
 
-int launch_split(const SplitArgs& a, int kv_dtype, int mode, hipStream_t stream) {
-    const dim3 grid((unsigned)a.B * a.NH * a.S), block(kBlock);
-    return dispatch_dtype(kv_dtype, [&](auto dtc) -> int {
-        constexpr int DT = decltype(dtc)::value;
-        if (mode == kPartialsOnly)
-            hipLaunchKernelGGL((split_kernel<DT, kPartialsOnly>), grid, block, 0, stream, a);
-        else
-            hipLaunchKernelGGL((split_kernel<DT, kLastBlockMerge>), grid, block, 0, stream, a);
-        KV_HIP(hipGetLastError());
+int split_threads(bool lat) { return (lat ? kWavesLat : kWaves) * kWave; }
+
+const void* split_ptr_dt(int kv_dtype, int mode, bool lat) {
+    const void* fn = nullptr;
+    dispatch_dtype(kv_dtype, [&](auto dtc) -> int {
+        fn = split_ptr<decltype(dtc)::value>(mode, lat);
         return KVATTN_OK;
     });
+    return fn;
+}
+
+int launch_split(const SplitArgs& a, int kv_dtype, int mode, bool lat, hipStream_t stream) {
+    const void* fn = split_ptr_dt(kv_dtype, mode, lat);
+    if (!fn) return KVATTN_ERR_DTYPE;
+    SplitArgs args = a;
+    void* params[] = {&args};
+    KV_HIP(hipLaunchKernel(fn, dim3((unsigned)a.B * a.NH * a.S), dim3(split_threads(lat)), params, 0, stream));
+    return KVATTN_OK;
 }
 
 int launch_merge(const SplitArgs& a, int kv_dtype, hipStream_t stream) {
@@ -1009,7 +1070,7 @@ int stream_capturing(hipStream_t stream, bool& capturing) {
     return KVATTN_OK;
 }
 
-int launch_coop(const SplitArgs& a, int kv_dtype, hipStream_t stream) {
+int launch_coop(const SplitArgs& a, int kv_dtype, bool lat, hipStream_t stream) {
     bool capturing = false;
     KV_TRY(stream_capturing(stream, capturing));
     if (capturing) return KVATTN_ERR_CAPTURE;
@@ -1019,42 +1080,48 @@ int launch_coop(const SplitArgs& a, int kv_dtype, hipStream_t stream) {
     KV_HIP(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev));
     if (!coop) return KVATTN_ERR_COOP_TOO_LARGE;
     const long long blocks = (long long)a.B * a.NH * a.S;
-    return dispatch_dtype(kv_dtype, [&](auto dtc) -> int {
-        constexpr int DT = decltype(dtc)::value;
-        const void* fn = (const void*)&split_kernel<DT, kCoopMerge>;
+    // Every workgroup must be resident at once: take the latency shape if the grid fits
+    // with it, else the 4-wave shape, else refuse.
+    for (int attempt = 0; attempt < 2; ++attempt) {
+        const bool use_lat = lat && attempt == 0;
+        if (attempt == 1 && !lat) break;
+        const void* fn = split_ptr_dt(kv_dtype, kCoopMerge, use_lat);
+        if (!fn) return KVATTN_ERR_DTYPE;
+        const int threads = split_threads(use_lat);
         int per_cu = 0;
-        KV_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kBlock, 0));
-        if (blocks > (long long)per_cu * cus) return KVATTN_ERR_COOP_TOO_LARGE;
+        KV_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, 0));
+        if (blocks > (long long)per_cu * cus) continue;
         SplitArgs args = a;
         void* params[] = {&args};
-        KV_HIP(hipLaunchCooperativeKernel(fn, dim3((unsigned)blocks), dim3(kBlock), params, 0, stream));
+        KV_HIP(hipLaunchCooperativeKernel(fn, dim3((unsigned)blocks), dim3(threads), params, 0, stream));
         return KVATTN_OK;
-    });
+    }
+    return KVATTN_ERR_COOP_TOO_LARGE;
 }
 
 // hipGraph holding the split and merge kernel nodes, built once per argument set.
 struct GraphKey {
-    int dev, dt;
+    int dev, dt, lat;
     const void *out, *qkv, *kv, *ks, *len, *po, *pl, *pm;
     int lens_per_seq, B, NH, maxT, S, seg_rows;
     bool operator<(const GraphKey& o) const {
-        return std::tie(dev, dt, out, qkv, kv, ks, len, po, pl, pm, lens_per_seq, B, NH, maxT, S, seg_rows) <
-               std::tie(o.dev, o.dt, o.out, o.qkv, o.kv, o.ks, o.len, o.po, o.pl, o.pm, o.lens_per_seq, o.B, o.NH,
-                        o.maxT, o.S, o.seg_rows);
+        return std::tie(dev, dt, lat, out, qkv, kv, ks, len, po, pl, pm, lens_per_seq, B, NH, maxT, S, seg_rows) <
+               std::tie(o.dev, o.dt, o.lat, o.out, o.qkv, o.kv, o.ks, o.len, o.po, o.pl, o.pm, o.lens_per_seq, o.B,
+                        o.NH, o.maxT, o.S, o.seg_rows);
     }
 };
 
-int launch_graph_pair(const SplitArgs& a, int kv_dtype, hipStream_t stream) {
+int launch_graph_pair(const SplitArgs& a, int kv_dtype, bool lat, hipStream_t stream) {
     bool capturing = false;
     KV_TRY(stream_capturing(stream, capturing));
     if (capturing) {
         // Inside a caller's capture the two kernels become nodes of the caller's graph.
-        KV_TRY(launch_split(a, kv_dtype, kPartialsOnly, stream));
+        KV_TRY(launch_split(a, kv_dtype, kPartialsOnly, lat, stream));
         return launch_merge(a, kv_dtype, stream);
     }
     int dev = 0;
     KV_HIP(hipGetDevice(&dev));
-    GraphKey key{dev, kv_dtype, a.out, a.qkv, a.kv, a.kv_scale, a.cur_len, a.part_out, a.part_lse, a.part_max,
+    GraphKey key{dev, kv_dtype, lat ? 1 : 0, a.out, a.qkv, a.kv, a.kv_scale, a.cur_len, a.part_out, a.part_lse, a.part_max,
                  a.lens_per_seq, a.B, a.NH, a.maxT, a.S, a.seg_rows};
     static std::mutex mu;
     static std::map<GraphKey, hipGraphExec_t> cache;
@@ -1065,12 +1132,10 @@ int launch_graph_pair(const SplitArgs& a, int kv_dtype, hipStream_t stream) {
             for (auto& kvp : cache) (void)hipGraphExecDestroy(kvp.second);
             cache.clear();
         }
-        void* fsplit = nullptr;
+        void* fsplit = const_cast<void*>(split_ptr_dt(kv_dtype, kPartialsOnly, lat));
         void* fmerge = nullptr;
         dispatch_dtype(kv_dtype, [&](auto dtc) -> int {
-            constexpr int DT = decltype(dtc)::value;
-            fsplit = (void*)&split_kernel<DT, kPartialsOnly>;
-            fmerge = (void*)&merge_kernel<DT>;
+            fmerge = (void*)&merge_kernel<decltype(dtc)::value>;
             return KVATTN_OK;
         });
         SplitArgs args = a;
@@ -1080,7 +1145,7 @@ int launch_graph_pair(const SplitArgs& a, int kv_dtype, hipStream_t stream) {
         hipKernelNodeParams ps{};
         ps.func = fsplit;
         ps.gridDim = dim3((unsigned)a.B * a.NH * a.S);
-        ps.blockDim = dim3(kBlock);
+        ps.blockDim = dim3(split_threads(lat));
         ps.sharedMemBytes = 0;
         ps.kernelParams = params;
         ps.extra = nullptr;
@@ -1165,7 +1230,11 @@ constexpr long long kStreamRows = 1 << 19; // AUTO: split + merge kernel from th
 // -S rows per segment; S == 0: automatic rows per segment from the length hint.
 struct Plan {
     int strategy, slots, seg_rows;
+    bool lat;   // latency-bound call: 16-wave workgroups with short tiles
 };
+
+// A call is latency bound while it streams fewer rows than kStreamRows.
+bool latency_bound(int B, int NH, int total_rows) { return (long long)B * NH * total_rows < kStreamRows; }
 
 int make_plan(int B, int NH, int maxT, int len_hint, int S, int strategy, Plan& p) {
     if (strategy < KVATTN_AUTO || strategy > KVATTN_SPLIT_LASTBLOCK) return KVATTN_ERR_STRATEGY;
@@ -1181,6 +1250,7 @@ int make_plan(int B, int NH, int maxT, int len_hint, int S, int strategy, Plan& 
         else strategy = KVATTN_SPLIT_LASTBLOCK;
     }
     p.strategy = strategy;
+    p.lat = latency_bound(B, NH, total_hint);
     if (strategy == KVATTN_FUSED_SINGLE) {
         p.slots = 1;
         p.seg_rows = 0;
@@ -1207,7 +1277,8 @@ int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scal
     hipStream_t stream = (hipStream_t)stream_v;
 
     if (plan.strategy == KVATTN_FUSED_SINGLE)
-        return launch_fused_single(out, qkv, kv, kv_scale, B, NH, maxT, d_cur_len, lens_per_seq, kv_dtype, stream);
+        return launch_fused_single(out, qkv, kv, kv_scale, B, NH, maxT, d_cur_len, lens_per_seq,
+                                   (lens_per_seq || len_hint < 0) ? 0 : len_hint + 1, kv_dtype, stream);
 
     if (!workspace) return KVATTN_ERR_WORKSPACE;
     if (!aligned16(workspace)) return KVATTN_ERR_MISALIGNED;
@@ -1230,15 +1301,16 @@ int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scal
     a.maxT = maxT;
     a.S = plan.slots;
     a.seg_rows = plan.seg_rows;
+    a.spec_rows = len_hint >= 0 ? len_hint + 1 : 0;
     a.qscale = qscale_for(hs);
 
     switch (plan.strategy) {
         case KVATTN_SPLIT_MERGE:
-            KV_TRY(launch_split(a, kv_dtype, kPartialsOnly, stream));
+            KV_TRY(launch_split(a, kv_dtype, kPartialsOnly, plan.lat, stream));
             return launch_merge(a, kv_dtype, stream);
-        case KVATTN_SPLIT_LASTBLOCK: return launch_split(a, kv_dtype, kLastBlockMerge, stream);
-        case KVATTN_SINGLE_LAUNCH_COOP: return launch_coop(a, kv_dtype, stream);
-        case KVATTN_SINGLE_LAUNCH_GRAPH: return launch_graph_pair(a, kv_dtype, stream);
+        case KVATTN_SPLIT_LASTBLOCK: return launch_split(a, kv_dtype, kLastBlockMerge, plan.lat, stream);
+        case KVATTN_SINGLE_LAUNCH_COOP: return launch_coop(a, kv_dtype, plan.lat, stream);
+        case KVATTN_SINGLE_LAUNCH_GRAPH: return launch_graph_pair(a, kv_dtype, plan.lat, stream);
         default: return KVATTN_ERR_STRATEGY;
     }
 }
@@ -1344,7 +1416,7 @@ int kvattn_forward_small(void* out, const void* qkv, const void* kv_cache, const
     if (!out) return KVATTN_ERR_NULL_POINTER;
     if (!aligned16(out)) return KVATTN_ERR_MISALIGNED;
     KV_TRY(resolve_len(d_cur_len));
-    return launch_fused_single(out, qkv, kv_cache, kv_scale, B, NH, maxT, d_cur_len, lens_per_seq, kv_dtype,
+    return launch_fused_single(out, qkv, kv_cache, kv_scale, B, NH, maxT, d_cur_len, lens_per_seq, 0, kv_dtype,
                                (hipStream_t)stream);
 }
 
@@ -1362,10 +1434,10 @@ int kvattn_forward_large(void* out, const void* qkv, const void* kv_cache, const
     bool capturing = false;
     KV_TRY(stream_capturing(stream, capturing));
     if (B == 1 && !capturing) {
-        const int st = launch_coop(a, kv_dtype, stream);
+        const int st = launch_coop(a, kv_dtype, latency_bound(B, NH, maxT), stream);
         if (st != KVATTN_ERR_COOP_TOO_LARGE) return st;
     }
-    KV_TRY(launch_split(a, kv_dtype, kPartialsOnly, stream));
+    KV_TRY(launch_split(a, kv_dtype, kPartialsOnly, latency_bound(B, NH, maxT), stream));
     return launch_merge(a, kv_dtype, stream);
 }
 
@@ -1377,7 +1449,7 @@ int kvattn_split(float* part_out, float* part_lse, float* part_max, const void* 
     KV_TRY(resolve_len(d_cur_len));
     const SplitArgs a = caller_partials(nullptr, qkv, kv_cache, kv_scale, B, NH, maxT, d_cur_len, lens_per_seq,
                                         part_out, part_lse, part_max, S);
-    return launch_split(a, kv_dtype, kPartialsOnly, (hipStream_t)stream);
+    return launch_split(a, kv_dtype, kPartialsOnly, latency_bound(B, NH, maxT), (hipStream_t)stream);
 }
 
 int kvattn_merge(void* out, const float* part_out, const float* part_lse, const float* part_max, int B, int NH,

@@ -115,6 +115,23 @@ def traffic(fetch_dir: str, write_dir: str, cmd_fetch: str, cmd_write: str) -> s
     return "\n".join(out) + "\n\n```\n" + "\n".join(lines) + "\n```\n"
 
 
+def l2(d: str, cmd: str) -> str:
+    """L2 (TCC) hit rate per kernel from a --pmc TCC_HIT_sum TCC_MISS_sum run."""
+    hit = _counter(d, "TCC_HIT_sum")
+    miss = _counter(d, "TCC_MISS_sum")
+    out = ["# L2 (TCC) hit rate per dispatch (rocprofv3 TCC_HIT_sum, TCC_MISS_sum)", "",
+           f"Command: `{cmd}`", "",
+           "MI355X exposes no Infinity Cache (MALL) counters through rocprofv3 on this stack; the L2 figures "
+           "below are the per-XCD L2 only.", "",
+           "| kernel (grid = work-items) | dispatches | L2 hits | L2 misses | hit rate |", "|---|---|---|---|---|"]
+    for k in sorted(hit, key=lambda x: -statistics.mean(miss.get(x, [0]))):
+        if not any(o in k for o in OWN_KERNELS):
+            continue
+        h, m = statistics.mean(hit[k]), statistics.mean(miss.get(k, [0.0]))
+        out.append(f"| `{k}` | {len(hit[k])} | {h:,.0f} | {m:,.0f} | {h / max(h + m, 1):.3f} |")
+    return "\n".join(out) + "\n"
+
+
 def read_traffic(md_path: str) -> dict:
     """{kernel-key: bytes} from a traffic summary written by this module."""
     res = {}
@@ -141,9 +158,14 @@ def main(argv=None):
     c.add_argument("write_dir")
     c.add_argument("--cmd-fetch", default="")
     c.add_argument("--cmd-write", default="")
+    h = sub.add_parser("l2")
+    h.add_argument("dir")
+    h.add_argument("--cmd", default="")
     a = p.parse_args(argv)
     if a.action == "trace":
         sys.stdout.write(trace(a.dir, a.title, a.cmd, a.all))
+    elif a.action == "l2":
+        sys.stdout.write(l2(a.dir, a.cmd))
     else:
         sys.stdout.write(traffic(a.fetch_dir, a.write_dir, a.cmd_fetch, a.cmd_write))
 
