@@ -1273,17 +1273,19 @@ int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scal
     if (!aligned16(out)) return KVATTN_ERR_MISALIGNED;
     Plan plan{};
     KV_TRY(make_plan(B, NH, maxT, len_hint, S, strategy, plan));
-    KV_TRY(resolve_len(d_cur_len));
     hipStream_t stream = (hipStream_t)stream_v;
 
-    if (plan.strategy == KVATTN_FUSED_SINGLE)
+    if (plan.strategy == KVATTN_FUSED_SINGLE) {
+        KV_TRY(resolve_len(d_cur_len));
         return launch_fused_single(out, qkv, kv, kv_scale, B, NH, maxT, d_cur_len, lens_per_seq,
                                    (lens_per_seq || len_hint < 0) ? 0 : len_hint + 1, kv_dtype, stream);
+    }
 
     if (!workspace) return KVATTN_ERR_WORKSPACE;
     if (!aligned16(workspace)) return KVATTN_ERR_MISALIGNED;
     const Workspace w = carve(workspace, B, NH, plan.slots);
     if (w.bytes > workspace_bytes) return KVATTN_ERR_WORKSPACE;
+    KV_TRY(resolve_len(d_cur_len));
 
     SplitArgs a{};
     a.out = out;

@@ -1,0 +1,86 @@
+"""CPU checks of the host-side planning (AUTO strategy, segmentation, workspace sizing) and
+of the Python binding's error mapping.  No GPU call is made: planning and argument
+validation happen before any HIP call."""
+import pytest
+
+from cuda_gpt2_inference_amd import kvattn
+
+ALIGNED = 1 << 20
+
+
+def up(x):
+    return (x + 255) // 256 * 256
+
+
+def carve_bytes(B, NH, slots):
+    return up(B * NH * 4) + 2 * up(B * NH * slots * 4) + up(B * NH * slots * 64 * 4)
+
+
+def test_auto_short_context_is_fused_single():
+    for hint in (0, 1, 100, 255):
+        assert kvattn.plan(1, 12, 64, 1024, kv_dtype="bf16", len_hint=hint) == (kvattn.FUSED_SINGLE, 1, 0)
+
+
+def test_auto_gpt2_layer_is_single_launch_split():
+    # T = 1024 at B=1, NH=12: about four 256-row segments per head, merged in-kernel.
+    assert kvattn.plan(1, 12, 64, 1024, kv_dtype="bf16", len_hint=1023) == (kvattn.SPLIT_LASTBLOCK, 4, 256)
+    # 257 positions: four segments would be 65 rows; rows per segment are a power of two.
+    assert kvattn.plan(1, 12, 64, 1024, kv_dtype="int8", len_hint=256) == (kvattn.SPLIT_LASTBLOCK, 8, 128)
+
+
+def test_auto_large_batch_streams_with_split_merge():
+    st, slots, rows = kvattn.plan(64, 12, 64, 8192, kv_dtype="bf16")
+    assert (st, slots, rows) == (kvattn.SPLIT_MERGE, 16, 512)
+
+
+def test_auto_skips_fused_single_when_scores_exceed_lds():
+    # 64 KB of LDS holds 16384 scores; maxT beyond that rules fused_single out.
+    st, _, _ = kvattn.plan(1, 12, 64, 20000, kv_dtype="bf16", len_hint=10)
+    assert st != kvattn.FUSED_SINGLE
+
+
+def test_explicit_strategies_and_partitions():
+    assert kvattn.plan(1, 12, 64, 1024, kv_dtype="f32", len_hint=1023, S=8, strategy="coop") == \
+        (kvattn.SINGLE_LAUNCH_COOP, 8, 0)
+    assert kvattn.plan(2, 3, 64, 1000, kv_dtype="bf16", S=-100, strategy="split_merge") == \
+        (kvattn.SPLIT_MERGE, 10, 100)
+    assert kvattn.plan(2, 3, 64, 1000, kv_dtype="bf16", S=0, strategy="graph")[0] == kvattn.SINGLE_LAUNCH_GRAPH
+
+
+@pytest.mark.parametrize("B,NH,maxT", [(1, 12, 1024), (64, 12, 8192), (3, 5, 777), (1, 1, 1)])
+def test_workspace_for_S0_covers_every_auto_plan(B, NH, maxT):
+    ws = kvattn.workspace_bytes(B, NH, 64, maxT, 0)
+    for hint in sorted(h for h in {-1, 0, 1, maxT // 7, maxT // 2, maxT - 1} if h < maxT):
+        for strategy in ("auto", "split_merge", "lastblock", "graph"):
+            _, slots, _ = kvattn.plan(B, NH, 64, maxT, kv_dtype="bf16", len_hint=hint, strategy=strategy)
+            assert carve_bytes(B, NH, slots) <= ws
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(len_hint=1024), kvattn.ERR_LENGTH),
+    (dict(len_hint=-2), kvattn.ERR_LENGTH),
+    (dict(strategy=9), kvattn.ERR_STRATEGY),
+    (dict(S=1 << 20, strategy="split_merge"), kvattn.ERR_SPLIT),
+])
+def test_plan_errors(kw, status):
+    a = dict(len_hint=-1, S=0, strategy="auto")
+    a.update(kw)
+    with pytest.raises(kvattn.KvAttnError) as ei:
+        kvattn.plan(1, 12, 64, 1024, kv_dtype="bf16", **a)
+    assert ei.value.status == status
+
+
+def test_binding_raises_with_status_and_text():
+    with pytest.raises(kvattn.KvAttnError) as ei:
+        kvattn.decode(ALIGNED, ALIGNED, ALIGNED, 1, 12, 48, 1024, kv_dtype="bf16", stream=0)
+    assert ei.value.status == kvattn.ERR_HEAD_DIM
+    assert "head size must be 64" in str(ei.value)
+    with pytest.raises(kvattn.KvAttnError) as ei:
+        kvattn.attention_kv_merge(ALIGNED, ALIGNED, ALIGNED, ALIGNED, 1, 12, 64, 0, kv_dtype="bf16", stream=0)
+    assert ei.value.status == kvattn.ERR_SPLIT
+    with pytest.raises(kvattn.KvAttnError) as ei:
+        kvattn.kv_cache_write(ALIGNED, ALIGNED, 1, 12, 64, 1024, kv_dtype="fp8", stream=0)
+    assert ei.value.status == kvattn.ERR_DTYPE
+    with pytest.raises(kvattn.KvAttnError) as ei:
+        kvattn.decode(ALIGNED, ALIGNED, ALIGNED, 1, 12, 64, 1024, kv_dtype="bf16", len_hint=1023, stream=0)
+    assert ei.value.status == kvattn.ERR_WORKSPACE     # split plan without a workspace
