@@ -118,6 +118,33 @@ class C2:
         graph_ms = timed(torch, graph.replay, a.steps)
         return graph_ms, eager_ms
 
+    def sweep(self, lengths=(1, 64, 128, 150, 255, 256, 257, 384, 512, 768, 1023, 1024), reps=50):
+        """AUTO across the context range of the 12-layer stack (the fused_single -> split
+        switch included): graph-replayed microseconds per call at each attended length."""
+        torch, kvattn = self.torch, self.kvattn
+        res = {}
+        for T in lengths:
+            self.cur.fill_(T - 1)
+            ws = kvattn.Workspace(self.B, self.NH, self.maxT, 0)
+            plan = kvattn.plan(self.B, self.NH, HD, self.maxT, kv_dtype="bf16", len_hint=T - 1)
+
+            def step():
+                for l in range(self.L):
+                    kvattn.decode(self.outs[l], self.qkvs[l], self.caches[l], self.B, self.NH, HD, self.maxT,
+                                  kv_dtype="bf16", cur_len=self.cur, len_hint=T - 1, **ws.kwargs())
+            s = torch.cuda.Stream()
+            graph = torch.cuda.CUDAGraph()
+            torch.cuda.synchronize()
+            with torch.cuda.stream(s):
+                with torch.cuda.graph(graph, stream=s):
+                    step()
+            graph.replay()
+            us = timed(torch, graph.replay, reps) * 1000.0 / self.L
+            res[str(T)] = {"us_per_call": round(us, 3), "strategy": kvattn.STRATEGY_NAMES[plan[0]],
+                           "segments_per_head": plan[1]}
+        self.cur.fill_(self.T - 1)
+        return res
+
     def cold(self, reps=50):
         """One call on a cold cache: before every call 512 MiB are written (more than the
         256 MiB Infinity Cache and the 32 MiB of L2), as the reference lab flushes L2 before
@@ -349,6 +376,7 @@ def main():
     graph_ms, eager_ms = c2.measure()
     rel = c2.check()
     cold_us = c2.cold()
+    t_sweep = c2.sweep()
     us_call = graph_ms * 1000.0 / c2.L
     nbytes = bytes_per_call([c2.T], c2.NH, 2, 2, c2.B)
     achieved = nbytes / (us_call * 1e-6) / 1e9
@@ -389,6 +417,7 @@ def main():
         "cpu_baseline": cpu,
         "extra": {"eager_us_per_call": round(eager_ms * 1000.0 / c2.L, 4),
                   "cold_us_per_call": round(cold_us, 3),
+                  "c2_context_sweep": t_sweep,
                   "rel_err_vs_f64": rel,
                   "gpu_vs_cpu_speedup": (round(cpu["value"] / us_call, 1) if cpu else None),
                   "c5": c5, "configs": configs, "gpu": torch.cuda.get_device_name(dev),

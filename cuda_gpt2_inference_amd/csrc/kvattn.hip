@@ -12,16 +12,20 @@
 // bound (1 flop per BF16 byte), so no matrix cores are involved.
 //
 // Strategies (host side at the bottom of this file):
-//   fused_single     one 256-thread workgroup per (b,h); scores staged in LDS, then a
-//                    V pass with the exact maximum (reference strategy 1)
+//   fused_single     one workgroup per (b,h); when every wave holds one tile the scores
+//                    stay in registers, otherwise they are staged in LDS, then a V pass
+//                    with the exact maximum (reference strategy 1)
 //   split            one workgroup per (b,h,segment); per-lane-group online softmax
 //                    (m, l, acc) in base 2, then a workgroup merge into the reference's
 //                    partial format (max in natural-log units, exp-sum, weighted V sum)
 //   merge            one wave per (b,h) combining the segment partials
-//   split+lastblock  split whose last finishing segment of a (b,h) merges, ordered by an
-//                    agent-scope release/acquire counter; one ordinary launch
+//   split+lastblock  split whose last finishing segment of a (b,h) merges; partials travel
+//                    through coherent (sc1) stores and loads and a counter atomic; one
+//                    ordinary, graph-capturable launch
 //   split+coop       split + grid barrier + merge by segment 0 (cooperative launch)
 //   split+graph      split and merge kernel nodes in a hipGraph, one hipGraphLaunch
+// Workgroup size and tile depth are template parameters (the "latency" and "streaming"
+// shapes picked per call by the host plan; both are 4 waves in this build).
 #include <hip/hip_runtime.h>
 #include <hip/hip_cooperative_groups.h>
 
