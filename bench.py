@@ -120,29 +120,90 @@ class C2:
 
     def sweep(self, lengths=(1, 64, 128, 150, 255, 256, 257, 384, 512, 768, 1023, 1024), reps=50):
         """AUTO across the context range of the 12-layer stack (the fused_single -> split
-        switch included): graph-replayed microseconds per call at each attended length."""
+        switch included): graph-replayed microseconds per call at each attended length, with
+        the plan made on the host from the length (`us_per_call`) and with no hint, the
+        segmentation planned on the device from the device length (`us_per_call_device_plan`)."""
         torch, kvattn = self.torch, self.kvattn
-        res = {}
-        for T in lengths:
-            self.cur.fill_(T - 1)
-            ws = kvattn.Workspace(self.B, self.NH, self.maxT, 0)
-            plan = kvattn.plan(self.B, self.NH, HD, self.maxT, kv_dtype="bf16", len_hint=T - 1)
+        ws = kvattn.Workspace(self.B, self.NH, self.maxT, 0)
 
+        def capture(hint):
             def step():
                 for l in range(self.L):
                     kvattn.decode(self.outs[l], self.qkvs[l], self.caches[l], self.B, self.NH, HD, self.maxT,
-                                  kv_dtype="bf16", cur_len=self.cur, len_hint=T - 1, **ws.kwargs())
+                                  kv_dtype="bf16", cur_len=self.cur, len_hint=hint, **ws.kwargs())
             s = torch.cuda.Stream()
             graph = torch.cuda.CUDAGraph()
             torch.cuda.synchronize()
             with torch.cuda.stream(s):
                 with torch.cuda.graph(graph, stream=s):
                     step()
+            return graph
+
+        device_plan = capture(-1)
+        res = {}
+        for T in lengths:
+            self.cur.fill_(T - 1)
+            plan = kvattn.plan(self.B, self.NH, HD, self.maxT, kv_dtype="bf16", len_hint=T - 1)
+            graph = capture(T - 1)
             graph.replay()
             us = timed(torch, graph.replay, reps) * 1000.0 / self.L
-            res[str(T)] = {"us_per_call": round(us, 3), "strategy": kvattn.STRATEGY_NAMES[plan[0]],
-                           "segments_per_head": plan[1]}
+            device_plan.replay()
+            us_dev = timed(torch, device_plan.replay, reps) * 1000.0 / self.L
+            res[str(T)] = {"us_per_call": round(us, 3), "us_per_call_device_plan": round(us_dev, 3),
+                           "strategy": kvattn.STRATEGY_NAMES[plan[0]], "segments_per_head": plan[1]}
         self.cur.fill_(self.T - 1)
+        return res
+
+    def token_sweep(self):
+        """Token by token over every context length 1..maxT, as the engine replays its step
+        graph: before each replay the device length is written by a stream-ordered kernel.
+        Graphs (12 layers each):
+          one_graph     per layer append + AUTO attention with no length hint (segmentation
+                        planned on the device), captured once;
+          graph_pair    the reference's pair: append + fused_single below 150 positions,
+                        append + split + merge with S = 8 from 150 on (host switch per token);
+          attn_only     AUTO attention with no hint, without the append.
+        Mean microseconds per token (whole 12-layer graph) and per layer."""
+        torch, kvattn = self.torch, self.kvattn
+        ws = kvattn.Workspace(self.B, self.NH, self.maxT, 0)
+        ws8 = kvattn.Workspace(self.B, self.NH, self.maxT, 8)
+
+        def capture(strategy, S, append, w):
+            def step():
+                for l in range(self.L):
+                    if append:
+                        kvattn.kv_cache_write(self.caches[l], self.qkvs[l], self.B, self.NH, HD, self.maxT,
+                                              kv_dtype="bf16", cur_len=self.cur)
+                    kvattn.decode(self.outs[l], self.qkvs[l], self.caches[l], self.B, self.NH, HD, self.maxT,
+                                  kv_dtype="bf16", cur_len=self.cur, S=S, strategy=strategy, **w.kwargs())
+            s = torch.cuda.Stream()
+            graph = torch.cuda.CUDAGraph()
+            torch.cuda.synchronize()
+            with torch.cuda.stream(s):
+                with torch.cuda.graph(graph, stream=s):
+                    step()
+            return graph
+
+        one = capture("auto", 0, True, ws)
+        small, large = capture("fused_single", 0, True, ws), capture("split_merge", 8, True, ws8)
+        attn = capture("auto", 0, False, ws)
+        modes = {"one_graph": lambda t: one, "graph_pair": lambda t: small if t < 150 else large,
+                 "attn_only": lambda t: attn}
+        res = {"tokens": self.maxT}
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for name, pick in modes.items():
+            for rep in range(2):            # the first pass warms up
+                torch.cuda.synchronize()
+                e0.record()
+                for t in range(self.maxT):
+                    kvattn.set_cur_len_async(t, d_cur_len=self.cur)
+                    pick(t).replay()
+                e1.record()
+                torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1000.0 / self.maxT
+            res[name] = {"us_per_token": round(us, 2), "us_per_layer": round(us / self.L, 3)}
+        self.cur.fill_(self.T - 1)
+        torch.cuda.synchronize()
         return res
 
     def cold(self, reps=50):
@@ -377,6 +438,7 @@ def main():
     rel = c2.check()
     cold_us = c2.cold()
     t_sweep = c2.sweep()
+    tok_sweep = c2.token_sweep()
     us_call = graph_ms * 1000.0 / c2.L
     nbytes = bytes_per_call([c2.T], c2.NH, 2, 2, c2.B)
     achieved = nbytes / (us_call * 1e-6) / 1e9
@@ -418,6 +480,7 @@ def main():
         "extra": {"eager_us_per_call": round(eager_ms * 1000.0 / c2.L, 4),
                   "cold_us_per_call": round(cold_us, 3),
                   "c2_context_sweep": t_sweep,
+                  "c2_token_sweep": tok_sweep,
                   "rel_err_vs_f64": rel,
                   "gpu_vs_cpu_speedup": (round(cpu["value"] / us_call, 1) if cpu else None),
                   "c5": c5, "configs": configs, "gpu": torch.cuda.get_device_name(dev),

@@ -50,6 +50,8 @@ constexpr float kLn2 = 0.69314718055994531f;
 constexpr float kEmptyMax = -FLT_MAX;   // max of an empty segment (reference sentinel)
 constexpr float kStartMax = -1.0e30f;   // finite start value of every running max
 constexpr int kMinSegRows = 64;         // smallest automatic segment length
+constexpr int kMaxSegRows = 512;        // largest automatic segment length
+constexpr int kFusedMaxRows = 256;      // automatic plans keep up to this many positions in one workgroup
 constexpr int kMaxSegments = 1 << 16;   // upper bound on segments per (b,h)
 constexpr int kMaxT = 1 << 23;          // keeps per-slot byte offsets inside 32 bits
 constexpr size_t kFusedMaxLds = 64 * 1024;  // dynamic LDS of fused_single (scores)
@@ -83,8 +85,8 @@ template <int DT> constexpr int kRowsPerLoad = kWave / Row<DT>::kLanes;
 #define KVATTN_UNROLL_BYTE 4
 #endif
 template <int DT> constexpr int kUnroll = Row<DT>::k8bit ? KVATTN_UNROLL_BYTE : KVATTN_UNROLL_WIDE;
-// Latency-bound calls use 16-wave workgroups with 16 rows per wave per tile, so that each
-// wave's dependent chain (dot, row reduction, exp, weighted sum) is short.
+// Latency-bound calls (the "latency" shape) take KVATTN_LAT_ROWS rows per wave per tile, so
+// that a GPT-2 head of up to 256 positions is one tile per wave of a 4-wave workgroup.
 #ifndef KVATTN_LAT_WAVES
 #define KVATTN_LAT_WAVES 4
 #endif
@@ -611,16 +613,39 @@ struct SplitArgs {
     int lens_per_seq;
     int B, NH, maxT;
     int S;          // segment slots per (b,h): the grid stride and the partial stride
-    int seg_rows;   // > 0: fixed rows per segment; 0: reference partition ceil(total/S)
+    int seg_rows;   // > 0: fixed rows per segment; 0: reference partition ceil(total/S);
+                    // kDevicePlan: planned_rows(total) of the device length
     int spec_rows;  // the host's view of the attended length (0: unknown); see split_kernel
     float qscale;   // scale * log2(e)
 };
 
 struct Item {
-    int b, h, s, total, n_seg;
+    int b, h, s, total, n_seg, rows;
 };
 
 __host__ __device__ __forceinline__ int ceil_div_i(int a, int b) { return (a + b - 1) / b; }
+
+constexpr int kDevicePlan = -1;
+
+// Rows per segment for an attended length of `total`: the whole length in one segment up
+// to kFusedMaxRows positions, otherwise about four segments of a power-of-two length
+// between kMinSegRows and kMaxSegRows.  The host plans with it from its length hint; with
+// seg_rows == kDevicePlan every workgroup plans with it from the device length, so one
+// launch (or one captured graph) serves every length up to maxT.
+__host__ __device__ __forceinline__ int planned_rows(int total) {
+    if (total <= kFusedMaxRows) return total > 0 ? total : 1;
+    const int want = ceil_div_i(total, 4);
+    int r = kMinSegRows;
+    while (r < want && r < kMaxSegRows) r <<= 1;
+    return r;
+}
+
+// Segments of a (b,h) whose length is `total` under fixed or device-planned rows
+// (seg_rows != 0); `rows` receives the segment length.
+__device__ __forceinline__ int seg_count(int seg_rows, int total, int& rows) {
+    rows = seg_rows > 0 ? seg_rows : planned_rows(total);
+    return ceil_div_i(total, rows);
+}
 
 // Map a workgroup index to (b, h, segment).  Uniform lengths (or the reference
 // partition) use the dense grid B*NH*S; ragged lengths with fixed-size segments pack
@@ -634,7 +659,8 @@ __device__ __forceinline__ bool locate(const SplitArgs& a, int x, Item& it) {
         it.h = bh - it.b * a.NH;
         if (it.b >= a.B) return false;
         it.total = seq_total(a.cur_len, a.lens_per_seq, it.b, a.maxT);
-        it.n_seg = a.seg_rows > 0 ? ceil_div_i(it.total, a.seg_rows) : a.S;
+        it.rows = 0;
+        it.n_seg = a.seg_rows != 0 ? seg_count(a.seg_rows, it.total, it.rows) : a.S;
         return it.s < it.n_seg;
     }
     const int lane = threadIdx.x & (kWave - 1);
@@ -643,8 +669,9 @@ __device__ __forceinline__ bool locate(const SplitArgs& a, int x, Item& it) {
         const int b = b0 + lane;
         int tot = 0, cnt = 0;
         if (b < a.B) {
+            int rows;
             tot = seq_total(a.cur_len, 1, b, a.maxT);
-            cnt = a.NH * ceil_div_i(tot, a.seg_rows);
+            cnt = a.NH * seg_count(a.seg_rows, tot, rows);
         }
         int incl = cnt;
 #pragma unroll
@@ -659,7 +686,7 @@ __device__ __forceinline__ bool locate(const SplitArgs& a, int x, Item& it) {
             const int excl = __shfl(incl - cnt, L);
             it.b = b0 + L;
             it.total = __shfl(tot, L);
-            it.n_seg = ceil_div_i(it.total, a.seg_rows);
+            it.n_seg = seg_count(a.seg_rows, it.total, it.rows);
             const int local = x - base - excl;
             it.h = local / it.n_seg;
             it.s = local - it.h * it.n_seg;
@@ -784,9 +811,9 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
 
     if (active) {
         int j0, j1;
-        if (a.seg_rows > 0) {
-            j0 = it.s * a.seg_rows;
-            j1 = min(j0 + a.seg_rows, it.total);
+        if (a.seg_rows != 0) {
+            j0 = it.s * it.rows;
+            j1 = min(j0 + it.rows, it.total);
         } else {
             const int chunk = ceil_div_i(it.total, a.S);
             j0 = it.s * chunk;
@@ -837,8 +864,13 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                     L = fmaf(g, s_l[w], L);
                     A = fmaf(g, s_acc[w][lane], A);
                 }
-                put<kCoh>(a.part_out + pidx * kHeadDim + lane, A);
-                if (lane == 0) { put<kCoh>(a.part_max + pidx, Mb * kLn2); put<kCoh>(a.part_lse + pidx, L); }
+                if (kMode == kLastBlockMerge && it.n_seg == 1) {
+                    // The only segment of its (b,h): the result needs no merge.
+                    store_out<DT>(a.out, (size_t)bh * kHeadDim + lane, A / L);
+                } else {
+                    put<kCoh>(a.part_out + pidx * kHeadDim + lane, A);
+                    if (lane == 0) { put<kCoh>(a.part_max + pidx, Mb * kLn2); put<kCoh>(a.part_lse + pidx, L); }
+                }
             }
         }
     }
@@ -847,8 +879,8 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
         // Wave 0 wrote this segment's partial with coherent stores.  Once they are
         // acknowledged it counts the segment; the wave that brings the (b,h) counter to
         // n_seg reads every partial with coherent loads, merges them and re-arms the
-        // counter for the next call.
-        if (wave == 0) {
+        // counter for the next call.  A (b,h) of one segment has already written out.
+        if (wave == 0 && it.n_seg > 1) {
             wait_vm_stores();
             unsigned prev = 0;
             if (lane == 0)
@@ -874,8 +906,8 @@ template <int DT>
 __global__ __launch_bounds__(kWave) void merge_kernel(SplitArgs a) {
     const int bh = blockIdx.x;
     const int b = bh / a.NH;
-    int n_seg = a.S;
-    if (a.seg_rows > 0) n_seg = ceil_div_i(seq_total(a.cur_len, a.lens_per_seq, b, a.maxT), a.seg_rows);
+    int n_seg = a.S, rows;
+    if (a.seg_rows != 0) n_seg = seg_count(a.seg_rows, seq_total(a.cur_len, a.lens_per_seq, b, a.maxT), rows);
     merge_partials<DT, false>(a.out, a.part_out, a.part_lse, a.part_max, a.S, n_seg, bh, threadIdx.x);
 }
 
@@ -936,6 +968,11 @@ __global__ __launch_bounds__(kBlock) void cache_write_w8_kernel(uint8_t* __restr
 }
 
 __device__ int g_cur_len = 0;
+
+// Stream-ordered write of the device length (one lane, one vector store).
+__global__ __launch_bounds__(kWave) void set_len_kernel(int* __restrict__ p, int v) {
+    if (threadIdx.x == 0) *p = v;
+}
 
 // ------------------------------------------------------------------------------------
 // Host side.
@@ -1223,15 +1260,24 @@ int segment_slots(int maxT, int S, int& slots, int& seg_rows) {
 int auto_seg_rows(int total_hint) {
     const int want = (total_hint + 3) / 4;
     int r = kMinSegRows;
-    while (r < want && r < 512) r <<= 1;
+    while (r < want && r < kMaxSegRows) r <<= 1;
     return r;
 }
 
-constexpr int kFusedMaxRows = 256;        // AUTO: fused_single up to this many positions
+// Segment slots that cover planned_rows() at every length up to maxT: one segment up to
+// kFusedMaxRows positions, at most four while planned_rows(total) >= total / 4, and
+// ceil(total / kMaxSegRows) beyond.
+int planned_slots(int maxT) {
+    if (maxT <= kFusedMaxRows) return 1;
+    const int s = ceil_div_i(maxT, kMaxSegRows);
+    return s > 4 ? s : 4;
+}
+
 constexpr long long kStreamRows = 1 << 19; // AUTO: split + merge kernel from this many rows
 
 // Resolve AUTO and the segmentation.  S > 0: reference partition with S slots; S < 0:
-// -S rows per segment; S == 0: automatic rows per segment from the length hint.
+// -S rows per segment; S == 0: automatic rows per segment, from the length hint, or
+// planned on the device from the device length when there is no hint (len_hint == -1).
 struct Plan {
     int strategy, slots, seg_rows;
     bool lat;   // latency-bound call: 16-wave workgroups with short tiles
@@ -1261,7 +1307,10 @@ int make_plan(int B, int NH, int maxT, int len_hint, int S, int strategy, Plan& 
         return KVATTN_OK;
     }
     KV_TRY(segment_slots(maxT, S, p.slots, p.seg_rows));
-    if (S == 0) {
+    if (S == 0 && len_hint < 0) {
+        p.seg_rows = kDevicePlan;
+        p.slots = planned_slots(maxT);
+    } else if (S == 0) {
         p.seg_rows = auto_seg_rows(total_hint);
         p.slots = ceil_div_i(maxT, p.seg_rows);
     }
@@ -1390,6 +1439,15 @@ int kvattn_cur_len_symbol(int** d_cur_len) {
 
 int kvattn_set_cur_len(int cur_len) {
     KV_HIP(hipMemcpyToSymbol(HIP_SYMBOL(g_cur_len), &cur_len, sizeof(int), 0, hipMemcpyHostToDevice));
+    return KVATTN_OK;
+}
+
+int kvattn_set_cur_len_async(int* d_cur_len, int cur_len, void* stream) {
+    if (cur_len < 0 || cur_len >= kMaxT) return KVATTN_ERR_LENGTH;
+    const int* p = d_cur_len;
+    KV_TRY(resolve_len(p));
+    hipLaunchKernelGGL(set_len_kernel, dim3(1), dim3(kWave), 0, (hipStream_t)stream, const_cast<int*>(p), cur_len);
+    KV_HIP(hipGetLastError());
     return KVATTN_OK;
 }
 

@@ -74,6 +74,7 @@ SIGNATURES = {
     "kvattn_last_hip_error": (_i, []),
     "kvattn_cur_len_symbol": (_i, [ctypes.POINTER(_vp)]),
     "kvattn_set_cur_len": (_i, [_i]),
+    "kvattn_set_cur_len_async": (_i, [_vp, _i, _vp]),
     "kvattn_cache_write": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp]),
     "kvattn_forward_small": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp]),
     "kvattn_forward_large": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _vp, _vp, _vp, _i, _i, _vp]),
@@ -164,6 +165,12 @@ def cur_len_symbol() -> int:
 
 def set_cur_len(cur_len: int) -> None:
     _check(lib().kvattn_set_cur_len(int(cur_len)), "kvattn_set_cur_len")
+
+
+def set_cur_len_async(cur_len: int, d_cur_len=None, stream=None) -> None:
+    """Stream-ordered write of the device length (no host synchronisation)."""
+    _check(lib().kvattn_set_cur_len_async(_ptr(d_cur_len), int(cur_len), _stream(stream)),
+           "kvattn_set_cur_len_async")
 
 
 def kv_cache_write(kv_cache, qkv, B, NH, hs, maxT, *, kv_dtype, kv_scale=None, cur_len=None,

@@ -88,6 +88,12 @@ int kvattn_cur_len_symbol(int** d_cur_len);
  * (inference_gpt2_opt.cu:409,548). */
 int kvattn_set_cur_len(int cur_len);
 
+/* Enqueue the write of cur_len into *d_cur_len (NULL: the library's own device length) on
+ * `stream`, without a host synchronisation; capturable.  Replaces the per-token
+ * cudaMemcpyToSymbol(g_cur_len, ...) before each graph replay (inference_gpt2_opt.cu:548),
+ * which blocks the host until the copy is done. */
+int kvattn_set_cur_len_async(int* d_cur_len, int cur_len, void* stream);
+
 /* Append the current token's K and V (from qkv) into column cur_len of every (b,h) slot.
  * F32/BF16 copy the elements; INT8/FP8 quantise each 64-element row with
  * scale = amax/127 (INT8) or amax/448 (FP8), store the codes and the FP32 scale.
@@ -149,7 +155,8 @@ int kvattn_workspace_init(void* workspace, size_t workspace_bytes, void* stream)
 /* The launch plan kvattn_decode would use for these arguments, without launching:
  * *strategy_out = the resolved kvattn_strategy (AUTO resolved), *segments_out = segment
  * slots per (b,h) (1 for FUSED_SINGLE), *seg_rows_out = rows per segment (0 when the
- * reference partition ceil(total/S) is used).  No reference counterpart: it exposes the
+ * reference partition ceil(total/S) is used, -1 when the kernels plan the rows from the
+ * device length).  No reference counterpart: it exposes the
  * AUTO choice, which the reference makes inline in its caller (inference_gpt2_opt.cu:247,
  * 304,331: fused_single below a length threshold, split + merge above it). */
 int kvattn_plan(int B, int NH, int hs, int maxT, int len_hint, int S, int strategy, int kv_dtype,
@@ -159,9 +166,15 @@ int kvattn_plan(int B, int NH, int hs, int maxT, int len_hint, int S, int strate
  * attention block of forward_kv_graph_ready (inference_gpt2_opt.cu:298-347) maps onto.
  *   strategy   kvattn_strategy; AUTO picks from len_hint (the host's view of cur_len,
  *              used for the choice only; -1 = unknown, treated as maxT-1).
+ *   len_hint   -1 when the call must serve any length, as a graph captured once and
+ *              replayed token after token: with S == 0 the kernels then plan the
+ *              segmentation from the device length (one segment up to 256 positions,
+ *              about four beyond), where the reference captures a small and a large
+ *              graph and picks one per token (inference_gpt2_opt.cu:420-449,556).
  *   S          segments per (b,h) for the split strategies: S > 0 uses the reference
- *              partition chunk = ceil(total/S); S == 0 lets the library pick a fixed
- *              number of rows per segment and the per-sequence count from each length.
+ *              partition chunk = ceil(total/S); S < 0 uses -S rows per segment; S == 0
+ *              lets the library pick the rows per segment (from len_hint, or on the
+ *              device) and the per-sequence count from each length.
  *   workspace  device memory of kvattn_workspace_bytes(B, NH, hs, maxT, S) bytes,
  *              initialised once with kvattn_workspace_init; may be NULL for
  *              FUSED_SINGLE.  Calls sharing a workspace must be ordered (one stream).

@@ -42,6 +42,11 @@ inline int* cur_len_symbol() {
 // cudaMemcpyToSymbol(g_cur_len, &cur_len, sizeof(int)) (inference_gpt2_opt.cu:409,548).
 inline void set_cur_len(int cur_len) { kvattnCheck(kvattn_set_cur_len(cur_len)); }
 
+// The same write, enqueued on a stream (no host synchronisation; capturable).
+inline void set_cur_len_async(int cur_len, hipStream_t stream, int* d_cur_len = nullptr) {
+    kvattnCheck(kvattn_set_cur_len_async(d_cur_len, cur_len, stream));
+}
+
 // kv_cache_write_kernel<<<CEIL_DIV(B*NH*hs,256), 256, 0, stream>>>(kv_cache, qkv, B, NH, hs, maxT)
 // (Inference_gpt2/attention_kvcache.cuh:46-64, launched at inference_gpt2_opt.cu:329).
 inline void kv_cache_write(void* kv_cache, const void* qkv, int B, int NH, int hs, int maxT,

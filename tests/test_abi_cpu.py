@@ -103,6 +103,8 @@ def test_other_entry_point_errors():
     assert L.kvattn_merge(ALIGNED, ALIGNED, ALIGNED, ALIGNED, 1, 12, 64, 1 << 20, 1, None) == kvattn.ERR_SPLIT
     assert L.kvattn_merge(ALIGNED + 4, ALIGNED, ALIGNED, ALIGNED, 1, 12, 64, 8, 1, None) == kvattn.ERR_MISALIGNED
     assert L.kvattn_cur_len_symbol(None) == kvattn.ERR_NULL_POINTER
+    assert L.kvattn_set_cur_len_async(ALIGNED, -1, None) == kvattn.ERR_LENGTH
+    assert L.kvattn_set_cur_len_async(ALIGNED, 1 << 23, None) == kvattn.ERR_LENGTH
     assert L.kvattn_workspace_init(None, 0, None) == kvattn.ERR_NULL_POINTER
 
 

@@ -1,0 +1,210 @@
+"""Engine-level use of the decode attention on an MI355X: lengths planned on the device and a
+12-layer decode step captured once and replayed token by token.
+
+The reference engine captures two whole-step graphs (a "small" one with fused_single below
+a length threshold and a "large" one with split + merge) and picks one per token, writing
+the device length with a blocking cudaMemcpyToSymbol before each replay
+(inference_gpt2_opt.cu:420-449,544-556).  Here the step is captured once with no length
+hint, the kernels plan the segmentation from the device length, and the length is written
+with a stream-ordered kernel.  Outputs are checked against the oracle at the stated
+tolerance (BF16 1e-2, FP32 1e-5, 8-bit 2e-2); appended cache rows bit for bit.
+"""
+import numpy as np
+import pytest
+
+from kvcases import HS, assert_close, make_case, out_tensor, to_device
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+# Lengths around every change of the device plan: one segment up to 256 positions, then
+# 128-row segments (257..512), 256-row (513..1024), 512-row (1025..).
+PLAN_EDGES = (1, 2, 63, 64, 255, 256, 257, 300, 511, 512, 513, 1000, 1024, 1025, 2048, 2049, 2100)
+
+
+def _kv():
+    from cuda_gpt2_inference_amd import kvattn
+    return kvattn
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "int8", "fp8"])
+def test_device_plan_uniform_length(dev, dtype):
+    """One device length for the whole batch (dense grid), no host hint: every split
+    strategy at every plan edge, from a single workspace sized for S = 0."""
+    import torch
+    kvattn = _kv()
+    B, NH, maxT = 2, 3, 2100
+    case = make_case(dtype, B, NH, maxT, 0, seed=31)
+    qkv, cache, scale, _ = to_device(case, dev)
+    cur = torch.zeros(1, dtype=torch.int32, device=dev)
+    ws = kvattn.Workspace(B, NH, maxT, 0)
+    for strategy in ("auto", "lastblock", "split_merge", "graph", "coop"):
+        assert kvattn.plan(B, NH, HS, maxT, kv_dtype=dtype, strategy=strategy)[2] == -1
+        for total in PLAN_EDGES:
+            cur.fill_(total - 1)
+            case.cur_lens[:] = total - 1
+            out = out_tensor(case, dev)
+            kvattn.decode(out, qkv, cache, B, NH, HS, maxT, kv_dtype=dtype, kv_scale=scale, cur_len=cur,
+                          strategy=strategy, **ws.kwargs())
+            torch.cuda.synchronize()
+            assert_close(out.float().cpu().numpy(), case.reference(), dtype, f"{strategy} T={total}")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "int8"])
+def test_device_plan_ragged_lengths(dev, dtype):
+    """Per-sequence lengths (compacted grid): each sequence plans its own segments."""
+    import torch
+    kvattn = _kv()
+    B, NH, maxT = len(PLAN_EDGES), 2, 2100
+    case = make_case(dtype, B, NH, maxT, np.array(PLAN_EDGES, np.int32) - 1, seed=32)
+    qkv, cache, scale, cur = to_device(case, dev)
+    ref = case.reference()
+    ws = kvattn.Workspace(B, NH, maxT, 0)
+    for strategy in ("auto", "lastblock", "split_merge", "graph", "coop"):
+        out = out_tensor(case, dev)
+        kvattn.decode(out, qkv, cache, B, NH, HS, maxT, kv_dtype=dtype, kv_scale=scale, cur_len=cur,
+                      lens_per_seq=True, strategy=strategy, **ws.kwargs())
+        torch.cuda.synchronize()
+        assert_close(out.float().cpu().numpy(), ref, dtype, f"ragged {strategy}")
+
+
+def test_set_cur_len_async(dev):
+    """The stream-ordered length write, into a caller's int and into the library's own
+    length (observed through an append that uses it)."""
+    import torch
+    kvattn = _kv()
+    d = torch.full((4,), -7, dtype=torch.int32, device=dev)
+    kvattn.set_cur_len_async(1234, d_cur_len=d[2:])
+    torch.cuda.synchronize()
+    assert d.cpu().tolist() == [-7, -7, 1234, -7]
+    maxT = 8
+    cache = torch.zeros(2 * maxT * HS, dtype=torch.float32, device=dev)
+    qkv = torch.arange(3 * HS, dtype=torch.float32, device=dev) + 1.0
+    kvattn.set_cur_len_async(5)
+    kvattn.kv_cache_write(cache, qkv, 1, 1, HS, maxT, kv_dtype="f32")
+    torch.cuda.synchronize()
+    c = cache.view(2, maxT, HS).cpu()
+    assert torch.equal(c[0, 5], qkv[HS:2 * HS].cpu()) and torch.equal(c[1, 5], qkv[2 * HS:].cpu())
+    assert int((c != 0).any(dim=2).sum()) == 2
+
+
+class Engine:
+    """The attention block of a decode step for L layers (append, then attention, per
+    layer), captured into a graph over per-layer qkv / out buffers and one KV cache
+    allocation with the reference's layer stride 2*B*NH*maxT*hs (inference_gpt2_opt.cu:324)."""
+
+    def __init__(self, dev, L, B, NH, maxT, dtype):
+        import torch
+        self.kvattn = _kv()
+        self.L, self.B, self.NH, self.maxT, self.dtype = L, B, NH, maxT, dtype
+        wide = torch.float32 if dtype == "f32" else torch.bfloat16
+        n_cache = 2 * B * NH * maxT * HS
+        self.cache = torch.zeros(L * n_cache, dtype=torch.uint8 if dtype in ("int8", "fp8") else wide, device=dev)
+        self.scale = torch.zeros(L * 2 * B * NH * maxT, dtype=torch.float32, device=dev) \
+            if dtype in ("int8", "fp8") else None
+        self.qkv = torch.zeros(L, B * 3 * NH * HS, dtype=wide, device=dev)
+        self.out = torch.zeros(L, B * NH * HS, dtype=wide, device=dev)
+        self.cur = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.ws = self.kvattn.Workspace(B, NH, maxT, 0)
+        self.n_cache = n_cache
+
+    def layer_cache(self, l):
+        return self.cache[l * self.n_cache:(l + 1) * self.n_cache]
+
+    def layer_scale(self, l):
+        n = 2 * self.B * self.NH * self.maxT
+        return None if self.scale is None else self.scale[l * n:(l + 1) * n]
+
+    def step(self, strategy="auto", S=0):
+        k = self.kvattn
+        for l in range(self.L):
+            k.kv_cache_write(self.layer_cache(l), self.qkv[l], self.B, self.NH, HS, self.maxT, kv_dtype=self.dtype,
+                             kv_scale=self.layer_scale(l), cur_len=self.cur)
+            k.decode(self.out[l], self.qkv[l], self.layer_cache(l), self.B, self.NH, HS, self.maxT,
+                     kv_dtype=self.dtype, kv_scale=self.layer_scale(l), cur_len=self.cur, S=S, strategy=strategy,
+                     **self.ws.kwargs())
+
+    def capture(self, strategy="auto", S=0):
+        import torch
+        torch.cuda.synchronize()
+        s = torch.cuda.Stream()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                self.step(strategy, S)
+        torch.cuda.synchronize()
+        return g
+
+
+def _host_values(t, dtype):
+    import torch
+    if dtype == "f32":
+        return t.cpu().numpy().astype(np.float32)
+    return oracle.bf16_decode(t.view(torch.int16).cpu().numpy().view(np.uint16))
+
+
+@pytest.mark.parametrize("dtype,mode", [("bf16", "one_graph"), ("bf16", "graph_pair"), ("fp8", "one_graph")])
+def test_decode_step_token_by_token(dev, dtype, mode):
+    """GPT-2 shape, 12 layers, B=1, NH=12, maxT=1024: the step graph is replayed for every
+    token 1..1024 with fresh qkv and the device length advanced by set_cur_len_async.
+    one_graph: one capture, AUTO with no hint.  graph_pair: the reference's two graphs,
+    fused_single below 150 positions and split + merge with S = 8 above (selection on the
+    host per token, as inference_gpt2_opt.cu:556).  Checked: every appended row bit for bit
+    (8-bit: codes and scales against the oracle's quantiser) and the outputs of all layers
+    at 40 tokens (every plan edge and a stride) against the oracle."""
+    import torch
+    kvattn = _kv()
+    L, B, NH, maxT = 12, 1, 12, 1024
+    eng = Engine(dev, L, B, NH, maxT, dtype)
+    if mode == "one_graph":
+        graphs = [eng.capture("auto")]
+        pick = lambda cur_len: graphs[0]
+    else:
+        graphs = [eng.capture("fused_single"), eng.capture("split_merge", S=8)]
+        pick = lambda cur_len: graphs[0] if cur_len < 150 else graphs[1]
+    g = torch.Generator(device=dev)
+    g.manual_seed(41)
+    wide = torch.float32 if dtype == "f32" else torch.bfloat16
+    qkv_all = torch.randn(maxT, L, B * 3 * NH * HS, generator=g, device=dev).to(wide)
+    check_tokens = sorted(set(PLAN_EDGES[:13]) | {149, 150, 151} | set(range(5, maxT, 41)))
+    hist = {}
+    for t in range(maxT):                  # token at position t, attends t + 1 positions
+        eng.qkv.copy_(qkv_all[t])
+        kvattn.set_cur_len_async(t, d_cur_len=eng.cur)
+        pick(t).replay()
+        if t + 1 in check_tokens:
+            hist[t + 1] = eng.out.clone()
+    torch.cuda.synchronize()
+
+    qh = _host_values(qkv_all, dtype).reshape(maxT, L, B, 3, NH, HS)
+    if dtype in ("bf16", "f32"):
+        # Appended rows: column j of layer l holds K and V of token j.
+        c = eng.cache.view(L, 2, B, NH, maxT, HS)
+        got_k = _host_values(c[:, 0], dtype)
+        got_v = _host_values(c[:, 1], dtype)
+        assert np.array_equal(got_k, qh[:, :, :, 1].transpose(1, 2, 3, 0, 4))
+        assert np.array_equal(got_v, qh[:, :, :, 2].transpose(1, 2, 3, 0, 4))
+        caches = [c[l].reshape(-1) for l in range(L)]
+        cache_vals = [_host_values(x, dtype) for x in caches]
+    else:
+        fmt = oracle.W8_FP8_E4M3 if dtype == "fp8" else oracle.W8_INT8
+        codes = eng.cache.cpu().numpy()
+        scales = eng.scale.cpu().numpy()
+        n_sc = 2 * B * NH * maxT
+        cache_vals = []
+        for l in range(L):
+            ref_codes = np.zeros(eng.n_cache, dtype=np.uint8)
+            ref_scales = np.zeros(n_sc, dtype=np.float32)
+            for j in range(maxT):
+                oracle.cache_write_w8(ref_codes, ref_scales, qh[j, l].reshape(-1), [j] * B, B, NH, HS, maxT, fmt)
+            lc = codes[l * eng.n_cache:(l + 1) * eng.n_cache]
+            ls = scales[l * n_sc:(l + 1) * n_sc]
+            assert np.array_equal(lc, ref_codes), f"layer {l} codes"
+            assert np.array_equal(ls.view(np.uint32), ref_scales.view(np.uint32)), f"layer {l} scales"
+            cache_vals.append(oracle.dequant_w8(ref_codes, ref_scales, B, NH, HS, maxT, fmt))
+    for total, out in hist.items():
+        o = out.float().cpu().numpy()
+        for l in range(L):
+            ref = oracle.attention_f32(qh[total - 1, l].reshape(-1), cache_vals[l], np.full(B, total, np.int32),
+                                       B, NH, HS, maxT)
+            assert_close(o[l], ref, dtype, f"{mode} layer {l} T={total}")

@@ -29,8 +29,23 @@ def test_auto_gpt2_layer_is_single_launch_split():
 
 
 def test_auto_large_batch_streams_with_split_merge():
-    st, slots, rows = kvattn.plan(64, 12, 64, 8192, kv_dtype="bf16")
+    st, slots, rows = kvattn.plan(64, 12, 64, 8192, kv_dtype="bf16", len_hint=8191)
     assert (st, slots, rows) == (kvattn.SPLIT_MERGE, 16, 512)
+
+
+def test_auto_without_hint_plans_on_the_device():
+    # No length hint (a graph replayed at every length): the kernels pick the rows per
+    # segment from the device length; the grid holds the most segments any length needs.
+    assert kvattn.plan(1, 12, 64, 1024, kv_dtype="bf16") == (kvattn.SPLIT_LASTBLOCK, 4, -1)
+    assert kvattn.plan(1, 12, 64, 300, kv_dtype="bf16") == (kvattn.SPLIT_LASTBLOCK, 4, -1)
+    assert kvattn.plan(64, 12, 64, 8192, kv_dtype="bf16") == (kvattn.SPLIT_MERGE, 16, -1)
+    assert kvattn.plan(1, 12, 64, 20000, kv_dtype="fp8", strategy="lastblock") == (kvattn.SPLIT_LASTBLOCK, 40, -1)
+    # Every length fits fused_single: no split at all.
+    assert kvattn.plan(1, 12, 64, 256, kv_dtype="bf16") == (kvattn.FUSED_SINGLE, 1, 0)
+    # An explicit partition keeps its meaning without a hint.
+    assert kvattn.plan(1, 12, 64, 1024, kv_dtype="bf16", S=8, strategy="split_merge") == (kvattn.SPLIT_MERGE, 8, 0)
+    assert kvattn.plan(1, 12, 64, 1024, kv_dtype="bf16", S=-128, strategy="lastblock") == \
+        (kvattn.SPLIT_LASTBLOCK, 8, 128)
 
 
 def test_auto_skips_fused_single_when_scores_exceed_lds():
