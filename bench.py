@@ -160,6 +160,8 @@ class C2:
         Graphs (12 layers each):
           one_graph     per layer append + AUTO attention with no length hint (segmentation
                         planned on the device), captured once;
+          fused         the same with append and attention in one launch per layer
+                        (kvattn_append_decode);
           graph_pair    the reference's pair: append + fused_single below 150 positions,
                         append + split + merge with S = 8 from 150 on (host switch per token);
           attn_only     AUTO attention with no hint, without the append.
@@ -168,9 +170,13 @@ class C2:
         ws = kvattn.Workspace(self.B, self.NH, self.maxT, 0)
         ws8 = kvattn.Workspace(self.B, self.NH, self.maxT, 8)
 
-        def capture(strategy, S, append, w):
+        def capture(strategy, S, append, w, fused=False):
             def step():
                 for l in range(self.L):
+                    if fused:
+                        kvattn.append_decode(self.outs[l], self.qkvs[l], self.caches[l], self.B, self.NH, HD,
+                                             self.maxT, kv_dtype="bf16", cur_len=self.cur, **w.kwargs())
+                        continue
                     if append:
                         kvattn.kv_cache_write(self.caches[l], self.qkvs[l], self.B, self.NH, HD, self.maxT,
                                               kv_dtype="bf16", cur_len=self.cur)
@@ -185,9 +191,11 @@ class C2:
             return graph
 
         one = capture("auto", 0, True, ws)
+        fused = capture("auto", 0, True, ws, fused=True)
         small, large = capture("fused_single", 0, True, ws), capture("split_merge", 8, True, ws8)
         attn = capture("auto", 0, False, ws)
-        modes = {"one_graph": lambda t: one, "graph_pair": lambda t: small if t < 150 else large,
+        modes = {"one_graph": lambda t: one, "fused": lambda t: fused,
+                 "graph_pair": lambda t: small if t < 150 else large,
                  "attn_only": lambda t: attn}
         res = {"tokens": self.maxT}
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

@@ -130,6 +130,24 @@ __device__ __forceinline__ uint8_t f32_to_e4m3_sat(float y) {
     return (uint8_t)(sign | code);
 }
 
+// 8-bit row quantisation of the append: scale = amax / limit (IEEE division), code of
+// x / scale (INT8: round half to even, clamp to +-127; FP8: saturating E4M3), and zero
+// codes when the scale is not positive (an all-zero row).
+template <int DT> constexpr float kW8Limit = DT == KVATTN_KV_FP8_E4M3 ? 448.0f : 127.0f;
+
+template <int DT>
+__device__ __forceinline__ uint8_t w8_code(float x, float scale) {
+    if (!(scale > 0.0f)) return 0;
+    const float y = x / scale;
+    if constexpr (DT == KVATTN_KV_FP8_E4M3) {
+        return f32_to_e4m3_sat(y);
+    } else {
+        int qv = (int)rintf(y);
+        qv = qv < -127 ? -127 : (qv > 127 ? 127 : qv);
+        return (uint8_t)(int8_t)qv;
+    }
+}
+
 // 16-byte row-chunk load; KVATTN_NT_LOADS=1 marks K/V loads non-temporal (streamed once).
 #ifndef KVATTN_NT_LOADS
 #define KVATTN_NT_LOADS 1
@@ -330,6 +348,109 @@ __device__ __forceinline__ Slot make_slot(const uint8_t* kv, const float* kv_sca
 }
 
 // ------------------------------------------------------------------------------------
+// The current token's K and V rows, for the kernels that append and attend in one launch.
+// Every lane loads its own channel slice from qkv (like q); the slice is brought to the
+// cache format (8-bit: row amax over the 4 lanes of the row, then the append's
+// quantisation), written to column cur_len by one row group of the owning workgroup, and
+// substituted for the cache row in the tile that holds position cur_len, so no workgroup
+// reads that cache row.
+// ------------------------------------------------------------------------------------
+template <int DT> struct FreshRaw {
+    uint4 k[Row<DT>::k8bit ? 2 : 1], v[Row<DT>::k8bit ? 2 : 1];
+};
+template <int DT> struct Fresh {
+    uint4 k, v;        // this lane's 16-byte slice of the K and V rows, cache format
+    float ks, vs;      // 8-bit row scales
+};
+
+template <int DT>
+__device__ __forceinline__ FreshRaw<DT> load_fresh(const void* qkv, int b, int h, int NH, int slice) {
+    constexpr int kActBytes = Row<DT>::kActF32 ? 4 : 2;
+    constexpr int kN = Row<DT>::k8bit ? 2 : 1;
+    const uint8_t* base = reinterpret_cast<const uint8_t*>(qkv);
+    const size_t off = (size_t)slice * Row<DT>::kElems * kActBytes;
+    const uint4* pk = reinterpret_cast<const uint4*>(base + (((size_t)b * 3 + 1) * NH + h) * kHeadDim * kActBytes + off);
+    const uint4* pv = reinterpret_cast<const uint4*>(base + (((size_t)b * 3 + 2) * NH + h) * kHeadDim * kActBytes + off);
+    FreshRaw<DT> r;
+#pragma unroll
+    for (int i = 0; i < kN; ++i) { r.k[i] = pk[i]; r.v[i] = pv[i]; }
+    return r;
+}
+
+// 16 bf16 channels -> 16 codes of one row whose other 48 channels sit in the other three
+// lanes of this lane's quad.
+template <int DT>
+__device__ __forceinline__ uint4 quantise_slice(const uint4 (&w)[2], float& scale) {
+    float x[16];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t u[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            x[8 * i + 2 * k] = bf16_lo(u[k]);
+            x[8 * i + 2 * k + 1] = bf16_hi(u[k]);
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) amax = fmaxf(amax, fabsf(x[e]));
+    amax = fmaxf(amax, dpp<kDppQuadXor1>(amax));
+    amax = fmaxf(amax, dpp<kDppQuadXor2>(amax));
+    scale = amax / kW8Limit<DT>;
+    uint32_t c[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        c[i] = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) c[i] |= (uint32_t)w8_code<DT>(x[4 * i + k], scale) << (8 * k);
+    }
+    return make_uint4(c[0], c[1], c[2], c[3]);
+}
+
+template <int DT>
+__device__ __forceinline__ Fresh<DT> finish_fresh(const FreshRaw<DT>& r) {
+    Fresh<DT> f;
+    if constexpr (Row<DT>::k8bit) {
+        f.k = quantise_slice<DT>(r.k, f.ks);
+        f.v = quantise_slice<DT>(r.v, f.vs);
+    } else {
+        f.k = r.k[0];
+        f.v = r.v[0];
+        f.ks = f.vs = 0.0f;
+    }
+    return f;
+}
+
+// Where the fresh row goes: column `cur` of slot bh.
+struct FreshDst {
+    uint8_t* kv;
+    float* kv_scale;
+    size_t rk, rv;     // cache row indices of the K and V rows
+    int slice;
+};
+
+__device__ __forceinline__ FreshDst fresh_dst(uint8_t* kv, float* kv_scale, int B, int NH, int maxT, int bh,
+                                              int slice, int cur) {
+    FreshDst d;
+    d.kv = kv;
+    d.kv_scale = kv_scale;
+    d.rk = (size_t)bh * maxT + cur;
+    d.rv = (size_t)B * NH * maxT + d.rk;
+    d.slice = slice;
+    return d;
+}
+
+// This lane's K and V slices of the row, and (slice 0) the row scales.
+template <int DT>
+__device__ __forceinline__ void store_fresh(const FreshDst& d, const Fresh<DT>& f) {
+    *reinterpret_cast<uint4*>(d.kv + d.rk * Row<DT>::kBytes + d.slice * 16) = f.k;
+    *reinterpret_cast<uint4*>(d.kv + d.rv * Row<DT>::kBytes + d.slice * 16) = f.v;
+    if constexpr (Row<DT>::k8bit) {
+        if (d.slice == 0) { d.kv_scale[d.rk] = f.ks; d.kv_scale[d.rv] = f.vs; }
+    }
+}
+
+// ------------------------------------------------------------------------------------
 // Online softmax over rows [r0, r1) of a slot by one wave.  Each group of kLanes lanes
 // owns one row per load instruction and keeps its own running (m, l, acc) in base-2
 // units; the groups are combined later.  A tile holds U K and U V row chunks per lane,
@@ -356,6 +477,24 @@ __device__ __forceinline__ void load_tile(Tile<DT, U>& t, const Slot& sl, int r,
             t.k[u] = make_uint4(0u, 0u, 0u, 0u);
             t.v[u] = make_uint4(0u, 0u, 0u, 0u);
             if constexpr (R::k8bit) { t.ks[u] = 0.0f; t.vs[u] = 0.0f; }
+        }
+    }
+}
+
+// In a tile whose rows start at r: the lanes holding row `cur` take the fresh row in place
+// of what they loaded from the cache and write it to the cache.
+template <int DT, int U>
+__device__ __forceinline__ void patch_tile(Tile<DT, U>& t, const FreshRaw<DT>& fr, const FreshDst& d, int r,
+                                           int slot_row, int cur) {
+    constexpr int kRPL = kRowsPerLoad<DT>;
+    const Fresh<DT> f = finish_fresh<DT>(fr);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        if (r + u * kRPL + slot_row == cur) {
+            t.k[u] = f.k;
+            t.v[u] = f.v;
+            if constexpr (Row<DT>::k8bit) { t.ks[u] = f.ks; t.vs[u] = f.vs; }
+            store_fresh<DT>(d, f);
         }
     }
 }
@@ -395,24 +534,31 @@ __device__ __forceinline__ void consume_tile(const Tile<DT, U>& t, int r, int r1
 // Online softmax over rows [r0, r1) of a slot by one wave, given the first tile (rows
 // [r0, r0 + kTile) clipped to a bound >= r1) and this lane's q slice already requested;
 // rows of that tile at or beyond r1 are masked.  The q slice is requested after the tile's
-// K/V loads, so nothing that depends on q is scheduled ahead of them.
-template <int DT, int kU>
-__device__ __forceinline__ void online_rows_from(const Tile<DT, kU>& t0, const QRaw<DT>& qr,
+// K/V loads, so nothing that depends on q is scheduled ahead of them.  kFresh: the row
+// `cur` (if inside [r0, r1)) is taken from f instead of the cache.
+template <int DT, int kU, bool kFresh>
+__device__ __forceinline__ void online_rows_from(Tile<DT, kU>& t0, const QRaw<DT>& qr,
                                                  const Slot& sl, int r0, int r1, int slot_row, float qscale,
+                                                 const FreshRaw<DT>& fr, const FreshDst& fd, int cur,
                                                  float& m, float& l, float (&acc)[Row<DT>::kElems]) {
     constexpr int kTile = kRowsPerLoad<DT> * kU;
     if (r0 >= r1) return;
     float q[Row<DT>::kElems];
     convert_q<DT>(qr, qscale, q);
+    // Only the wave whose rows [r, min(r + kTile, r1)) contain cur patches (and stores).
+    auto holds = [&](int r) { return kFresh && cur >= r && cur < min(r + kTile, r1); };
+    if (holds(r0)) patch_tile<DT, kU>(t0, fr, fd, r0, slot_row, cur);
     consume_tile<DT, kU, true>(t0, r0, r1, slot_row, q, m, l, acc);
     Tile<DT, kU> t;
     int r = r0 + kTile;
     for (; r + kTile <= r1; r += kTile) {
         load_tile<DT, kU, false>(t, sl, r, r1, slot_row);
+        if (holds(r)) patch_tile<DT, kU>(t, fr, fd, r, slot_row, cur);
         consume_tile<DT, kU, false>(t, r, r1, slot_row, q, m, l, acc);
     }
     if (r < r1) {
         load_tile<DT, kU, true>(t, sl, r, r1, slot_row);
+        if (holds(r)) patch_tile<DT, kU>(t, fr, fd, r, slot_row, cur);
         consume_tile<DT, kU, true>(t, r, r1, slot_row, q, m, l, acc);
     }
 }
@@ -421,9 +567,10 @@ __device__ __forceinline__ void online_rows_from(const Tile<DT, kU>& t0, const Q
 // fused_single: one workgroup per (b,h), grid B*NH.  Pass 1 writes every score to LDS
 // and finds the exact maximum; pass 2 weights V with exp2(score - max).
 // ------------------------------------------------------------------------------------
-template <int DT, int U, bool kChecked>
+template <int DT, int U, bool kChecked, bool kFresh>
 __device__ __forceinline__ void score_tile(const Slot& sl, int r, int total, int slot_row, int slice,
-                                           const float (&q)[Row<DT>::kElems], float* scores, float& mloc) {
+                                           const float (&q)[Row<DT>::kElems], float* scores, float& mloc,
+                                           const FreshRaw<DT>& fr, const FreshDst& fd) {
     using R = Row<DT>;
     constexpr int kRPL = kRowsPerLoad<DT>;
     uint4 kd[U];
@@ -439,6 +586,19 @@ __device__ __forceinline__ void score_tile(const Slot& sl, int r, int total, int
             if constexpr (R::k8bit) ks[u] = 0.0f;
         }
     }
+    // The fresh row (position total - 1) replaces the cache row and is written out here.
+    const int cur = total - 1;
+    if (kFresh && cur >= r && cur < r + U * kRPL) {
+        const Fresh<DT> f = finish_fresh<DT>(fr);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (r + u * kRPL + slot_row == cur) {
+                kd[u] = f.k;
+                if constexpr (R::k8bit) ks[u] = f.ks;
+                store_fresh<DT>(fd, f);
+            }
+        }
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         float s = row_sum<R::kLanes>(dot_chunk<DT>(q, kd[u]));
@@ -451,9 +611,10 @@ __device__ __forceinline__ void score_tile(const Slot& sl, int r, int total, int
     }
 }
 
-template <int DT, int U, bool kChecked>
+template <int DT, int U, bool kChecked, bool kFresh>
 __device__ __forceinline__ void weight_tile(const Slot& sl, int r, int total, int slot_row, float M,
-                                            const float* scores, float& l, float (&acc)[Row<DT>::kElems]) {
+                                            const float* scores, float& l, float (&acc)[Row<DT>::kElems],
+                                            const FreshRaw<DT>& fr) {
     using R = Row<DT>;
     constexpr int kRPL = kRowsPerLoad<DT>;
     uint4 vd[U];
@@ -467,6 +628,17 @@ __device__ __forceinline__ void weight_tile(const Slot& sl, int r, int total, in
         } else {
             vd[u] = make_uint4(0u, 0u, 0u, 0u);
             if constexpr (R::k8bit) vs[u] = 0.0f;
+        }
+    }
+    const int cur = total - 1;
+    if (kFresh && cur >= r && cur < r + U * kRPL) {
+        const Fresh<DT> f = finish_fresh<DT>(fr);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (r + u * kRPL + slot_row == cur) {
+                vd[u] = f.v;
+                if constexpr (R::k8bit) vs[u] = f.vs;
+            }
         }
     }
 #pragma unroll
@@ -484,11 +656,13 @@ __device__ __forceinline__ void weight_tile(const Slot& sl, int r, int total, in
     }
 }
 
-template <int DT, int kThreads, int kU>
+// kFresh: append and attend in one launch; kv_out / kv_scale_out receive the current
+// token's row (they alias kv / kv_scale, whose row cur_len is then never used).
+template <int DT, int kThreads, int kU, bool kFresh>
 __global__ __launch_bounds__(kThreads) void fused_single_kernel(
-    void* __restrict__ out, const void* __restrict__ qkv, const uint8_t* __restrict__ kv,
-    const float* __restrict__ kv_scale, const int* __restrict__ cur_len, int lens_per_seq,
-    int B, int NH, int maxT, int spec_rows, float qscale) {
+    void* __restrict__ out, const void* __restrict__ qkv, const uint8_t* kv,
+    const float* kv_scale, uint8_t* kv_out, float* kv_scale_out, const int* __restrict__ cur_len,
+    int lens_per_seq, int B, int NH, int maxT, int spec_rows, float qscale) {
     using R = Row<DT>;
     constexpr int kW = kThreads / kWave;
     constexpr int kRPL = kRowsPerLoad<DT>;
@@ -513,7 +687,12 @@ __global__ __launch_bounds__(kThreads) void fused_single_kernel(
         load_tile<DT, kU, true>(t, sl, wave * kTile, spec_lim, slot_row);
         qr = load_q<DT>(qkv, b, h, NH, slice);
     }
+    FreshRaw<DT> fr{};
+    if constexpr (kFresh) fr = load_fresh<DT>(qkv, b, h, NH, slice);
     const int total = seq_total(cur_len, lens_per_seq, b, maxT);
+    const int cur = total - 1;
+    FreshDst fd{};
+    if constexpr (kFresh) fd = fresh_dst(kv_out, kv_scale_out, B, NH, maxT, bh, slice, cur);
     float q[R::kElems];
 
     float l = 0.0f, acc[R::kElems];
@@ -529,6 +708,7 @@ __global__ __launch_bounds__(kThreads) void fused_single_kernel(
             qr = load_q<DT>(qkv, b, h, NH, slice);
         }
         convert_q<DT>(qr, qscale, q);
+        if (kFresh && cur >= r && cur < r + kTile) patch_tile<DT, kU>(t, fr, fd, r, slot_row, cur);
         float s[kU];
         float mloc = kStartMax;
 #pragma unroll
@@ -561,9 +741,9 @@ __global__ __launch_bounds__(kThreads) void fused_single_kernel(
         float mloc = kStartMax;
         const int full = total / kTile * kTile;
         for (int r = wave * kTile; r < full; r += kW * kTile)
-            score_tile<DT, kU, false>(sl, r, total, slot_row, slice, q, s_scores, mloc);
+            score_tile<DT, kU, false, kFresh>(sl, r, total, slot_row, slice, q, s_scores, mloc, fr, fd);
         for (int r = full + wave * kTile; r < total; r += kW * kTile)
-            score_tile<DT, kU, true>(sl, r, total, slot_row, slice, q, s_scores, mloc);
+            score_tile<DT, kU, true, kFresh>(sl, r, total, slot_row, slice, q, s_scores, mloc, fr, fd);
         mloc = wave_max(mloc);
         if (lane == 0) s_max[wave] = mloc;
         __syncthreads();
@@ -572,9 +752,9 @@ __global__ __launch_bounds__(kThreads) void fused_single_kernel(
         for (int w = 1; w < kW; ++w) M = fmaxf(M, s_max[w]);
         // Pass 2: V rows weighted by exp2(score - M).
         for (int r = wave * kTile; r < full; r += kW * kTile)
-            weight_tile<DT, kU, false>(sl, r, total, slot_row, M, s_scores, l, acc);
+            weight_tile<DT, kU, false, kFresh>(sl, r, total, slot_row, M, s_scores, l, acc, fr);
         for (int r = full + wave * kTile; r < total; r += kW * kTile)
-            weight_tile<DT, kU, true>(sl, r, total, slot_row, M, s_scores, l, acc);
+            weight_tile<DT, kU, true, kFresh>(sl, r, total, slot_row, M, s_scores, l, acc, fr);
     }
 
     l = slot_reduce<R::kLanes, false>(l);
@@ -609,6 +789,8 @@ struct SplitArgs {
     const void* qkv;
     const uint8_t* kv;
     const float* kv_scale;
+    uint8_t* kv_out;        // append-and-attend launches: where the current row goes
+    float* kv_scale_out;
     const int* cur_len;
     int lens_per_seq;
     int B, NH, maxT;
@@ -763,7 +945,9 @@ __device__ __forceinline__ void merge_partials(void* out, const float* part_out,
 #define KVATTN_STREAM_MIN_BLOCKS 1
 #endif
 
-template <int DT, int kMode, int kW, int kU>
+// kFresh: append and attend in one launch (the workgroup whose segment holds position
+// cur_len takes that row from qkv and writes it to the cache).
+template <int DT, int kMode, int kW, int kU, bool kFresh>
 __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS : 1) void split_kernel(SplitArgs a) {
     using R = Row<DT>;
     __shared__ float s_m[kW];
@@ -782,6 +966,7 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
     // the same first tile is requested once the length is known.
     Tile<DT, kU> t0;
     QRaw<DT> q0;
+    FreshRaw<DT> fr{};
     bool spec = false;
     int w0 = 0, w1 = 0;
     if (!a.lens_per_seq && a.seg_rows > 0) {
@@ -796,6 +981,7 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
             const Slot sl0 = make_slot<DT>(a.kv, a.kv_scale, a.B, a.NH, a.maxT, bh0, slice);
             load_tile<DT, kU, true>(t0, sl0, w0, w1, slot_row);
             q0 = load_q<DT>(a.qkv, b0, bh0 - b0 * a.NH, a.NH, slice);
+            if constexpr (kFresh) fr = load_fresh<DT>(a.qkv, b0, bh0 - b0 * a.NH, a.NH, slice);
             spec = true;
         }
     }
@@ -835,11 +1021,15 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                 w1 = min(w0 + per_wave, j1);
                 load_tile<DT, kU, true>(t0, sl, w0, w1, slot_row);
                 q0 = load_q<DT>(a.qkv, it.b, it.h, a.NH, slice);
+                if constexpr (kFresh) fr = load_fresh<DT>(a.qkv, it.b, it.h, a.NH, slice);
             }
+            const int cur = it.total - 1;
+            FreshDst fd{};
+            if constexpr (kFresh) fd = fresh_dst(a.kv_out, a.kv_scale_out, a.B, a.NH, a.maxT, bh, slice, cur);
             float m = kStartMax, l = 0.0f, acc[R::kElems];
 #pragma unroll
             for (int e = 0; e < R::kElems; ++e) acc[e] = 0.0f;
-            online_rows_from<DT, kU>(t0, q0, sl, w0, w1, slot_row, a.qscale, m, l, acc);
+            online_rows_from<DT, kU, kFresh>(t0, q0, sl, w0, w1, slot_row, a.qscale, fr, fd, cur, m, l, acc);
 
             // Combine the row slots of this wave, then the 4 waves.
             const float mw = slot_reduce<R::kLanes, true>(m);
@@ -949,19 +1139,8 @@ __global__ __launch_bounds__(kBlock) void cache_write_w8_kernel(uint8_t* __restr
     const int cl = seq_total(cur_len, lens_per_seq, b, maxT) - 1;
     const float x = bf16_to_f32(qkv[(((size_t)b * 3 + 1 + is_v) * NH + h) * kHeadDim + c]);
     const float amax = wave_max(fabsf(x));
-    const float limit = DT == KVATTN_KV_FP8_E4M3 ? 448.0f : 127.0f;
-    const float scale = amax / limit;
-    uint8_t code = 0;
-    if (scale > 0.0f) {
-        const float y = x / scale;
-        if constexpr (DT == KVATTN_KV_FP8_E4M3) {
-            code = f32_to_e4m3_sat(y);
-        } else {
-            int qv = (int)rintf(y);
-            qv = qv < -127 ? -127 : (qv > 127 ? 127 : qv);
-            code = (uint8_t)(int8_t)qv;
-        }
-    }
+    const float scale = amax / kW8Limit<DT>;
+    const uint8_t code = w8_code<DT>(x, scale);
     const size_t r = (size_t)is_v * B * NH * maxT + (size_t)kh * maxT + cl;
     kv[r * kHeadDim + c] = code;
     if (c == 0) kv_scale[r] = scale;
@@ -1042,52 +1221,63 @@ int dispatch_dtype(int dt, F&& f) {
     }
 }
 
-int launch_fused_single(void* out, const void* qkv, const void* kv, const float* kv_scale, int B, int NH,
-                        int maxT, const int* cur_len, int lens_per_seq, int spec_rows, int kv_dtype,
-                        hipStream_t stream) {
+// kv_out == nullptr: attention only.  Otherwise the kernel also appends the current
+// token's row into kv_out / kv_scale_out (the same cache as kv / kv_scale).
+int launch_fused_single(void* out, const void* qkv, const void* kv, const float* kv_scale, void* kv_out,
+                        float* kv_scale_out, int B, int NH, int maxT, const int* cur_len, int lens_per_seq,
+                        int spec_rows, int kv_dtype, hipStream_t stream) {
     const size_t lds = (size_t)maxT * sizeof(float);
     if (lds > kFusedMaxLds) return KVATTN_ERR_LDS;
     const float qs = qscale_for(kHeadDim);
     return dispatch_dtype(kv_dtype, [&](auto dtc) -> int {
         constexpr int DT = decltype(dtc)::value;
         constexpr int kThreads = kWavesLat * kWave;
-        hipLaunchKernelGGL((fused_single_kernel<DT, kThreads, kUnrollLat<DT>>), dim3(B * NH), dim3(kThreads), lds,
-                           stream, out, qkv,
-                           (const uint8_t*)kv, kv_scale, cur_len, lens_per_seq, B, NH, maxT, spec_rows, qs);
+        if (kv_out)
+            hipLaunchKernelGGL((fused_single_kernel<DT, kThreads, kUnrollLat<DT>, true>), dim3(B * NH),
+                               dim3(kThreads), lds, stream, out, qkv, (const uint8_t*)kv, kv_scale,
+                               (uint8_t*)kv_out, kv_scale_out, cur_len, lens_per_seq, B, NH, maxT, spec_rows, qs);
+        else
+            hipLaunchKernelGGL((fused_single_kernel<DT, kThreads, kUnrollLat<DT>, false>), dim3(B * NH),
+                               dim3(kThreads), lds, stream, out, qkv, (const uint8_t*)kv, kv_scale,
+                               (uint8_t*)nullptr, (float*)nullptr, cur_len, lens_per_seq, B, NH, maxT, spec_rows,
+                               qs);
         KV_HIP(hipGetLastError());
         return KVATTN_OK;
     });
 }
 
-// Split kernel instance for a mode and a shape: 16-wave workgroups with short tiles for
-// latency-bound calls (`lat`), 4-wave workgroups with deep tiles for streaming calls.
+// Split kernel instance for a mode, a shape (`lat`: the latency shape, else the streaming
+// shape) and whether the launch also appends the current row.
+template <int DT, int W, int U, bool kFresh>
+const void* split_ptr_mode(int mode) {
+    if (mode == kPartialsOnly) return (const void*)&split_kernel<DT, kPartialsOnly, W, U, kFresh>;
+    if (mode == kLastBlockMerge) return (const void*)&split_kernel<DT, kLastBlockMerge, W, U, kFresh>;
+    return (const void*)&split_kernel<DT, kCoopMerge, W, U, kFresh>;
+}
+
 template <int DT>
-const void* split_ptr(int mode, bool lat) {
+const void* split_ptr(int mode, bool lat, bool fresh) {
     if (lat) {
-        constexpr int W = kWavesLat, U = kUnrollLat<DT>;
-        if (mode == kPartialsOnly) return (const void*)&split_kernel<DT, kPartialsOnly, W, U>;
-        if (mode == kLastBlockMerge) return (const void*)&split_kernel<DT, kLastBlockMerge, W, U>;
-        return (const void*)&split_kernel<DT, kCoopMerge, W, U>;
+        return fresh ? split_ptr_mode<DT, kWavesLat, kUnrollLat<DT>, true>(mode)
+                     : split_ptr_mode<DT, kWavesLat, kUnrollLat<DT>, false>(mode);
     }
-    constexpr int W = kWaves, U = kUnroll<DT>;
-    if (mode == kPartialsOnly) return (const void*)&split_kernel<DT, kPartialsOnly, W, U>;
-    if (mode == kLastBlockMerge) return (const void*)&split_kernel<DT, kLastBlockMerge, W, U>;
-    return (const void*)&split_kernel<DT, kCoopMerge, W, U>;
+    return fresh ? split_ptr_mode<DT, kWaves, kUnroll<DT>, true>(mode)
+                 : split_ptr_mode<DT, kWaves, kUnroll<DT>, false>(mode);
 }
 
 int split_threads(bool lat) { return (lat ? kWavesLat : kWaves) * kWave; }
 
-const void* split_ptr_dt(int kv_dtype, int mode, bool lat) {
+const void* split_ptr_dt(int kv_dtype, int mode, bool lat, bool fresh) {
     const void* fn = nullptr;
     dispatch_dtype(kv_dtype, [&](auto dtc) -> int {
-        fn = split_ptr<decltype(dtc)::value>(mode, lat);
+        fn = split_ptr<decltype(dtc)::value>(mode, lat, fresh);
         return KVATTN_OK;
     });
     return fn;
 }
 
 int launch_split(const SplitArgs& a, int kv_dtype, int mode, bool lat, hipStream_t stream) {
-    const void* fn = split_ptr_dt(kv_dtype, mode, lat);
+    const void* fn = split_ptr_dt(kv_dtype, mode, lat, a.kv_out != nullptr);
     if (!fn) return KVATTN_ERR_DTYPE;
     SplitArgs args = a;
     void* params[] = {&args};
@@ -1126,7 +1316,7 @@ int launch_coop(const SplitArgs& a, int kv_dtype, bool lat, hipStream_t stream) 
     for (int attempt = 0; attempt < 2; ++attempt) {
         const bool use_lat = lat && attempt == 0;
         if (attempt == 1 && !lat) break;
-        const void* fn = split_ptr_dt(kv_dtype, kCoopMerge, use_lat);
+        const void* fn = split_ptr_dt(kv_dtype, kCoopMerge, use_lat, a.kv_out != nullptr);
         if (!fn) return KVATTN_ERR_DTYPE;
         const int threads = split_threads(use_lat);
         int per_cu = 0;
@@ -1143,12 +1333,13 @@ int launch_coop(const SplitArgs& a, int kv_dtype, bool lat, hipStream_t stream) 
 // hipGraph holding the split and merge kernel nodes, built once per argument set.
 struct GraphKey {
     int dev, dt, lat;
-    const void *out, *qkv, *kv, *ks, *len, *po, *pl, *pm;
+    const void *out, *qkv, *kv, *ks, *kv_out, *len, *po, *pl, *pm;
     int lens_per_seq, B, NH, maxT, S, seg_rows;
     bool operator<(const GraphKey& o) const {
-        return std::tie(dev, dt, lat, out, qkv, kv, ks, len, po, pl, pm, lens_per_seq, B, NH, maxT, S, seg_rows) <
-               std::tie(o.dev, o.dt, o.lat, o.out, o.qkv, o.kv, o.ks, o.len, o.po, o.pl, o.pm, o.lens_per_seq, o.B,
-                        o.NH, o.maxT, o.S, o.seg_rows);
+        return std::tie(dev, dt, lat, out, qkv, kv, ks, kv_out, len, po, pl, pm, lens_per_seq, B, NH, maxT, S,
+                        seg_rows) <
+               std::tie(o.dev, o.dt, o.lat, o.out, o.qkv, o.kv, o.ks, o.kv_out, o.len, o.po, o.pl, o.pm,
+                        o.lens_per_seq, o.B, o.NH, o.maxT, o.S, o.seg_rows);
     }
 };
 
@@ -1162,8 +1353,8 @@ int launch_graph_pair(const SplitArgs& a, int kv_dtype, bool lat, hipStream_t st
     }
     int dev = 0;
     KV_HIP(hipGetDevice(&dev));
-    GraphKey key{dev, kv_dtype, lat ? 1 : 0, a.out, a.qkv, a.kv, a.kv_scale, a.cur_len, a.part_out, a.part_lse, a.part_max,
-                 a.lens_per_seq, a.B, a.NH, a.maxT, a.S, a.seg_rows};
+    GraphKey key{dev, kv_dtype, lat ? 1 : 0, a.out, a.qkv, a.kv, a.kv_scale, a.kv_out, a.cur_len, a.part_out,
+                 a.part_lse, a.part_max, a.lens_per_seq, a.B, a.NH, a.maxT, a.S, a.seg_rows};
     static std::mutex mu;
     static std::map<GraphKey, hipGraphExec_t> cache;
     std::lock_guard<std::mutex> lock(mu);
@@ -1173,7 +1364,7 @@ int launch_graph_pair(const SplitArgs& a, int kv_dtype, bool lat, hipStream_t st
             for (auto& kvp : cache) (void)hipGraphExecDestroy(kvp.second);
             cache.clear();
         }
-        void* fsplit = const_cast<void*>(split_ptr_dt(kv_dtype, kPartialsOnly, lat));
+        void* fsplit = const_cast<void*>(split_ptr_dt(kv_dtype, kPartialsOnly, lat, a.kv_out != nullptr));
         void* fmerge = nullptr;
         dispatch_dtype(kv_dtype, [&](auto dtc) -> int {
             fmerge = (void*)&merge_kernel<decltype(dtc)::value>;
@@ -1318,9 +1509,10 @@ int make_plan(int B, int NH, int maxT, int len_hint, int S, int strategy, Plan& 
     return KVATTN_OK;
 }
 
+// append == true: the launch also writes the current token's K/V row (kvattn_append_decode).
 int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scale, int B, int NH, int hs,
                 int maxT, const int* d_cur_len, int lens_per_seq, int len_hint, void* workspace,
-                size_t workspace_bytes, int S, int strategy, int kv_dtype, void* stream_v) {
+                size_t workspace_bytes, int S, int strategy, int kv_dtype, void* stream_v, bool append) {
     KV_TRY(check_common(qkv, kv, kv_scale, B, NH, hs, maxT, kv_dtype));
     if (!out) return KVATTN_ERR_NULL_POINTER;
     if (!aligned16(out)) return KVATTN_ERR_MISALIGNED;
@@ -1330,8 +1522,10 @@ int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scal
 
     if (plan.strategy == KVATTN_FUSED_SINGLE) {
         KV_TRY(resolve_len(d_cur_len));
-        return launch_fused_single(out, qkv, kv, kv_scale, B, NH, maxT, d_cur_len, lens_per_seq,
-                                   (lens_per_seq || len_hint < 0) ? 0 : len_hint + 1, kv_dtype, stream);
+        return launch_fused_single(out, qkv, kv, kv_scale, append ? const_cast<void*>(kv) : nullptr,
+                                   append ? const_cast<float*>(kv_scale) : nullptr, B, NH, maxT, d_cur_len,
+                                   lens_per_seq, (lens_per_seq || len_hint < 0) ? 0 : len_hint + 1, kv_dtype,
+                                   stream);
     }
 
     if (!workspace) return KVATTN_ERR_WORKSPACE;
@@ -1349,6 +1543,8 @@ int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scal
     a.qkv = qkv;
     a.kv = (const uint8_t*)kv;
     a.kv_scale = kv_scale;
+    a.kv_out = append ? (uint8_t*)const_cast<void*>(kv) : nullptr;
+    a.kv_scale_out = append ? const_cast<float*>(kv_scale) : nullptr;
     a.cur_len = d_cur_len;
     a.lens_per_seq = lens_per_seq ? 1 : 0;
     a.B = B;
@@ -1480,8 +1676,8 @@ int kvattn_forward_small(void* out, const void* qkv, const void* kv_cache, const
     if (!out) return KVATTN_ERR_NULL_POINTER;
     if (!aligned16(out)) return KVATTN_ERR_MISALIGNED;
     KV_TRY(resolve_len(d_cur_len));
-    return launch_fused_single(out, qkv, kv_cache, kv_scale, B, NH, maxT, d_cur_len, lens_per_seq, 0, kv_dtype,
-                               (hipStream_t)stream);
+    return launch_fused_single(out, qkv, kv_cache, kv_scale, nullptr, nullptr, B, NH, maxT, d_cur_len,
+                               lens_per_seq, 0, kv_dtype, (hipStream_t)stream);
 }
 
 int kvattn_forward_large(void* out, const void* qkv, const void* kv_cache, const float* kv_scale, int B, int NH,
@@ -1561,7 +1757,14 @@ int kvattn_decode(void* out, const void* qkv, const void* kv_cache, const float*
                   int maxT, const int* d_cur_len, int lens_per_seq, int len_hint, void* workspace,
                   size_t workspace_bytes, int S, int strategy, int kv_dtype, void* stream) {
     return decode_impl(out, qkv, kv_cache, kv_scale, B, NH, hs, maxT, d_cur_len, lens_per_seq, len_hint,
-                       workspace, workspace_bytes, S, strategy, kv_dtype, stream);
+                       workspace, workspace_bytes, S, strategy, kv_dtype, stream, false);
+}
+
+int kvattn_append_decode(void* out, const void* qkv, void* kv_cache, float* kv_scale, int B, int NH, int hs,
+                         int maxT, const int* d_cur_len, int lens_per_seq, int len_hint, void* workspace,
+                         size_t workspace_bytes, int S, int strategy, int kv_dtype, void* stream) {
+    return decode_impl(out, qkv, kv_cache, kv_scale, B, NH, hs, maxT, d_cur_len, lens_per_seq, len_hint,
+                       workspace, workspace_bytes, S, strategy, kv_dtype, stream, true);
 }
 
 }  // extern "C"

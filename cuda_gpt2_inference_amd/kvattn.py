@@ -85,6 +85,7 @@ SIGNATURES = {
     "kvattn_plan": (_i, [_i, _i, _i, _i, _i, _i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i),
                          ctypes.POINTER(_i)]),
     "kvattn_decode": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp, _sz, _i, _i, _i, _vp]),
+    "kvattn_append_decode": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp, _sz, _i, _i, _i, _vp]),
 }
 
 
@@ -241,6 +242,16 @@ def decode(out, qkv, kv_cache, B, NH, hs, maxT, *, kv_dtype, kv_scale=None, cur_
                                _ptr(cur_len), int(bool(lens_per_seq)), int(len_hint), _ptr(workspace),
                                int(workspace_nbytes), int(S), strategy_code(strategy),
                                kv_dtype_code(kv_dtype), _stream(stream)), "kvattn_decode")
+
+
+def append_decode(out, qkv, kv_cache, B, NH, hs, maxT, *, kv_dtype, kv_scale=None, cur_len=None,
+                  lens_per_seq=False, len_hint=-1, workspace=None, workspace_nbytes=0, S=0, strategy="auto",
+                  stream=None) -> None:
+    """kv_cache_write + decode in one launch (kvattn_append_decode)."""
+    _check(lib().kvattn_append_decode(_ptr(out), _ptr(qkv), _ptr(kv_cache), _ptr(kv_scale), B, NH, hs, maxT,
+                                      _ptr(cur_len), int(bool(lens_per_seq)), int(len_hint), _ptr(workspace),
+                                      int(workspace_nbytes), int(S), strategy_code(strategy),
+                                      kv_dtype_code(kv_dtype), _stream(stream)), "kvattn_append_decode")
 
 
 class Workspace:

@@ -185,6 +185,19 @@ int kvattn_decode(void* out, const void* qkv, const void* kv_cache, const float*
                   void* workspace, size_t workspace_bytes,
                   int S, int strategy, int kv_dtype, void* stream);
 
+/* kvattn_cache_write followed by kvattn_decode with the same arguments, in one launch
+ * (two for SPLIT_MERGE): the current token's K and V rows are taken from qkv in registers
+ * (8-bit: quantised exactly as kvattn_cache_write does), written into column cur_len, and
+ * used in place of that cache column.  Cache contents and outputs equal those of the two
+ * calls.  Replaces the append launch kv_cache_write_kernel[_w8] together with the attention
+ * call after it (inference_gpt2_opt.cu:302-316, 329-345); the reference's ranked follow-up
+ * removes the same launch by moving the append into the QKV GEMV epilogue instead. */
+int kvattn_append_decode(void* out, const void* qkv, void* kv_cache, float* kv_scale,
+                         int B, int NH, int hs, int maxT,
+                         const int* d_cur_len, int lens_per_seq, int len_hint,
+                         void* workspace, size_t workspace_bytes,
+                         int S, int strategy, int kv_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

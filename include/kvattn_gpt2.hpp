@@ -114,4 +114,15 @@ inline void attention_kv_merge(void* out, const float* part_out, const float* pa
     kvattnCheck(kvattn_merge(out, part_out, part_lse, part_max, B, NH, hs, S, kv_dtype, stream));
 }
 
+// The append launch and the attention call of one layer (inference_gpt2_opt.cu:302-316,
+// 329-345) as one launch: AUTO strategy with no length hint, so the kernels plan the
+// segmentation from the device length and one captured step graph serves every length.
+// workspace: kvattn_workspace_bytes(B, NH, hs, maxT, 0) bytes, initialised once.
+inline void kv_append_attention(void* out, const void* qkv, void* kv_cache, float* kv_scale, int B, int NH,
+                                int hs, int maxT, void* workspace, size_t workspace_bytes, hipStream_t stream,
+                                int kv_dtype = KVATTN_KV_BF16, const int* d_cur_len = nullptr) {
+    kvattnCheck(kvattn_append_decode(out, qkv, kv_cache, kv_scale, B, NH, hs, maxT, d_cur_len, 0, -1, workspace,
+                                     workspace_bytes, 0, KVATTN_AUTO, kv_dtype, stream));
+}
+
 }  // namespace kvattn_gpt2

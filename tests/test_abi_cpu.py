@@ -78,14 +78,15 @@ ALIGNED = 1 << 20   # a fake, 16-byte aligned address; never dereferenced by the
     (dict(strategy=9), 6),                  # KVATTN_ERR_STRATEGY
     (dict(len_hint=5000), 12),              # KVATTN_ERR_LENGTH
 ])
-def test_decode_argument_errors(kw, status):
+@pytest.mark.parametrize("entry", ["kvattn_decode", "kvattn_append_decode"])
+def test_decode_argument_errors(kw, status, entry):
     kvattn = _kv()
     a = dict(out=ALIGNED, qkv=ALIGNED, kv=ALIGNED, kv_scale=ALIGNED, B=1, NH=12, hs=64, maxT=1024,
              kv_dtype=1, strategy=0, len_hint=-1)
     a.update(kw)
-    st = kvattn.lib().kvattn_decode(a["out"], a["qkv"], a["kv"], a["kv_scale"], a["B"], a["NH"], a["hs"],
-                                    a["maxT"], None, 0, a["len_hint"], None, 0, 0, a["strategy"],
-                                    a["kv_dtype"], None)
+    st = getattr(kvattn.lib(), entry)(a["out"], a["qkv"], a["kv"], a["kv_scale"], a["B"], a["NH"], a["hs"],
+                                      a["maxT"], None, 0, a["len_hint"], None, 0, 0, a["strategy"],
+                                      a["kv_dtype"], None)
     assert st == status, kvattn.strerror(st)
 
 

@@ -88,6 +88,67 @@ def test_set_cur_len_async(dev):
     assert int((c != 0).any(dim=2).sum()) == 2
 
 
+def _cache_bytes(t):
+    import torch
+    return t.view(torch.uint8).cpu().numpy().copy()
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "int8", "fp8"])
+@pytest.mark.parametrize("lens", ["uniform", "ragged"])
+def test_append_decode_equals_append_then_decode(dev, dtype, lens):
+    """kvattn_append_decode against kvattn_cache_write + kvattn_decode on copies of the same
+    cache: identical cache bytes (codes and scales included) and identical outputs, for every
+    strategy and partition, at lengths inside one tile, at the fused_single / split edge and
+    on the fused_single LDS path; outputs also against the oracle."""
+    import torch
+    kvattn = _kv()
+    B, NH, maxT = 2, 3, 600
+    totals = [[1, 1], [100, 100], [256, 256], [257, 257], [600, 600]] if lens == "uniform" else \
+        [[600, 131], [1, 257], [256, 64]]
+    runs = [("auto", 0, True), ("auto", 0, False), ("fused_single", 0, True), ("split_merge", 8, True),
+            ("split_merge", 0, False), ("lastblock", 0, False), ("lastblock", -64, True), ("graph", 0, False),
+            ("coop", 8, True), ("coop", 0, False)]
+    for tt in totals:
+        case = make_case(dtype, B, NH, maxT, np.array(tt, np.int32) - 1, seed=50 + tt[0])
+        qkv, cache, scale, cur = to_device(case, dev)
+        if lens == "uniform":
+            cur = cur[:1].contiguous()
+        hint = max(tt) - 1
+        for strategy, S, hinted in runs:
+            ws = kvattn.Workspace(B, NH, maxT, S)
+            kw = dict(kv_dtype=dtype, cur_len=cur, lens_per_seq=(lens == "ragged"), S=S, strategy=strategy,
+                      len_hint=hint if hinted else -1, **ws.kwargs())
+            c_a, c_b = cache.clone(), cache.clone()
+            s_a = scale.clone() if scale is not None else None
+            s_b = scale.clone() if scale is not None else None
+            o_a, o_b = out_tensor(case, dev), out_tensor(case, dev)
+            kvattn.kv_cache_write(c_a, qkv, B, NH, HS, maxT, kv_dtype=dtype, kv_scale=s_a, cur_len=cur,
+                                  lens_per_seq=(lens == "ragged"))
+            kvattn.decode(o_a, qkv, c_a, B, NH, HS, maxT, kv_scale=s_a, **kw)
+            kvattn.append_decode(o_b, qkv, c_b, B, NH, HS, maxT, kv_scale=s_b, **kw)
+            torch.cuda.synchronize()
+            what = f"{dtype} {lens} T={tt} {strategy} S={S} hint={hinted}"
+            assert np.array_equal(_cache_bytes(c_a), _cache_bytes(c_b)), what + ": cache"
+            if scale is not None:
+                assert np.array_equal(_cache_bytes(s_a), _cache_bytes(s_b)), what + ": scales"
+            ga, gb = o_a.float().cpu().numpy(), o_b.float().cpu().numpy()
+            assert np.array_equal(ga, gb), what + f": outputs differ by {np.abs(ga - gb).max():.3e}"
+        # The appended cache through the oracle's append, then the oracle's attention.
+        ref_case = make_case(dtype, B, NH, maxT, np.array(tt, np.int32) - 1, seed=50 + tt[0])
+        if dtype in ("int8", "fp8"):
+            fmt = oracle.W8_INT8 if dtype == "int8" else oracle.W8_FP8_E4M3
+            codes, scales = ref_case.cache_raw.copy(), ref_case.scale_raw.copy()
+            oracle.cache_write_w8(codes, scales, ref_case.qkv_host, ref_case.cur_lens, B, NH, HS, maxT, fmt)
+            assert np.array_equal(_cache_bytes(c_b), codes), f"{dtype} {lens} T={tt}: codes vs oracle"
+            assert np.array_equal(_cache_bytes(s_b).view(np.uint32), scales.view(np.uint32))
+            vals = oracle.dequant_w8(codes, scales, B, NH, HS, maxT, fmt)
+        else:
+            vals = ref_case.cache_host.copy()
+            oracle.cache_write(vals, ref_case.qkv_host, ref_case.cur_lens, B, NH, HS, maxT)
+        ref = oracle.attention_f32(ref_case.qkv_host, vals, ref_case.totals, B, NH, HS, maxT)
+        assert_close(gb, ref, dtype, f"append_decode {dtype} {lens} T={tt}")
+
+
 class Engine:
     """The attention block of a decode step for L layers (append, then attention, per
     layer), captured into a graph over per-layer qkv / out buffers and one KV cache
@@ -115,23 +176,27 @@ class Engine:
         n = 2 * self.B * self.NH * self.maxT
         return None if self.scale is None else self.scale[l * n:(l + 1) * n]
 
-    def step(self, strategy="auto", S=0):
+    def step(self, strategy="auto", S=0, fused=False):
         k = self.kvattn
         for l in range(self.L):
+            args = (self.out[l], self.qkv[l], self.layer_cache(l), self.B, self.NH, HS, self.maxT)
+            kw = dict(kv_dtype=self.dtype, kv_scale=self.layer_scale(l), cur_len=self.cur, S=S, strategy=strategy,
+                      **self.ws.kwargs())
+            if fused:
+                k.append_decode(*args, **kw)
+                continue
             k.kv_cache_write(self.layer_cache(l), self.qkv[l], self.B, self.NH, HS, self.maxT, kv_dtype=self.dtype,
                              kv_scale=self.layer_scale(l), cur_len=self.cur)
-            k.decode(self.out[l], self.qkv[l], self.layer_cache(l), self.B, self.NH, HS, self.maxT,
-                     kv_dtype=self.dtype, kv_scale=self.layer_scale(l), cur_len=self.cur, S=S, strategy=strategy,
-                     **self.ws.kwargs())
+            k.decode(*args, **kw)
 
-    def capture(self, strategy="auto", S=0):
+    def capture(self, strategy="auto", S=0, fused=False):
         import torch
         torch.cuda.synchronize()
         s = torch.cuda.Stream()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.stream(s):
             with torch.cuda.graph(g, stream=s):
-                self.step(strategy, S)
+                self.step(strategy, S, fused)
         torch.cuda.synchronize()
         return g
 
@@ -143,11 +208,13 @@ def _host_values(t, dtype):
     return oracle.bf16_decode(t.view(torch.int16).cpu().numpy().view(np.uint16))
 
 
-@pytest.mark.parametrize("dtype,mode", [("bf16", "one_graph"), ("bf16", "graph_pair"), ("fp8", "one_graph")])
+@pytest.mark.parametrize("dtype,mode", [("bf16", "one_graph"), ("bf16", "graph_pair"), ("fp8", "one_graph"),
+                                        ("bf16", "fused"), ("int8", "fused")])
 def test_decode_step_token_by_token(dev, dtype, mode):
     """GPT-2 shape, 12 layers, B=1, NH=12, maxT=1024: the step graph is replayed for every
     token 1..1024 with fresh qkv and the device length advanced by set_cur_len_async.
-    one_graph: one capture, AUTO with no hint.  graph_pair: the reference's two graphs,
+    one_graph: one capture, AUTO with no hint.  fused: the same with kvattn_append_decode
+    (append and attention in one launch per layer).  graph_pair: the reference's two graphs,
     fused_single below 150 positions and split + merge with S = 8 above (selection on the
     host per token, as inference_gpt2_opt.cu:556).  Checked: every appended row bit for bit
     (8-bit: codes and scales against the oracle's quantiser) and the outputs of all layers
@@ -156,8 +223,8 @@ def test_decode_step_token_by_token(dev, dtype, mode):
     kvattn = _kv()
     L, B, NH, maxT = 12, 1, 12, 1024
     eng = Engine(dev, L, B, NH, maxT, dtype)
-    if mode == "one_graph":
-        graphs = [eng.capture("auto")]
+    if mode in ("one_graph", "fused"):
+        graphs = [eng.capture("auto", fused=(mode == "fused"))]
         pick = lambda cur_len: graphs[0]
     else:
         graphs = [eng.capture("fused_single"), eng.capture("split_merge", S=8)]
