@@ -359,6 +359,66 @@ def other_configs(torch, kvattn, dev):
     }
 
 
+GEMV_SHAPES = (("qkv", 2304, 768, False), ("attproj", 768, 768, False), ("fc", 3072, 768, True),
+               ("fcproj", 768, 3072, False))
+
+
+def gemv_configs(torch, kvattn, dev, layers=12, reps=100):
+    """The fully connected decode layer (kvattn_gemv) at GPT-2's four shapes, B = 1: one graph
+    of `layers` calls on distinct weights (as a decode step walks the layers), replayed back
+    to back.  Bytes per call: weights (+ row scales) + x + bias + out."""
+    res = {}
+    g = torch.Generator(device=dev)
+    g.manual_seed(9)
+    for w_dtype in ("bf16", "int8", "fp8"):
+        for name, M, K, gelu in GEMV_SHAPES:
+            if w_dtype == "bf16":
+                Ws = [(torch.randn(M * K, generator=g, device=dev) / K ** 0.5).to(torch.bfloat16)
+                      for _ in range(layers)]
+                scales = [None] * layers
+                wbytes = M * K * 2
+            else:
+                Ws = [torch.randint(0, 126, (M * K,), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
+                      for _ in range(layers)]
+                scales = [torch.full((M,), 1e-3, device=dev) for _ in range(layers)]
+                wbytes = M * K + M * 4
+            x = torch.randn(K, generator=g, device=dev).to(torch.bfloat16)
+            bias = torch.randn(M, generator=g, device=dev).to(torch.bfloat16)
+            outs = [torch.empty(M, device=dev, dtype=torch.bfloat16) for _ in range(layers)]
+
+            def step():
+                for l in range(layers):
+                    kvattn.gemv(outs[l], Ws[l], x, 1, M, K, w_dtype=w_dtype, w_scale=scales[l], bias=bias,
+                                gelu=gelu)
+            s = torch.cuda.Stream()
+            graph = torch.cuda.CUDAGraph()
+            torch.cuda.synchronize()
+            with torch.cuda.stream(s):
+                with torch.cuda.graph(graph, stream=s):
+                    step()
+            graph.replay()
+            us = timed(torch, graph.replay, reps) * 1000.0 / layers
+            nbytes = wbytes + K * 2 + 2 * M * 2
+            gbs = nbytes / (us * 1e-6) / 1e9
+            res[f"{name}_{w_dtype}_{M}x{K}"] = {"us_per_call": round(us, 3), "bytes_per_call": nbytes,
+                                                "GBps": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+            del Ws, scales, outs
+    return res
+
+
+def gemv_cpu_baseline(seconds=3.0):
+    """oracle_gemv (FP32, one thread) at the attention output projection, 768 x 768."""
+    from oracle import oracle
+    import numpy as np
+    r = np.random.RandomState(0)
+    W = r.standard_normal((768, 768)).astype(np.float32)
+    x = r.standard_normal((1, 768)).astype(np.float32)
+    t1 = oracle.time_gemv(W, x, 1, 768, 768, reps=3)
+    reps = max(3, int(seconds * 1e6 / max(t1, 1.0)))
+    return {"value": round(oracle.time_gemv(W, x, 1, 768, 768, reps=reps), 2), "unit": "us/call", "cores": 1,
+            "kind": "port", "sample": f"oracle_gemv FP32 768x768, B=1, median of {reps} calls"}
+
+
 def kernel_key(plan, B, NH):
     """(name prefix, grid suffix) of the split kernel a plan launches (BF16 = dtype 1), as
     keyed in the rocprof summaries: `split_kernel<1, MODE, WAVES, TILE> grid=WORKITEMS`."""
@@ -460,6 +520,8 @@ def main():
         c5["kernel"] = k5
         c5["traffic_bytes_split_kernel"] = t5
     configs = None if args.no_configs else other_configs(torch, kvattn, dev)
+    gemv = None if args.no_configs else gemv_configs(torch, kvattn, dev)
+    gemv_cpu = None if (args.no_configs or args.no_cpu) else gemv_cpu_baseline()
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds, c2)
 
     line = {
@@ -489,6 +551,7 @@ def main():
                   "cold_us_per_call": round(cold_us, 3),
                   "c2_context_sweep": t_sweep,
                   "c2_token_sweep": tok_sweep,
+                  "gemv": gemv, "gemv_cpu_baseline": gemv_cpu,
                   "rel_err_vs_f64": rel,
                   "gpu_vs_cpu_speedup": (round(cpu["value"] / us_call, 1) if cpu else None),
                   "c5": c5, "configs": configs, "gpu": torch.cuda.get_device_name(dev),

@@ -1,0 +1,192 @@
+// gemv.hip -- the decode step's fully connected layer on MI355X (gfx950, wave64):
+// out[b][m] = act(scale_m * sum_k W[m][k] x[b][k] + bias[m]), act = identity or GPT-2's
+// tanh GELU, for FP32, BF16 and 8-bit (INT8 / FP8-E4M3 codes with one FP32 scale per row)
+// weights.  The attention output projection consumes the attention output this way.
+//
+// One wave per output row.  A row of K weights is K*wbytes/16 chunks of 16 bytes; lane l
+// holds chunks l, l+64, ... in registers (all requested at once), multiplies them with the
+// matching x chunks of every input vector, and a wave reduction (DPP + permlane) finishes
+// each dot product.  The weights are read once for all B vectors.  At GPT-2 sizes (0.6 to
+// 4.7 MB of weights per layer) a call is bound by launch and memory latency, not by HBM
+// bandwidth; MFMA is not used (B is a handful of decode tokens, 1-2 flops per byte).
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "kvattn.h"
+#include "lanes.hpp"
+
+namespace {
+
+constexpr int kGemvWaves = 4;          // rows (waves) per workgroup
+constexpr int kGemvMaxChunks = 16;     // 16-byte weight chunks per lane: K*wbytes <= 16 KB
+
+template <int WT> struct WFmt;
+template <> struct WFmt<KVATTN_KV_F32> {   // x, bias, out: float
+    static constexpr int kWBytes = 4, kElems = 4, kXBytes = 16;
+    static constexpr bool kActF32 = true, k8bit = false;
+};
+template <> struct WFmt<KVATTN_KV_BF16> {  // x, bias, out: bf16
+    static constexpr int kWBytes = 2, kElems = 8, kXBytes = 16;
+    static constexpr bool kActF32 = false, k8bit = false;
+};
+template <> struct WFmt<KVATTN_KV_INT8> {  // x, bias, out: bf16
+    static constexpr int kWBytes = 1, kElems = 16, kXBytes = 32;
+    static constexpr bool kActF32 = false, k8bit = true;
+};
+template <> struct WFmt<KVATTN_KV_FP8_E4M3> {
+    static constexpr int kWBytes = 1, kElems = 16, kXBytes = 32;
+    static constexpr bool kActF32 = false, k8bit = true;
+};
+
+struct GemvArgs {
+    void* out;
+    void* pre_gelu;
+    const uint8_t* W;
+    const float* w_scale;
+    const uint8_t* x;
+    const void* bias;
+    int B, M, K, gelu;
+};
+
+// Dot product of one 16-byte weight chunk with the x values it multiplies.
+template <int WT>
+__device__ __forceinline__ float chunk_dot(const uint4& w, const uint8_t* xp) {
+    using F = WFmt<WT>;
+    float wf[F::kElems], xf[F::kElems];
+    if constexpr (WT == KVATTN_KV_F32) {
+        const uint4 xv = *reinterpret_cast<const uint4*>(xp);
+        wf[0] = __uint_as_float(w.x); wf[1] = __uint_as_float(w.y);
+        wf[2] = __uint_as_float(w.z); wf[3] = __uint_as_float(w.w);
+        xf[0] = __uint_as_float(xv.x); xf[1] = __uint_as_float(xv.y);
+        xf[2] = __uint_as_float(xv.z); xf[3] = __uint_as_float(xv.w);
+    } else if constexpr (WT == KVATTN_KV_BF16) {
+        const uint4 xv = *reinterpret_cast<const uint4*>(xp);
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w}, xw[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            wf[2 * i] = bf16_lo(ww[i]); wf[2 * i + 1] = bf16_hi(ww[i]);
+            xf[2 * i] = bf16_lo(xw[i]); xf[2 * i + 1] = bf16_hi(xw[i]);
+        }
+    } else {
+        decode_codes<WT == KVATTN_KV_FP8_E4M3>(w, wf);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint4 xv = reinterpret_cast<const uint4*>(xp)[h];
+            const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                xf[8 * h + 2 * i] = bf16_lo(xw[i]);
+                xf[8 * h + 2 * i + 1] = bf16_hi(xw[i]);
+            }
+        }
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int e = 0; e < F::kElems; ++e) s = fmaf(wf[e], xf[e], s);
+    return s;
+}
+
+template <int WT>
+__device__ __forceinline__ float load_act(const void* p, size_t i) {
+    if constexpr (WFmt<WT>::kActF32) return reinterpret_cast<const float*>(p)[i];
+    else return bf16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+}
+
+template <int WT>
+__device__ __forceinline__ void store_act(void* p, size_t i, float v) {
+    if constexpr (WFmt<WT>::kActF32) reinterpret_cast<float*>(p)[i] = v;
+    else reinterpret_cast<uint16_t*>(p)[i] = f32_to_bf16(v);
+}
+
+// GPT-2's GELU, tanh form: 0.5 v (1 + tanh(sqrt(2/pi) (v + 0.044715 v^3))).
+__device__ __forceinline__ float gelu_tanh(float v) {
+    const float cube = 0.044715f * v * v * v;
+    return 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + cube)));
+}
+
+template <int WT, int kC>
+__global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(GemvArgs a) {
+    using F = WFmt<WT>;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int m = blockIdx.x * kGemvWaves + wave;
+    if (m >= a.M) return;   // whole wave; the kernel has no workgroup barrier
+    const int nch = a.K * F::kWBytes / 16;
+    const uint8_t* wrow = a.W + (size_t)m * a.K * F::kWBytes;
+    uint4 w[kC];
+#pragma unroll
+    for (int i = 0; i < kC; ++i) {
+        const int c = lane + i * kWave;
+        w[i] = c < nch ? *reinterpret_cast<const uint4*>(wrow + (size_t)c * 16) : make_uint4(0u, 0u, 0u, 0u);
+    }
+    const float ws = F::k8bit ? a.w_scale[m] : 1.0f;
+    const float bias = a.bias ? load_act<WT>(a.bias, m) : 0.0f;
+    constexpr int kActBytes = F::kActF32 ? 4 : 2;
+    for (int b = 0; b < a.B; ++b) {
+        const uint8_t* xb = a.x + (size_t)b * a.K * kActBytes;
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kC; ++i) {
+            const int c = lane + i * kWave;
+            if (c < nch) acc += chunk_dot<WT>(w[i], xb + (size_t)c * F::kXBytes);
+        }
+        acc = wave_sum(acc);
+        if (lane == 0) {
+            float pre = acc * ws + bias;
+            const size_t o = (size_t)b * a.M + m;
+            if (a.pre_gelu) store_act<WT>(a.pre_gelu, o, pre);
+            if (a.gelu) pre = gelu_tanh(pre);
+            store_act<WT>(a.out, o, pre);
+        }
+    }
+}
+
+template <int WT>
+const void* gemv_ptr(int chunks_per_lane) {
+    if (chunks_per_lane <= 1) return (const void*)&gemv_kernel<WT, 1>;
+    if (chunks_per_lane <= 2) return (const void*)&gemv_kernel<WT, 2>;
+    if (chunks_per_lane <= 4) return (const void*)&gemv_kernel<WT, 4>;
+    if (chunks_per_lane <= 8) return (const void*)&gemv_kernel<WT, 8>;
+    return (const void*)&gemv_kernel<WT, kGemvMaxChunks>;
+}
+
+}  // namespace
+
+namespace kvattn_internal {
+void set_last_hip_error(int e);   // kvattn.hip: read back by kvattn_last_hip_error
+}
+
+extern "C" int kvattn_gemv(void* out, void* pre_gelu, const void* W, const float* w_scale, const void* x,
+                           const void* bias, int B, int M, int K, int w_dtype, int gelu, void* stream) {
+    if (w_dtype < KVATTN_KV_F32 || w_dtype > KVATTN_KV_FP8_E4M3) return KVATTN_ERR_DTYPE;
+    const bool w8 = w_dtype == KVATTN_KV_INT8 || w_dtype == KVATTN_KV_FP8_E4M3;
+    const int wbytes = w_dtype == KVATTN_KV_F32 ? 4 : (w_dtype == KVATTN_KV_BF16 ? 2 : 1);
+    const size_t act = w_dtype == KVATTN_KV_F32 ? 4 : 2;
+    if (B < 1 || M < 1 || K < 16 || K % 16 != 0) return KVATTN_ERR_SHAPE;
+    if ((long long)K * wbytes > (long long)kGemvMaxChunks * kWave * 16) return KVATTN_ERR_SHAPE;
+    if ((long long)B * M >= (1ll << 31) || (long long)M * K * wbytes >= (1ll << 40)) return KVATTN_ERR_SHAPE;
+    if (!out || !W || !x) return KVATTN_ERR_NULL_POINTER;
+    if (w8 && !w_scale) return KVATTN_ERR_DTYPE;
+    if (((uintptr_t)W & 15u) || ((uintptr_t)x & 15u)) return KVATTN_ERR_MISALIGNED;
+    if (((uintptr_t)out % act) || ((uintptr_t)pre_gelu % act) || ((uintptr_t)bias % act) ||
+        ((uintptr_t)w_scale & 3u))
+        return KVATTN_ERR_MISALIGNED;
+    const int nch = K * wbytes / 16;
+    const int per_lane = (nch + kWave - 1) / kWave;
+    const void* fn = nullptr;
+    switch (w_dtype) {
+        case KVATTN_KV_F32: fn = gemv_ptr<KVATTN_KV_F32>(per_lane); break;
+        case KVATTN_KV_BF16: fn = gemv_ptr<KVATTN_KV_BF16>(per_lane); break;
+        case KVATTN_KV_INT8: fn = gemv_ptr<KVATTN_KV_INT8>(per_lane); break;
+        default: fn = gemv_ptr<KVATTN_KV_FP8_E4M3>(per_lane); break;
+    }
+    GemvArgs a{out, pre_gelu, (const uint8_t*)W, w_scale, (const uint8_t*)x, bias, B, M, K, gelu ? 1 : 0};
+    void* params[] = {&a};
+    const hipError_t e = hipLaunchKernel(fn, dim3((unsigned)((M + kGemvWaves - 1) / kGemvWaves)),
+                                         dim3(kGemvWaves * kWave), params, 0, (hipStream_t)stream);
+    if (e != hipSuccess) {
+        kvattn_internal::set_last_hip_error((int)e);
+        return KVATTN_ERR_HIP;
+    }
+    return KVATTN_OK;
+}

@@ -38,11 +38,11 @@
 #include <tuple>
 
 #include "kvattn.h"
+#include "lanes.hpp"
 
 namespace {
 
 constexpr int kHeadDim = 64;
-constexpr int kWave = 64;
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / kWave;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -96,21 +96,6 @@ template <int DT> constexpr int kUnroll = Row<DT>::k8bit ? KVATTN_UNROLL_BYTE : 
 template <int DT> constexpr int kUnrollLat = KVATTN_LAT_ROWS / kRowsPerLoad<DT> > 0 ? KVATTN_LAT_ROWS / kRowsPerLoad<DT> : 1;
 constexpr int kWavesLat = KVATTN_LAT_WAVES;
 
-// ------------------------------------------------------------------------------------
-// Element helpers.
-// ------------------------------------------------------------------------------------
-__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
-__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
-
-// float -> bfloat16 bits, round to nearest even; NaN stays a quiet NaN.
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
-}
-
 // OCP E4M3 ("FN": max 448, no infinities) encode of y, round to nearest even, finite
 // overflow saturates to +-448 (the reference's __NV_SATFINITE request).
 __device__ __forceinline__ uint8_t f32_to_e4m3_sat(float y) {
@@ -148,20 +133,6 @@ __device__ __forceinline__ uint8_t w8_code(float x, float scale) {
     }
 }
 
-// 16-byte row-chunk load; KVATTN_NT_LOADS=1 marks K/V loads non-temporal (streamed once).
-#ifndef KVATTN_NT_LOADS
-#define KVATTN_NT_LOADS 1
-#endif
-__device__ __forceinline__ uint4 load16(const uint8_t* p) {
-#if KVATTN_NT_LOADS
-    typedef unsigned v4u __attribute__((ext_vector_type(4)));
-    const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
-    return make_uint4(v.x, v.y, v.z, v.w);
-#else
-    return *reinterpret_cast<const uint4*>(p);
-#endif
-}
-
 // Decode one lane's 16-byte chunk of a row into kElems floats.
 template <int DT>
 __device__ __forceinline__ void decode(const uint4& d, float (&x)[Row<DT>::kElems]) {
@@ -172,19 +143,8 @@ __device__ __forceinline__ void decode(const uint4& d, float (&x)[Row<DT>::kElem
     } else if constexpr (DT == KVATTN_KV_BF16) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) { x[2 * i] = bf16_lo(w[i]); x[2 * i + 1] = bf16_hi(w[i]); }
-    } else if constexpr (DT == KVATTN_KV_INT8) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-#pragma unroll
-            for (int k = 0; k < 4; ++k) x[4 * i + k] = (float)(int8_t)(w[i] >> (8 * k));
-        }
     } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], false);
-            const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], true);
-            x[4 * i] = lo[0]; x[4 * i + 1] = lo[1]; x[4 * i + 2] = hi[0]; x[4 * i + 3] = hi[1];
-        }
+        decode_codes<DT == KVATTN_KV_FP8_E4M3>(d, x);
     }
 }
 
@@ -197,82 +157,6 @@ __device__ __forceinline__ float dot_chunk(const float (&q)[Row<DT>::kElems], co
     for (int e = 0; e < Row<DT>::kElems; ++e) s = fmaf(q[e], x[e], s);
     return s;
 }
-
-// ------------------------------------------------------------------------------------
-// Cross-lane reductions.  DPP control words (GFX9 encoding).
-// ------------------------------------------------------------------------------------
-constexpr int kDppQuadXor1 = 0xB1;    // quad_perm [1,0,3,2]
-constexpr int kDppQuadXor2 = 0x4E;    // quad_perm [2,3,0,1]
-constexpr int kDppRowRor4 = 0x124;    // rotate 16-lane row by 4
-constexpr int kDppRowRor8 = 0x128;    // rotate 16-lane row by 8
-constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i inside each 8-lane half row
-constexpr int kDppRowMirror = 0x140;  // lane i <-> 15-i inside each 16-lane row
-
-template <int kCtrl>
-__device__ __forceinline__ float dpp(float x) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xF, 0xF, true));
-}
-
-// Sum over the kLanes lanes holding one row (aligned groups of 4, 8 or 16 lanes).
-template <int kLanes>
-__device__ __forceinline__ float row_sum(float x) {
-    x += dpp<kDppQuadXor1>(x);
-    x += dpp<kDppQuadXor2>(x);
-    if constexpr (kLanes >= 8) x += dpp<kDppHalfMirror>(x);
-    if constexpr (kLanes >= 16) x += dpp<kDppRowMirror>(x);
-    return x;
-}
-
-// op(x, x of lane ^ 16) and op(x, x of lane ^ 32) with the gfx950 row-swap permutes:
-// permlane16_swap / permlane32_swap of x with itself return x with 16-lane rows (resp.
-// 32-lane halves) exchanged in one of the two results, so op over both outputs is op
-// over the lane pair.
-template <bool kMax>
-__device__ __forceinline__ float op_xor16(float x) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    const float a = __uint_as_float(r[0]), b = __uint_as_float(r[1]);
-    return kMax ? fmaxf(a, b) : a + b;
-}
-template <bool kMax>
-__device__ __forceinline__ float op_xor32(float x) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    const float a = __uint_as_float(r[0]), b = __uint_as_float(r[1]);
-    return kMax ? fmaxf(a, b) : a + b;
-}
-
-// Reduce over the lanes that hold the same channel slice of different rows
-// (lane = row_slot * kLanes + slice): every lane receives the result for its slice.
-template <int kLanes, bool kMax>
-__device__ __forceinline__ float slot_reduce(float x) {
-    auto op = [](float a, float b) { return kMax ? fmaxf(a, b) : a + b; };
-    if constexpr (kLanes == 4) { x = op(x, dpp<kDppRowRor4>(x)); x = op(x, dpp<kDppRowRor8>(x)); }
-    if constexpr (kLanes == 8) { x = op(x, dpp<kDppRowRor8>(x)); }
-    x = op_xor16<kMax>(x);
-    x = op_xor32<kMax>(x);
-    return x;
-}
-
-__device__ __forceinline__ float wave_max(float x) {
-    x = fmaxf(x, dpp<kDppQuadXor1>(x));
-    x = fmaxf(x, dpp<kDppQuadXor2>(x));
-    x = fmaxf(x, dpp<kDppHalfMirror>(x));
-    x = fmaxf(x, dpp<kDppRowMirror>(x));
-    x = op_xor16<true>(x);
-    x = op_xor32<true>(x);
-    return x;
-}
-
-__device__ __forceinline__ float wave_sum(float x) {
-    x += dpp<kDppQuadXor1>(x);
-    x += dpp<kDppQuadXor2>(x);
-    x += dpp<kDppHalfMirror>(x);
-    x += dpp<kDppRowMirror>(x);
-    x = op_xor16<false>(x);
-    x = op_xor32<false>(x);
-    return x;
-}
-
-__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Attended positions of sequence b: device length clamped to [0, maxT-1], plus one.
 __device__ __forceinline__ int seq_total(const int* cur_len, int lens_per_seq, int b, int maxT) {
@@ -1597,6 +1481,11 @@ int check_partials(const float* po, const float* pl, const float* pm, int S) {
 }
 
 }  // namespace
+
+// Shared with the other translation units of the library (not exported).
+namespace kvattn_internal {
+__attribute__((visibility("hidden"))) void set_last_hip_error(int e) { t_last_hip_error = e; }
+}  // namespace kvattn_internal
 
 // ======================================================================================
 // C ABI

@@ -1,0 +1,134 @@
+// lanes.hpp -- wave64 building blocks shared by the gfx950 kernels of this library:
+// bfloat16 and 8-bit code conversion, 16-byte lane loads and DPP / permlane reductions.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+constexpr int kWave = 64;
+
+// ------------------------------------------------------------------------------------
+// Element helpers.
+// ------------------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+// float -> bfloat16 bits, round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+// Sixteen 8-bit codes of one 16-byte chunk as floats: FP8 through the hardware OCP E4M3
+// conversion (v_cvt_pk_f32_fp8), INT8 by sign extension.
+template <bool kFp8>
+__device__ __forceinline__ void decode_codes(const uint4& d, float (&x)[16]) {
+    const uint32_t w[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if constexpr (kFp8) {
+            const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], false);
+            const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], true);
+            x[4 * i] = lo[0]; x[4 * i + 1] = lo[1]; x[4 * i + 2] = hi[0]; x[4 * i + 3] = hi[1];
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) x[4 * i + k] = (float)(int8_t)(w[i] >> (8 * k));
+        }
+    }
+}
+
+// 16-byte row-chunk load; KVATTN_NT_LOADS=1 marks K/V loads non-temporal (streamed once).
+#ifndef KVATTN_NT_LOADS
+#define KVATTN_NT_LOADS 1
+#endif
+__device__ __forceinline__ uint4 load16(const uint8_t* p) {
+#if KVATTN_NT_LOADS
+    typedef unsigned v4u __attribute__((ext_vector_type(4)));
+    const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+#else
+    return *reinterpret_cast<const uint4*>(p);
+#endif
+}
+
+// ------------------------------------------------------------------------------------
+// Cross-lane reductions.  DPP control words (GFX9 encoding).
+// ------------------------------------------------------------------------------------
+constexpr int kDppQuadXor1 = 0xB1;    // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;    // quad_perm [2,3,0,1]
+constexpr int kDppRowRor4 = 0x124;    // rotate 16-lane row by 4
+constexpr int kDppRowRor8 = 0x128;    // rotate 16-lane row by 8
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i inside each 8-lane half row
+constexpr int kDppRowMirror = 0x140;  // lane i <-> 15-i inside each 16-lane row
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xF, 0xF, true));
+}
+
+// Sum over the kLanes lanes holding one row (aligned groups of 4, 8 or 16 lanes).
+template <int kLanes>
+__device__ __forceinline__ float row_sum(float x) {
+    x += dpp<kDppQuadXor1>(x);
+    x += dpp<kDppQuadXor2>(x);
+    if constexpr (kLanes >= 8) x += dpp<kDppHalfMirror>(x);
+    if constexpr (kLanes >= 16) x += dpp<kDppRowMirror>(x);
+    return x;
+}
+
+// op(x, x of lane ^ 16) and op(x, x of lane ^ 32) with the gfx950 row-swap permutes:
+// permlane16_swap / permlane32_swap of x with itself return x with 16-lane rows (resp.
+// 32-lane halves) exchanged in one of the two results, so op over both outputs is op
+// over the lane pair.
+template <bool kMax>
+__device__ __forceinline__ float op_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float a = __uint_as_float(r[0]), b = __uint_as_float(r[1]);
+    return kMax ? fmaxf(a, b) : a + b;
+}
+template <bool kMax>
+__device__ __forceinline__ float op_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float a = __uint_as_float(r[0]), b = __uint_as_float(r[1]);
+    return kMax ? fmaxf(a, b) : a + b;
+}
+
+// Reduce over the lanes that hold the same channel slice of different rows
+// (lane = row_slot * kLanes + slice): every lane receives the result for its slice.
+template <int kLanes, bool kMax>
+__device__ __forceinline__ float slot_reduce(float x) {
+    auto op = [](float a, float b) { return kMax ? fmaxf(a, b) : a + b; };
+    if constexpr (kLanes == 4) { x = op(x, dpp<kDppRowRor4>(x)); x = op(x, dpp<kDppRowRor8>(x)); }
+    if constexpr (kLanes == 8) { x = op(x, dpp<kDppRowRor8>(x)); }
+    x = op_xor16<kMax>(x);
+    x = op_xor32<kMax>(x);
+    return x;
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+    x = fmaxf(x, dpp<kDppQuadXor1>(x));
+    x = fmaxf(x, dpp<kDppQuadXor2>(x));
+    x = fmaxf(x, dpp<kDppHalfMirror>(x));
+    x = fmaxf(x, dpp<kDppRowMirror>(x));
+    x = op_xor16<true>(x);
+    x = op_xor32<true>(x);
+    return x;
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+    x += dpp<kDppQuadXor1>(x);
+    x += dpp<kDppQuadXor2>(x);
+    x += dpp<kDppHalfMirror>(x);
+    x += dpp<kDppRowMirror>(x);
+    x = op_xor16<false>(x);
+    x = op_xor32<false>(x);
+    return x;
+}
+
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+}  // namespace

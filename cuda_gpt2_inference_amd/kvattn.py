@@ -86,6 +86,7 @@ SIGNATURES = {
                          ctypes.POINTER(_i)]),
     "kvattn_decode": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp, _sz, _i, _i, _i, _vp]),
     "kvattn_append_decode": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp, _sz, _i, _i, _i, _vp]),
+    "kvattn_gemv": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
 }
 
 
@@ -252,6 +253,13 @@ def append_decode(out, qkv, kv_cache, B, NH, hs, maxT, *, kv_dtype, kv_scale=Non
                                       _ptr(cur_len), int(bool(lens_per_seq)), int(len_hint), _ptr(workspace),
                                       int(workspace_nbytes), int(S), strategy_code(strategy),
                                       kv_dtype_code(kv_dtype), _stream(stream)), "kvattn_append_decode")
+
+
+def gemv(out, W, x, B, M, K, *, w_dtype, w_scale=None, bias=None, pre_gelu=None, gelu=False,
+         stream=None) -> None:
+    """Decode-step fully connected layer out = [GELU](W x [* w_scale] + bias) (kvattn_gemv)."""
+    _check(lib().kvattn_gemv(_ptr(out), _ptr(pre_gelu), _ptr(W), _ptr(w_scale), _ptr(x), _ptr(bias), B, M, K,
+                             kv_dtype_code(w_dtype), int(bool(gelu)), _stream(stream)), "kvattn_gemv")
 
 
 class Workspace:

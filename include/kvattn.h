@@ -198,6 +198,24 @@ int kvattn_append_decode(void* out, const void* qkv, void* kv_cache, float* kv_s
                          void* workspace, size_t workspace_bytes,
                          int S, int strategy, int kv_dtype, void* stream);
 
+/* The decode step's fully connected layer, used after the attention for the output
+ * projection: for b < B, m < M
+ *   pre = w_scale[m] * sum_k W[m][k] * x[b][k] + bias[m]      (w_scale: 8-bit weights only)
+ *   pre_gelu[b][m] = pre (if pre_gelu != NULL);  out[b][m] = gelu ? GELU_tanh(pre) : pre
+ * with FP32 accumulation.  Types by w_dtype (a kvattn_dtype):
+ *   F32        W, x, bias, out, pre_gelu float
+ *   BF16       W, x, bias, out, pre_gelu bf16
+ *   INT8, FP8  W one code per weight ([M][K] bytes) with one FP32 scale per row; x, bias,
+ *              out, pre_gelu bf16
+ * W is row-major [M][K]; x [B][K]; out [B][M].  Requires K % 16 == 0, K * weight bytes <=
+ * 16 KB, 16-byte aligned W and x.  bias may be NULL.
+ * Replaces launch_GEMV6_fused (Inference_gpt2/GEMV.cuh:132-206) and launch_GEMV6_w8x2
+ * (Inference_gpt2/GEMV_w8.cuh:64-184), which matmul_forward[_w8] calls for one decode token
+ * (inference_gpt2_opt.cu:106-132); the attention output projection is at :349-355.  B > 1
+ * reads the weights once for all B vectors (the reference takes cuBLASLt there). */
+int kvattn_gemv(void* out, void* pre_gelu, const void* W, const float* w_scale, const void* x,
+                const void* bias, int B, int M, int K, int w_dtype, int gelu, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

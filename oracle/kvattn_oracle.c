@@ -375,3 +375,49 @@ double oracle_time_attention_f32(float* out, const float* qkv, const float* kv_c
     free(t);
     return med;
 }
+
+/* ---------------------------------------------------------------------------------
+ * GEMV6_fused / GEMV6_w8x2 per output (Inference_gpt2/GEMV.cuh:132-197,
+ * GEMV_w8.cuh:64-157): an FP32 dot product of the row with x, the 8-bit row scale applied
+ * once after the sum (GEMV_w8.cuh:136), the bias added (GEMV.cuh:192), the pre-GELU value
+ * kept (:193) and GPT-2's tanh GELU with the reference's evaluation order (:195-197).
+ * The reference sums in lane-strided order and reduces across a warp; this sums k in
+ * ascending order, so the two agree to FP32 rounding of a K-term sum.
+ * ------------------------------------------------------------------------------- */
+float oracle_gelu_tanh(float v) {
+    const float cube = 0.044715f * v * v * v;
+    return 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + cube)));
+}
+
+void oracle_gemv(float* out, float* pre_gelu, const float* W, const float* w_scale, const float* x,
+                 const float* bias, int B, int M, int K, int gelu) {
+    for (int b = 0; b < B; b++) {
+        const float* xb = x + (size_t)b * K;
+        for (int m = 0; m < M; m++) {
+            const float* wr = W + (size_t)m * K;
+            float sum = 0.0f;
+            for (int k = 0; k < K; k++) sum += wr[k] * xb[k];
+            if (w_scale) sum *= w_scale[m];
+            float pre = sum;
+            if (bias) pre += bias[m];
+            const size_t o = (size_t)b * M + m;
+            if (pre_gelu) pre_gelu[o] = pre;
+            out[o] = gelu ? oracle_gelu_tanh(pre) : pre;
+        }
+    }
+}
+
+double oracle_time_gemv(float* out, const float* W, const float* w_scale, const float* x, const float* bias,
+                        int B, int M, int K, int reps) {
+    if (reps < 1) reps = 1;
+    double* t = (double*)malloc(sizeof(double) * (size_t)reps);
+    for (int r = 0; r < reps; r++) {
+        const double t0 = now_us();
+        oracle_gemv(out, NULL, W, w_scale, x, bias, B, M, K, 0);
+        t[r] = now_us() - t0;
+    }
+    qsort(t, (size_t)reps, sizeof(double), cmp_double);
+    const double med = t[reps / 2];
+    free(t);
+    return med;
+}

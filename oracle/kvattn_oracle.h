@@ -113,6 +113,20 @@ double oracle_time_attention_f32(float* out, const float* qkv, const float* kv_c
                                  int B, int total, int NH, int hs, int maxT, float scale,
                                  int reps);
 
+/* The decode step's fully connected layer (the GEMV after the attention):
+ * for b < B, m < M: pre = (sum_{k ascending} W[m*K+k] * x[b*K+k]) * s_m + bias[m] in
+ * FP32, s_m = w_scale[m] (8-bit weights, W holding the decoded codes) or 1 (w_scale NULL);
+ * pre_gelu[b*M+m] = pre (if non-NULL); out[b*M+m] = gelu ? GELU_tanh(pre) : pre.
+ * Follows GEMV6_fused (Inference_gpt2/GEMV.cuh:132-197) and GEMV6_w8x2
+ * (Inference_gpt2/GEMV_w8.cuh:64-157).  Outputs are not rounded to the activation type. */
+void oracle_gemv(float* out, float* pre_gelu, const float* W, const float* w_scale, const float* x,
+                 const float* bias, int B, int M, int K, int gelu);
+float oracle_gelu_tanh(float v);
+
+/* Median microseconds of `reps` single-threaded oracle_gemv calls (CPU baseline). */
+double oracle_time_gemv(float* out, const float* W, const float* w_scale, const float* x, const float* bias,
+                        int B, int M, int K, int reps);
+
 #ifdef __cplusplus
 }
 #endif

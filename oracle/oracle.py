@@ -55,6 +55,9 @@ def lib():
             "oracle_lab_rand": (None, [ctypes.c_uint, _vp, ctypes.c_size_t]),
             "oracle_time_attention_f32": (ctypes.c_double,
                                           [_vp, _vp, _vp, _i, _i, _i, _i, _i, ctypes.c_float, _i]),
+            "oracle_gemv": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i]),
+            "oracle_gelu_tanh": (ctypes.c_float, [ctypes.c_float]),
+            "oracle_time_gemv": (ctypes.c_double, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -183,3 +186,29 @@ def time_attention_f32(qkv, kv_cache, total, B, NH, hs, maxT, reps: int) -> floa
     scale = np.float32(1.0 / np.sqrt(np.float32(hs)))
     return float(lib().oracle_time_attention_f32(_p(out), _p(qkv), _p(kv), B, total, NH, hs, maxT,
                                                  float(scale), reps))
+
+
+def gemv(W, x, B, M, K, *, w_scale=None, bias=None, gelu=False, want_pre=False):
+    """Fully connected decode layer (oracle_gemv): returns out [B*M] (and pre_gelu)."""
+    Wf, xf = _f32(W), _f32(x)
+    ws = None if w_scale is None else _f32(w_scale)
+    bs = None if bias is None else _f32(bias)
+    out = np.empty(B * M, dtype=np.float32)
+    pre = np.empty(B * M, dtype=np.float32) if want_pre else None
+    lib().oracle_gemv(_p(out), None if pre is None else _p(pre), _p(Wf), None if ws is None else _p(ws), _p(xf),
+                      None if bs is None else _p(bs), B, M, K, int(bool(gelu)))
+    return (out, pre) if want_pre else out
+
+
+def gelu_tanh(v: float) -> float:
+    return float(lib().oracle_gelu_tanh(float(v)))
+
+
+def time_gemv(W, x, B, M, K, w_scale=None, bias=None, reps: int = 20) -> float:
+    """Median microseconds of one single-threaded oracle_gemv call."""
+    Wf, xf = _f32(W), _f32(x)
+    ws = None if w_scale is None else _f32(w_scale)
+    bs = None if bias is None else _f32(bias)
+    out = np.empty(B * M, dtype=np.float32)
+    return float(lib().oracle_time_gemv(_p(out), _p(Wf), None if ws is None else _p(ws), _p(xf),
+                                        None if bs is None else _p(bs), B, M, K, reps))

@@ -1,0 +1,112 @@
+"""GPU parity of kvattn_gemv (the decode step's fully connected layer) against the oracle.
+
+Weights, inputs and biases are seeded and stored in the kernel's types (bf16 values and
+8-bit codes are decoded exactly for the oracle).  Bars, as norm-wise relative error over
+each output vector and max-abs error relative to max|ref|: FP32 1e-5; bf16 outputs 1e-2.
+GPT-2 shapes: the QKV projection (2304 x 768), the attention output projection
+(768 x 768), the MLP up projection with GELU (3072 x 768) and down projection (768 x 3072).
+"""
+import zlib
+
+import numpy as np
+import pytest
+
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"f32": 1e-5, "bf16": 1e-2, "int8": 1e-2, "fp8": 1e-2}
+FMT = {"int8": oracle.W8_INT8, "fp8": oracle.W8_FP8_E4M3}
+
+
+def _kv():
+    from cuda_gpt2_inference_amd import kvattn
+    return kvattn
+
+
+def _make(dtype, B, M, K, seed, with_bias=True):
+    """Host tensors in the kernel's types (moved to the GPU by _run) and the float values
+    the oracle sees."""
+    import torch
+    r = np.random.RandomState(seed)
+    x = r.standard_normal((B, K)).astype(np.float32)
+    bias = r.standard_normal(M).astype(np.float32) if with_bias else None
+    scale = None
+    if dtype == "f32":
+        W = (r.standard_normal((M, K)) / np.sqrt(K)).astype(np.float32)
+        dev = dict(W=torch.from_numpy(W), x=torch.from_numpy(x),
+                   bias=None if bias is None else torch.from_numpy(bias))
+        return dev, dict(W=W, x=x, bias=bias, scale=None)
+
+    def bf16_tensor(bits):
+        return torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16)
+
+    xb = oracle.bf16_round(x)
+    bb = None if bias is None else oracle.bf16_round(bias)
+    if dtype == "bf16":
+        Wb = oracle.bf16_round((r.standard_normal((M, K)) / np.sqrt(K)).astype(np.float32))
+        dW = bf16_tensor(Wb)
+        Wf = oracle.bf16_decode(Wb).reshape(M, K)
+    else:
+        codes = r.randint(0, 256, size=(M, K)).astype(np.uint8)
+        if dtype == "fp8":
+            codes[(codes & 0x7F) == 0x7F] = 0                 # no NaN codes
+        table = np.array([oracle.w8_decode(c, FMT[dtype]) for c in range(256)], dtype=np.float32)
+        Wf = table[codes]
+        scale = (1.0 / (np.abs(Wf).max(axis=1) + 1.0) / np.sqrt(K)).astype(np.float32)
+        dW = torch.from_numpy(codes)
+    dev = dict(W=dW, x=bf16_tensor(xb), bias=None if bb is None else bf16_tensor(bb),
+               scale=None if scale is None else torch.from_numpy(scale))
+    host = dict(W=Wf, x=oracle.bf16_decode(xb).reshape(B, K),
+                bias=None if bb is None else oracle.bf16_decode(bb), scale=scale)
+    return dev, host
+
+
+def _run(dev_t, dtype, B, M, K, gelu, want_pre):
+    import torch
+    kvattn = _kv()
+    d = {k: (None if v is None else v.to("cuda:0")) for k, v in dev_t.items()}
+    act = torch.float32 if dtype == "f32" else torch.bfloat16
+    out = torch.full((B * M,), float("nan"), dtype=act, device="cuda:0")
+    pre = torch.full((B * M,), float("nan"), dtype=act, device="cuda:0") if want_pre else None
+    kvattn.gemv(out, d["W"], d["x"], B, M, K, w_dtype=dtype, w_scale=d.get("scale"), bias=d["bias"],
+                pre_gelu=pre, gelu=gelu)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy(), (None if pre is None else pre.float().cpu().numpy())
+
+
+def _check(got, ref, dtype, B, M, what):
+    assert np.all(np.isfinite(got)), what
+    g = got.reshape(B, M).astype(np.float64)
+    r = ref.reshape(B, M).astype(np.float64)
+    nrm = (np.linalg.norm(g - r, axis=1) / np.linalg.norm(r, axis=1)).max()
+    mabs = np.abs(g - r).max() / np.abs(r).max()
+    assert nrm <= TOL[dtype] and mabs <= TOL[dtype], f"{what}: {nrm:.3e} {mabs:.3e}"
+
+
+SHAPES = [("qkv", 2304, 768, False), ("attproj", 768, 768, False), ("fc", 3072, 768, True),
+          ("fcproj", 768, 3072, False)]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "int8", "fp8"])
+@pytest.mark.parametrize("name,M,K,gelu", SHAPES)
+def test_gemv_gpt2_shapes(dev, dtype, name, M, K, gelu):
+    for B in (1, 3):
+        d, h = _make(dtype, B, M, K, seed=zlib.crc32(f"{dtype} {name} {B}".encode()) % 10000)
+        got, pre = _run(d, dtype, B, M, K, gelu, want_pre=gelu)
+        ref, rpre = oracle.gemv(h["W"], h["x"], B, M, K, w_scale=h["scale"], bias=h["bias"], gelu=gelu,
+                                want_pre=True)
+        _check(got, ref, dtype, B, M, f"{name} {dtype} B={B}")
+        if gelu:
+            _check(pre, rpre, dtype, B, M, f"{name} {dtype} B={B} pre_gelu")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "int8", "fp8"])
+@pytest.mark.parametrize("M,K", [(1, 16), (5, 48), (7, 1040), (130, 4096)])
+def test_gemv_ragged_shapes(dev, dtype, M, K):
+    """Rows not a multiple of the 4 per workgroup, rows whose chunks do not fill the 64
+    lanes, and the longest rows each dtype keeps in registers; no bias."""
+    d, h = _make(dtype, 2, M, K, seed=M * 7 + K, with_bias=False)
+    got, _ = _run(d, dtype, 2, M, K, False, False)
+    ref = oracle.gemv(h["W"], h["x"], 2, M, K, w_scale=h["scale"])
+    _check(got, ref, dtype, 2, M, f"M={M} K={K} {dtype}")
