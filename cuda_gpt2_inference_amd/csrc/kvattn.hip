@@ -52,6 +52,7 @@ constexpr float kStartMax = -1.0e30f;   // finite start value of every running m
 constexpr int kMinSegRows = 64;         // smallest automatic segment length
 constexpr int kMaxSegRows = 512;        // largest automatic segment length
 constexpr int kFusedMaxRows = 256;      // automatic plans keep up to this many positions in one workgroup
+constexpr int kMaxPagedSegRows = 4096;  // paged caches: at most 64 tiles per wave and segment
 constexpr int kMaxSegments = 1 << 16;   // upper bound on segments per (b,h)
 constexpr int kMaxT = 1 << 23;          // keeps per-slot byte offsets inside 32 bits
 constexpr size_t kFusedMaxLds = 64 * 1024;  // dynamic LDS of fused_single (scores)
@@ -448,6 +449,67 @@ __device__ __forceinline__ void online_rows_from(Tile<DT, kU>& t0, const QRaw<DT
 }
 
 // ------------------------------------------------------------------------------------
+// Paged caches.  A page holds page_rows positions (a multiple of 64) of one sequence for
+// all heads: [2][NH][page_rows] rows, K block then V block.  Tiles of kTile rows (which
+// divides page_rows) start at multiples of kTile and so never cross a page; within a
+// segment the waves take tiles round-robin.  Each wave loads the page ids of all its tiles
+// with one vector load (lane i: tile i) before its first tile, so the table costs one
+// memory round trip, not one per tile.  A page id outside [0, num_pages) is never
+// dereferenced: its rows are skipped.
+// ------------------------------------------------------------------------------------
+struct PagedView {
+    const uint8_t* pool;
+    const float* scale_pool;
+    const int* table;
+    int max_pages, page_rows, num_pages, NH;
+};
+
+// Slot pointers of head h inside page `page` (rows counted from the page's first row).
+template <int DT>
+__device__ __forceinline__ Slot page_slot(const PagedView& pv, int page, int h, int slice) {
+    const size_t rk = ((size_t)page * 2 * pv.NH + h) * pv.page_rows;
+    const size_t rv = rk + (size_t)pv.NH * pv.page_rows;
+    Slot s;
+    s.k = pv.pool + rk * Row<DT>::kBytes + slice * 16;
+    s.v = pv.pool + rv * Row<DT>::kBytes + slice * 16;
+    s.ks = Row<DT>::k8bit ? pv.scale_pool + rk : nullptr;
+    s.vs = Row<DT>::k8bit ? pv.scale_pool + rv : nullptr;
+    return s;
+}
+
+// Online softmax over rows [j0, j1) of (b, h) (j0 a multiple of kTile) by one wave of kW.
+// kFresh: the row `cur` is taken from fr and written through the table.
+template <int DT, int kU, int kW, bool kFresh>
+__device__ __forceinline__ void online_tiles_paged(const PagedView& pv, int b, int h, int j0, int j1, int wave,
+                                                   int slot_row, int slice, const QRaw<DT>& qr, float qscale,
+                                                   const FreshRaw<DT>& fr, uint8_t* kv_out, float* kv_scale_out,
+                                                   int cur, float& m, float& l, float (&acc)[Row<DT>::kElems]) {
+    constexpr int kTile = kRowsPerLoad<DT> * kU;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int P = pv.page_rows;
+    const int* row_table = pv.table + (size_t)b * pv.max_pages;
+    const int tr = j0 + (wave + lane * kW) * kTile;     // first row of this lane's tile
+    const int pid = tr < j1 ? row_table[tr / P] : -1;
+    float q[Row<DT>::kElems];
+    convert_q<DT>(qr, qscale, q);
+    Tile<DT, kU> t;
+    int i = 0;
+    for (int r = j0 + wave * kTile; r < j1; r += kW * kTile, ++i) {
+        const int page = __shfl(pid, i);
+        if (page < 0 || page >= pv.num_pages) continue;
+        const int pr0 = r / P * P;
+        const Slot sp = page_slot<DT>(pv, page, h, slice);
+        load_tile<DT, kU, true>(t, sp, r - pr0, j1 - pr0, slot_row);
+        if (kFresh && cur >= r && cur < min(r + kTile, j1)) {
+            const size_t rk = ((size_t)page * 2 * pv.NH + h) * P + (cur - pr0);
+            const FreshDst fd{kv_out, kv_scale_out, rk, rk + (size_t)pv.NH * P, slice};
+            patch_tile<DT, kU>(t, fr, fd, r - pr0, slot_row, cur - pr0);
+        }
+        consume_tile<DT, kU, true>(t, r - pr0, j1 - pr0, slot_row, q, m, l, acc);
+    }
+}
+
+// ------------------------------------------------------------------------------------
 // fused_single: one workgroup per (b,h), grid B*NH.  Pass 1 writes every score to LDS
 // and finds the exact maximum; pass 2 weights V with exp2(score - max).
 // ------------------------------------------------------------------------------------
@@ -675,6 +737,10 @@ struct SplitArgs {
     const float* kv_scale;
     uint8_t* kv_out;        // append-and-attend launches: where the current row goes
     float* kv_scale_out;
+    // Paged cache (table != nullptr): kv / kv_scale are page pools [page][2][NH][page_rows]
+    // rows, table[b * max_pages + j / page_rows] is the page holding position j of sequence b.
+    const int* table;
+    int max_pages, page_rows, num_pages;
     const int* cur_len;
     int lens_per_seq;
     int B, NH, maxT;
@@ -830,8 +896,9 @@ __device__ __forceinline__ void merge_partials(void* out, const float* part_out,
 #endif
 
 // kFresh: append and attend in one launch (the workgroup whose segment holds position
-// cur_len takes that row from qkv and writes it to the cache).
-template <int DT, int kMode, int kW, int kU, bool kFresh>
+// cur_len takes that row from qkv and writes it to the cache).  kPaged: the cache is a page
+// pool addressed through a block table (segments then start at multiples of the tile).
+template <int DT, int kMode, int kW, int kU, bool kFresh, bool kPaged>
 __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS : 1) void split_kernel(SplitArgs a) {
     using R = Row<DT>;
     __shared__ float s_m[kW];
@@ -853,7 +920,7 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
     FreshRaw<DT> fr{};
     bool spec = false;
     int w0 = 0, w1 = 0;
-    if (!a.lens_per_seq && a.seg_rows > 0) {
+    if (!kPaged && !a.lens_per_seq && a.seg_rows > 0) {
         const int bh0 = blockIdx.x / a.S;
         const int j0 = (blockIdx.x - bh0 * a.S) * a.seg_rows;
         const int nend = min(j0 + a.seg_rows, a.maxT);
@@ -896,24 +963,33 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                 if (lane == 0) { put<kCoh>(a.part_max + pidx, kEmptyMax); put<kCoh>(a.part_lse + pidx, 0.0f); }
             }
         } else {
-            const Slot sl = make_slot<DT>(a.kv, a.kv_scale, a.B, a.NH, a.maxT, bh, slice);
-            if (spec) {
-                w1 = min(w1, j1);
-            } else {
-                const int per_wave = ceil_div_i(j1 - j0, kW);
-                w0 = min(j0 + wave * per_wave, j1);
-                w1 = min(w0 + per_wave, j1);
-                load_tile<DT, kU, true>(t0, sl, w0, w1, slot_row);
-                q0 = load_q<DT>(a.qkv, it.b, it.h, a.NH, slice);
-                if constexpr (kFresh) fr = load_fresh<DT>(a.qkv, it.b, it.h, a.NH, slice);
-            }
             const int cur = it.total - 1;
-            FreshDst fd{};
-            if constexpr (kFresh) fd = fresh_dst(a.kv_out, a.kv_scale_out, a.B, a.NH, a.maxT, bh, slice, cur);
             float m = kStartMax, l = 0.0f, acc[R::kElems];
 #pragma unroll
             for (int e = 0; e < R::kElems; ++e) acc[e] = 0.0f;
-            online_rows_from<DT, kU, kFresh>(t0, q0, sl, w0, w1, slot_row, a.qscale, fr, fd, cur, m, l, acc);
+            if constexpr (kPaged) {
+                q0 = load_q<DT>(a.qkv, it.b, it.h, a.NH, slice);
+                if constexpr (kFresh) fr = load_fresh<DT>(a.qkv, it.b, it.h, a.NH, slice);
+                const PagedView pv{a.kv, a.kv_scale, a.table, a.max_pages, a.page_rows, a.num_pages, a.NH};
+                online_tiles_paged<DT, kU, kW, kFresh>(pv, it.b, it.h, j0, j1, wave, slot_row, slice, q0, a.qscale,
+                                                       fr, a.kv_out, a.kv_scale_out, cur, m, l, acc);
+            } else {
+                const Slot sl = make_slot<DT>(a.kv, a.kv_scale, a.B, a.NH, a.maxT, bh, slice);
+                if (spec) {
+                    w1 = min(w1, j1);
+                } else {
+                    const int per_wave = ceil_div_i(j1 - j0, kW);
+                    w0 = min(j0 + wave * per_wave, j1);
+                    w1 = min(w0 + per_wave, j1);
+                    load_tile<DT, kU, true>(t0, sl, w0, w1, slot_row);
+                    q0 = load_q<DT>(a.qkv, it.b, it.h, a.NH, slice);
+                    if constexpr (kFresh) fr = load_fresh<DT>(a.qkv, it.b, it.h, a.NH, slice);
+                }
+                FreshDst fd{};
+                if constexpr (kFresh)
+                    fd = fresh_dst(a.kv_out, a.kv_scale_out, a.B, a.NH, a.maxT, bh, slice, cur);
+                online_rows_from<DT, kU, kFresh>(t0, q0, sl, w0, w1, slot_row, a.qscale, fr, fd, cur, m, l, acc);
+            }
 
             // Combine the row slots of this wave, then the 4 waves.
             const float mw = slot_reduce<R::kLanes, true>(m);
@@ -988,11 +1064,33 @@ __global__ __launch_bounds__(kWave) void merge_kernel(SplitArgs a) {
 // ------------------------------------------------------------------------------------
 // KV append.
 // ------------------------------------------------------------------------------------
+// Where column cl of (b, h) lives: the contiguous cache [2][B][NH][maxT] rows, or, with a
+// block table, row cl % page_rows of head h in page table[b][cl / page_rows] of a pool
+// [page][2][NH][page_rows].  Returns false for a page id outside [0, num_pages).
+struct CacheMap {
+    const int* table;      // nullptr: contiguous
+    int max_pages, page_rows, num_pages;
+};
+
+__device__ __forceinline__ bool cache_rows(const CacheMap& cm, int B, int NH, int maxT, int b, int h, int cl,
+                                           size_t& rk, size_t& rv) {
+    if (!cm.table) {
+        rk = ((size_t)b * NH + h) * maxT + cl;
+        rv = (size_t)B * NH * maxT + rk;
+        return true;
+    }
+    const int page = cm.table[(size_t)b * cm.max_pages + cl / cm.page_rows];
+    if (page < 0 || page >= cm.num_pages) return false;
+    rk = ((size_t)page * 2 * NH + h) * cm.page_rows + cl % cm.page_rows;
+    rv = rk + (size_t)NH * cm.page_rows;
+    return true;
+}
+
 // F32 / BF16: one thread per 16-byte chunk of the 2*B*NH rows (K rows, then V rows).
 template <int DT>
 __global__ __launch_bounds__(kBlock) void cache_write_kernel(uint8_t* __restrict__ kv, const uint8_t* __restrict__ qkv,
                                                              const int* __restrict__ cur_len, int lens_per_seq,
-                                                             int B, int NH, int maxT) {
+                                                             int B, int NH, int maxT, CacheMap cm) {
     constexpr int kChunks = Row<DT>::kBytes / 16;
     const int t = blockIdx.x * kBlock + threadIdx.x;
     const int rows = 2 * B * NH;
@@ -1002,8 +1100,10 @@ __global__ __launch_bounds__(kBlock) void cache_write_kernel(uint8_t* __restrict
     const int kh = row - is_v * B * NH;
     const int b = kh / NH, h = kh - b * NH;
     const int cl = seq_total(cur_len, lens_per_seq, b, maxT) - 1;
+    size_t rk, rv;
+    if (!cache_rows(cm, B, NH, maxT, b, h, cl, rk, rv)) return;
     const size_t src = (((size_t)b * 3 + 1 + is_v) * NH + h) * Row<DT>::kBytes + c * 16;
-    const size_t dst = ((size_t)is_v * B * NH * maxT + (size_t)kh * maxT + cl) * Row<DT>::kBytes + c * 16;
+    const size_t dst = (is_v ? rv : rk) * Row<DT>::kBytes + c * 16;
     *reinterpret_cast<uint4*>(kv + dst) = *reinterpret_cast<const uint4*>(qkv + src);
 }
 
@@ -1013,7 +1113,7 @@ template <int DT>
 __global__ __launch_bounds__(kBlock) void cache_write_w8_kernel(uint8_t* __restrict__ kv, float* __restrict__ kv_scale,
                                                                 const uint16_t* __restrict__ qkv,
                                                                 const int* __restrict__ cur_len, int lens_per_seq,
-                                                                int B, int NH, int maxT) {
+                                                                int B, int NH, int maxT, CacheMap cm) {
     const int row = blockIdx.x * kWaves + threadIdx.x / kWave;
     const int c = threadIdx.x & (kWave - 1);
     if (row >= 2 * B * NH) return;
@@ -1025,7 +1125,9 @@ __global__ __launch_bounds__(kBlock) void cache_write_w8_kernel(uint8_t* __restr
     const float amax = wave_max(fabsf(x));
     const float scale = amax / kW8Limit<DT>;
     const uint8_t code = w8_code<DT>(x, scale);
-    const size_t r = (size_t)is_v * B * NH * maxT + (size_t)kh * maxT + cl;
+    size_t rk, rv;
+    if (!cache_rows(cm, B, NH, maxT, b, h, cl, rk, rv)) return;   // uniform over the wave
+    const size_t r = is_v ? rv : rk;
     kv[r * kHeadDim + c] = code;
     if (c == 0) kv_scale[r] = scale;
 }
@@ -1132,36 +1234,41 @@ int launch_fused_single(void* out, const void* qkv, const void* kv, const float*
 
 // Split kernel instance for a mode, a shape (`lat`: the latency shape, else the streaming
 // shape) and whether the launch also appends the current row.
-template <int DT, int W, int U, bool kFresh>
+// (Paged caches have no cooperative instance: the host never plans one.)
+template <int DT, int W, int U, bool kFresh, bool kPaged>
 const void* split_ptr_mode(int mode) {
-    if (mode == kPartialsOnly) return (const void*)&split_kernel<DT, kPartialsOnly, W, U, kFresh>;
-    if (mode == kLastBlockMerge) return (const void*)&split_kernel<DT, kLastBlockMerge, W, U, kFresh>;
-    return (const void*)&split_kernel<DT, kCoopMerge, W, U, kFresh>;
+    if (mode == kPartialsOnly) return (const void*)&split_kernel<DT, kPartialsOnly, W, U, kFresh, kPaged>;
+    if (mode == kLastBlockMerge) return (const void*)&split_kernel<DT, kLastBlockMerge, W, U, kFresh, kPaged>;
+    if constexpr (kPaged) return nullptr;
+    else return (const void*)&split_kernel<DT, kCoopMerge, W, U, kFresh, false>;
+}
+
+template <int DT, int W, int U>
+const void* split_ptr_shape(int mode, bool fresh, bool paged) {
+    if (paged) return fresh ? split_ptr_mode<DT, W, U, true, true>(mode) : split_ptr_mode<DT, W, U, false, true>(mode);
+    return fresh ? split_ptr_mode<DT, W, U, true, false>(mode) : split_ptr_mode<DT, W, U, false, false>(mode);
 }
 
 template <int DT>
-const void* split_ptr(int mode, bool lat, bool fresh) {
-    if (lat) {
-        return fresh ? split_ptr_mode<DT, kWavesLat, kUnrollLat<DT>, true>(mode)
-                     : split_ptr_mode<DT, kWavesLat, kUnrollLat<DT>, false>(mode);
-    }
-    return fresh ? split_ptr_mode<DT, kWaves, kUnroll<DT>, true>(mode)
-                 : split_ptr_mode<DT, kWaves, kUnroll<DT>, false>(mode);
+const void* split_ptr(int mode, bool lat, bool fresh, bool paged) {
+    if (lat) return split_ptr_shape<DT, kWavesLat, kUnrollLat<DT>>(mode, fresh, paged);
+    return split_ptr_shape<DT, kWaves, kUnroll<DT>>(mode, fresh, paged);
 }
 
 int split_threads(bool lat) { return (lat ? kWavesLat : kWaves) * kWave; }
 
-const void* split_ptr_dt(int kv_dtype, int mode, bool lat, bool fresh) {
+// The split kernel for these arguments: appending when kv_out is set, paged when table is.
+const void* split_ptr_for(const SplitArgs& a, int kv_dtype, int mode, bool lat) {
     const void* fn = nullptr;
     dispatch_dtype(kv_dtype, [&](auto dtc) -> int {
-        fn = split_ptr<decltype(dtc)::value>(mode, lat, fresh);
+        fn = split_ptr<decltype(dtc)::value>(mode, lat, a.kv_out != nullptr, a.table != nullptr);
         return KVATTN_OK;
     });
     return fn;
 }
 
 int launch_split(const SplitArgs& a, int kv_dtype, int mode, bool lat, hipStream_t stream) {
-    const void* fn = split_ptr_dt(kv_dtype, mode, lat, a.kv_out != nullptr);
+    const void* fn = split_ptr_for(a, kv_dtype, mode, lat);
     if (!fn) return KVATTN_ERR_DTYPE;
     SplitArgs args = a;
     void* params[] = {&args};
@@ -1200,7 +1307,7 @@ int launch_coop(const SplitArgs& a, int kv_dtype, bool lat, hipStream_t stream) 
     for (int attempt = 0; attempt < 2; ++attempt) {
         const bool use_lat = lat && attempt == 0;
         if (attempt == 1 && !lat) break;
-        const void* fn = split_ptr_dt(kv_dtype, kCoopMerge, use_lat, a.kv_out != nullptr);
+        const void* fn = split_ptr_for(a, kv_dtype, kCoopMerge, use_lat);
         if (!fn) return KVATTN_ERR_DTYPE;
         const int threads = split_threads(use_lat);
         int per_cu = 0;
@@ -1217,13 +1324,14 @@ int launch_coop(const SplitArgs& a, int kv_dtype, bool lat, hipStream_t stream) 
 // hipGraph holding the split and merge kernel nodes, built once per argument set.
 struct GraphKey {
     int dev, dt, lat;
-    const void *out, *qkv, *kv, *ks, *kv_out, *len, *po, *pl, *pm;
-    int lens_per_seq, B, NH, maxT, S, seg_rows;
+    const void *out, *qkv, *kv, *ks, *kv_out, *table, *len, *po, *pl, *pm;
+    int lens_per_seq, B, NH, maxT, S, seg_rows, max_pages, page_rows, num_pages;
     bool operator<(const GraphKey& o) const {
-        return std::tie(dev, dt, lat, out, qkv, kv, ks, kv_out, len, po, pl, pm, lens_per_seq, B, NH, maxT, S,
-                        seg_rows) <
-               std::tie(o.dev, o.dt, o.lat, o.out, o.qkv, o.kv, o.ks, o.kv_out, o.len, o.po, o.pl, o.pm,
-                        o.lens_per_seq, o.B, o.NH, o.maxT, o.S, o.seg_rows);
+        return std::tie(dev, dt, lat, out, qkv, kv, ks, kv_out, table, len, po, pl, pm, lens_per_seq, B, NH, maxT,
+                        S, seg_rows, max_pages, page_rows, num_pages) <
+               std::tie(o.dev, o.dt, o.lat, o.out, o.qkv, o.kv, o.ks, o.kv_out, o.table, o.len, o.po, o.pl, o.pm,
+                        o.lens_per_seq, o.B, o.NH, o.maxT, o.S, o.seg_rows, o.max_pages, o.page_rows,
+                        o.num_pages);
     }
 };
 
@@ -1237,8 +1345,10 @@ int launch_graph_pair(const SplitArgs& a, int kv_dtype, bool lat, hipStream_t st
     }
     int dev = 0;
     KV_HIP(hipGetDevice(&dev));
-    GraphKey key{dev, kv_dtype, lat ? 1 : 0, a.out, a.qkv, a.kv, a.kv_scale, a.kv_out, a.cur_len, a.part_out,
-                 a.part_lse, a.part_max, a.lens_per_seq, a.B, a.NH, a.maxT, a.S, a.seg_rows};
+    GraphKey key{dev,        kv_dtype,   lat ? 1 : 0, a.out,          a.qkv,      a.kv,
+                 a.kv_scale, a.kv_out,   a.table,     a.cur_len,      a.part_out, a.part_lse,
+                 a.part_max, a.lens_per_seq, a.B,     a.NH,           a.maxT,     a.S,
+                 a.seg_rows, a.max_pages, a.page_rows, a.num_pages};
     static std::mutex mu;
     static std::map<GraphKey, hipGraphExec_t> cache;
     std::lock_guard<std::mutex> lock(mu);
@@ -1248,7 +1358,7 @@ int launch_graph_pair(const SplitArgs& a, int kv_dtype, bool lat, hipStream_t st
             for (auto& kvp : cache) (void)hipGraphExecDestroy(kvp.second);
             cache.clear();
         }
-        void* fsplit = const_cast<void*>(split_ptr_dt(kv_dtype, kPartialsOnly, lat, a.kv_out != nullptr));
+        void* fsplit = const_cast<void*>(split_ptr_for(a, kv_dtype, kPartialsOnly, lat));
         void* fmerge = nullptr;
         dispatch_dtype(kv_dtype, [&](auto dtc) -> int {
             fmerge = (void*)&merge_kernel<decltype(dtc)::value>;
@@ -1361,16 +1471,23 @@ struct Plan {
 // A call is latency bound while it streams fewer rows than kStreamRows.
 bool latency_bound(int B, int NH, int total_rows) { return (long long)B * NH * total_rows < kStreamRows; }
 
-int make_plan(int B, int NH, int maxT, int len_hint, int S, int strategy, Plan& p) {
+// paged: a paged cache, which has no fused_single or cooperative instance and whose
+// segments start at multiples of 64 rows (the tile), so rows per segment are planned on
+// the device unless S < 0 gives a multiple of 64.
+int make_plan(int B, int NH, int maxT, int len_hint, int S, int strategy, Plan& p, bool paged = false) {
     if (strategy < KVATTN_AUTO || strategy > KVATTN_SPLIT_LASTBLOCK) return KVATTN_ERR_STRATEGY;
     if (len_hint >= maxT || len_hint < -1) return KVATTN_ERR_LENGTH;
+    if (paged) {
+        if (strategy == KVATTN_FUSED_SINGLE || strategy == KVATTN_SINGLE_LAUNCH_COOP) return KVATTN_ERR_STRATEGY;
+        if (S > 0 || (S < 0 && ((-S) % kMinSegRows != 0 || -S > kMaxPagedSegRows))) return KVATTN_ERR_SPLIT;
+    }
     const int total_hint = (len_hint < 0 ? maxT - 1 : len_hint) + 1;
     if (strategy == KVATTN_AUTO) {
         // Short contexts: one workgroup per (b,h).  Otherwise split; a single launch with
         // the in-kernel merge while the whole call is latency bound, and split + merge
         // kernel once the call streams enough rows to be bandwidth bound.
         const bool fits = (size_t)maxT * sizeof(float) <= kFusedMaxLds;
-        if (fits && total_hint <= kFusedMaxRows) strategy = KVATTN_FUSED_SINGLE;
+        if (!paged && fits && total_hint <= kFusedMaxRows) strategy = KVATTN_FUSED_SINGLE;
         else if ((long long)B * NH * total_hint >= kStreamRows) strategy = KVATTN_SPLIT_MERGE;
         else strategy = KVATTN_SPLIT_LASTBLOCK;
     }
@@ -1382,7 +1499,7 @@ int make_plan(int B, int NH, int maxT, int len_hint, int S, int strategy, Plan& 
         return KVATTN_OK;
     }
     KV_TRY(segment_slots(maxT, S, p.slots, p.seg_rows));
-    if (S == 0 && len_hint < 0) {
+    if (S == 0 && (len_hint < 0 || paged)) {
         p.seg_rows = kDevicePlan;
         p.slots = planned_slots(maxT);
     } else if (S == 0) {
@@ -1394,14 +1511,16 @@ int make_plan(int B, int NH, int maxT, int len_hint, int S, int strategy, Plan& 
 }
 
 // append == true: the launch also writes the current token's K/V row (kvattn_append_decode).
+// pm != nullptr: kv / kv_scale are page pools addressed through pm's block table.
 int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scale, int B, int NH, int hs,
                 int maxT, const int* d_cur_len, int lens_per_seq, int len_hint, void* workspace,
-                size_t workspace_bytes, int S, int strategy, int kv_dtype, void* stream_v, bool append) {
+                size_t workspace_bytes, int S, int strategy, int kv_dtype, void* stream_v, bool append,
+                const CacheMap* pm = nullptr) {
     KV_TRY(check_common(qkv, kv, kv_scale, B, NH, hs, maxT, kv_dtype));
     if (!out) return KVATTN_ERR_NULL_POINTER;
     if (!aligned16(out)) return KVATTN_ERR_MISALIGNED;
     Plan plan{};
-    KV_TRY(make_plan(B, NH, maxT, len_hint, S, strategy, plan));
+    KV_TRY(make_plan(B, NH, maxT, len_hint, S, strategy, plan, pm != nullptr));
     hipStream_t stream = (hipStream_t)stream_v;
 
     if (plan.strategy == KVATTN_FUSED_SINGLE) {
@@ -1429,6 +1548,12 @@ int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scal
     a.kv_scale = kv_scale;
     a.kv_out = append ? (uint8_t*)const_cast<void*>(kv) : nullptr;
     a.kv_scale_out = append ? const_cast<float*>(kv_scale) : nullptr;
+    if (pm) {
+        a.table = pm->table;
+        a.max_pages = pm->max_pages;
+        a.page_rows = pm->page_rows;
+        a.num_pages = pm->num_pages;
+    }
     a.cur_len = d_cur_len;
     a.lens_per_seq = lens_per_seq ? 1 : 0;
     a.B = B;
@@ -1471,6 +1596,38 @@ SplitArgs caller_partials(void* out, const void* qkv, const void* kv, const floa
     a.seg_rows = 0;
     a.qscale = qscale_for(kHeadDim);
     return a;
+}
+
+int launch_cache_write(void* kv, float* kv_scale, const void* qkv, int B, int NH, int maxT, const int* d_cur_len,
+                       int lens_per_seq, int kv_dtype, const CacheMap& cm, hipStream_t stream) {
+    const int lps = lens_per_seq ? 1 : 0;
+    return dispatch_dtype(kv_dtype, [&](auto dtc) -> int {
+        constexpr int DT = decltype(dtc)::value;
+        if constexpr (Row<DT>::k8bit) {
+            const int rows = 2 * B * NH;
+            hipLaunchKernelGGL((cache_write_w8_kernel<DT>), dim3((rows + kWaves - 1) / kWaves), dim3(kBlock), 0,
+                               stream, (uint8_t*)kv, kv_scale, (const uint16_t*)qkv, d_cur_len, lps, B, NH, maxT,
+                               cm);
+        } else {
+            const int chunks = 2 * B * NH * (Row<DT>::kBytes / 16);
+            hipLaunchKernelGGL((cache_write_kernel<DT>), dim3((chunks + kBlock - 1) / kBlock), dim3(kBlock), 0,
+                               stream, (uint8_t*)kv, (const uint8_t*)qkv, d_cur_len, lps, B, NH, maxT, cm);
+        }
+        KV_HIP(hipGetLastError());
+        return KVATTN_OK;
+    });
+}
+
+// Paged-cache arguments; maxT receives the positions a sequence can hold.
+int check_paged(const int* table, int max_pages, int page_rows, int num_pages, int NH, int& maxT) {
+    if (!table) return KVATTN_ERR_NULL_POINTER;
+    if ((uintptr_t)table & 3u) return KVATTN_ERR_MISALIGNED;
+    if (max_pages < 1 || num_pages < 1 || page_rows < kMinSegRows || page_rows % kMinSegRows != 0)
+        return KVATTN_ERR_SHAPE;
+    if ((long long)max_pages * page_rows > kMaxT) return KVATTN_ERR_SHAPE;
+    if ((long long)num_pages * 2 * NH * page_rows >= (1ll << 40)) return KVATTN_ERR_SHAPE;
+    maxT = max_pages * page_rows;
+    return KVATTN_OK;
 }
 
 int check_partials(const float* po, const float* pl, const float* pm, int S) {
@@ -1540,23 +1697,30 @@ int kvattn_cache_write(void* kv_cache, float* kv_scale, const void* qkv, int B, 
                        const int* d_cur_len, int lens_per_seq, int kv_dtype, void* stream_v) {
     KV_TRY(check_common(qkv, kv_cache, kv_scale, B, NH, hs, maxT, kv_dtype));
     KV_TRY(resolve_len(d_cur_len));
-    hipStream_t stream = (hipStream_t)stream_v;
-    const int lps = lens_per_seq ? 1 : 0;
-    return dispatch_dtype(kv_dtype, [&](auto dtc) -> int {
-        constexpr int DT = decltype(dtc)::value;
-        if constexpr (Row<DT>::k8bit) {
-            const int rows = 2 * B * NH;
-            hipLaunchKernelGGL((cache_write_w8_kernel<DT>), dim3((rows + kWaves - 1) / kWaves), dim3(kBlock), 0,
-                               stream, (uint8_t*)kv_cache, kv_scale, (const uint16_t*)qkv, d_cur_len, lps, B, NH,
-                               maxT);
-        } else {
-            const int chunks = 2 * B * NH * (Row<DT>::kBytes / 16);
-            hipLaunchKernelGGL((cache_write_kernel<DT>), dim3((chunks + kBlock - 1) / kBlock), dim3(kBlock), 0,
-                               stream, (uint8_t*)kv_cache, (const uint8_t*)qkv, d_cur_len, lps, B, NH, maxT);
-        }
-        KV_HIP(hipGetLastError());
-        return KVATTN_OK;
-    });
+    return launch_cache_write(kv_cache, kv_scale, qkv, B, NH, maxT, d_cur_len, lens_per_seq, kv_dtype, CacheMap{},
+                              (hipStream_t)stream_v);
+}
+
+int kvattn_paged_cache_write(void* pages, float* page_scales, const int* block_table, int max_pages,
+                             int page_rows, int num_pages, const void* qkv, int B, int NH, int hs,
+                             const int* d_cur_len, int lens_per_seq, int kv_dtype, void* stream) {
+    int maxT = 0;
+    KV_TRY(check_paged(block_table, max_pages, page_rows, num_pages, NH, maxT));
+    KV_TRY(check_common(qkv, pages, page_scales, B, NH, hs, maxT, kv_dtype));
+    KV_TRY(resolve_len(d_cur_len));
+    return launch_cache_write(pages, page_scales, qkv, B, NH, maxT, d_cur_len, lens_per_seq, kv_dtype,
+                              CacheMap{block_table, max_pages, page_rows, num_pages}, (hipStream_t)stream);
+}
+
+int kvattn_paged_decode(void* out, const void* qkv, void* pages, float* page_scales, const int* block_table,
+                        int max_pages, int page_rows, int num_pages, int B, int NH, int hs, const int* d_cur_len,
+                        int lens_per_seq, int len_hint, void* workspace, size_t workspace_bytes, int S,
+                        int strategy, int kv_dtype, int append, void* stream) {
+    int maxT = 0;
+    KV_TRY(check_paged(block_table, max_pages, page_rows, num_pages, NH, maxT));
+    const CacheMap cm{block_table, max_pages, page_rows, num_pages};
+    return decode_impl(out, qkv, pages, page_scales, B, NH, hs, maxT, d_cur_len, lens_per_seq, len_hint, workspace,
+                       workspace_bytes, S, strategy, kv_dtype, stream, append != 0, &cm);
 }
 
 int kvattn_forward_small(void* out, const void* qkv, const void* kv_cache, const float* kv_scale, int B, int NH,

@@ -87,6 +87,9 @@ SIGNATURES = {
     "kvattn_decode": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp, _sz, _i, _i, _i, _vp]),
     "kvattn_append_decode": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp, _sz, _i, _i, _i, _vp]),
     "kvattn_gemv": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
+    "kvattn_paged_cache_write": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _i, _i, _i, _vp, _i, _i, _vp]),
+    "kvattn_paged_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _i, _i, _vp, _sz, _i, _i,
+                                 _i, _i, _vp]),
 }
 
 
@@ -260,6 +263,43 @@ def gemv(out, W, x, B, M, K, *, w_dtype, w_scale=None, bias=None, pre_gelu=None,
     """Decode-step fully connected layer out = [GELU](W x [* w_scale] + bias) (kvattn_gemv)."""
     _check(lib().kvattn_gemv(_ptr(out), _ptr(pre_gelu), _ptr(W), _ptr(w_scale), _ptr(x), _ptr(bias), B, M, K,
                              kv_dtype_code(w_dtype), int(bool(gelu)), _stream(stream)), "kvattn_gemv")
+
+
+class PagedCache:
+    """A paged KV cache: a page pool [num_pages][2][NH][page_rows][hs] (+ row scales for
+    8-bit caches) and a block table [B][max_pages] of page ids (device tensors)."""
+
+    def __init__(self, pages, block_table, max_pages, page_rows, num_pages, page_scales=None):
+        self.pages, self.block_table, self.page_scales = pages, block_table, page_scales
+        self.max_pages, self.page_rows, self.num_pages = int(max_pages), int(page_rows), int(num_pages)
+
+    @property
+    def maxT(self) -> int:
+        return self.max_pages * self.page_rows
+
+    def _args(self):
+        return (_ptr(self.pages), _ptr(self.page_scales), _ptr(self.block_table), self.max_pages, self.page_rows,
+                self.num_pages)
+
+
+def paged_cache_write(cache: PagedCache, qkv, B, NH, hs, *, kv_dtype, cur_len=None, lens_per_seq=False,
+                      stream=None) -> None:
+    """kv_cache_write into a paged cache (kvattn_paged_cache_write)."""
+    _check(lib().kvattn_paged_cache_write(*cache._args(), _ptr(qkv), B, NH, hs, _ptr(cur_len),
+                                          int(bool(lens_per_seq)), kv_dtype_code(kv_dtype), _stream(stream)),
+           "kvattn_paged_cache_write")
+
+
+def paged_decode(out, qkv, cache: PagedCache, B, NH, hs, *, kv_dtype, cur_len=None, lens_per_seq=False,
+                 len_hint=-1, workspace=None, workspace_nbytes=0, S=0, strategy="auto", append=False,
+                 stream=None) -> None:
+    """decode / append_decode on a paged cache (kvattn_paged_decode)."""
+    p = cache._args()
+    _check(lib().kvattn_paged_decode(_ptr(out), _ptr(qkv), p[0], p[1], p[2], p[3], p[4], p[5], B, NH, hs,
+                                     _ptr(cur_len), int(bool(lens_per_seq)), int(len_hint), _ptr(workspace),
+                                     int(workspace_nbytes), int(S), strategy_code(strategy),
+                                     kv_dtype_code(kv_dtype), int(bool(append)), _stream(stream)),
+           "kvattn_paged_decode")
 
 
 class Workspace:

@@ -198,6 +198,38 @@ int kvattn_append_decode(void* out, const void* qkv, void* kv_cache, float* kv_s
                          void* workspace, size_t workspace_bytes,
                          int S, int strategy, int kv_dtype, void* stream);
 
+/* ---- Paged KV cache ------------------------------------------------------------------
+ * No reference counterpart: the reference keeps one contiguous [2][B][NH][maxT][hs] cache
+ * per layer and names paged KV management as its gap for multi-request serving
+ * (README.md:62-63).  Here a layer's cache may instead be a pool of pages:
+ *   pages        [num_pages][2][NH][page_rows][hs] elements (K block, then V block, of
+ *                page_rows positions of one sequence for every head)
+ *   page_scales  [num_pages][2][NH][page_rows] FP32 row scales (8-bit caches), else NULL
+ *   block_table  [B][max_pages] int32: page id holding positions
+ *                [i*page_rows, (i+1)*page_rows) of sequence b at block_table[b*max_pages+i]
+ * page_rows is a multiple of 64; a sequence holds up to max_pages*page_rows positions
+ * (the maxT of these calls).  Table entries outside [0, num_pages) are never dereferenced:
+ * their positions are skipped (attention) or not written (append).  Row layout, element
+ * types and 8-bit codes are those of the contiguous cache. */
+
+/* kvattn_cache_write into a paged cache. */
+int kvattn_paged_cache_write(void* pages, float* page_scales, const int* block_table,
+                             int max_pages, int page_rows, int num_pages,
+                             const void* qkv, int B, int NH, int hs,
+                             const int* d_cur_len, int lens_per_seq, int kv_dtype, void* stream);
+
+/* kvattn_decode (append == 0) or kvattn_append_decode (append != 0) on a paged cache.
+ * Strategies: AUTO, SPLIT_MERGE, SPLIT_LASTBLOCK, SINGLE_LAUNCH_GRAPH (no FUSED_SINGLE or
+ * cooperative launch: short contexts take a single segment of the split kernel).  S == 0
+ * plans the segments on the device; S < 0 gives -S rows per segment, a multiple of 64 and
+ * at most 4096.  Workspace: kvattn_workspace_bytes(B, NH, hs, max_pages*page_rows, S). */
+int kvattn_paged_decode(void* out, const void* qkv, void* pages, float* page_scales,
+                        const int* block_table, int max_pages, int page_rows, int num_pages,
+                        int B, int NH, int hs,
+                        const int* d_cur_len, int lens_per_seq, int len_hint,
+                        void* workspace, size_t workspace_bytes,
+                        int S, int strategy, int kv_dtype, int append, void* stream);
+
 /* The decode step's fully connected layer, used after the attention for the output
  * projection: for b < B, m < M
  *   pre = w_scale[m] * sum_k W[m][k] * x[b][k] + bias[m]      (w_scale: 8-bit weights only)

@@ -115,3 +115,32 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(kvattn, "LIB_PATH", str(tmp_path / "libkvattn.so"))
     with pytest.raises(kvattn.KvAttnError):
         kvattn.lib()
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(table=None), 1),               # KVATTN_ERR_NULL_POINTER
+    (dict(table=ALIGNED + 2), 2),        # KVATTN_ERR_MISALIGNED
+    (dict(page_rows=32), 4),             # below one 64-row tile: KVATTN_ERR_SHAPE
+    (dict(page_rows=100), 4),            # not a multiple of 64
+    (dict(max_pages=0), 4),
+    (dict(num_pages=0), 4),
+    (dict(max_pages=1 << 20, page_rows=1 << 10), 4),   # more positions than a cache may hold
+    (dict(strategy=1), 6),               # FUSED_SINGLE: KVATTN_ERR_STRATEGY
+    (dict(strategy=3), 6),               # cooperative
+    (dict(S=8), 8),                      # reference partition: KVATTN_ERR_SPLIT
+    (dict(S=-100), 8),                   # rows per segment not a multiple of 64
+    (dict(S=-8192), 8),                  # more than 4096 rows per segment
+    (dict(len_hint=1 << 20), 12),        # KVATTN_ERR_LENGTH
+])
+def test_paged_decode_argument_errors(kw, status):
+    kvattn = _kv()
+    a = dict(table=ALIGNED, max_pages=16, page_rows=64, num_pages=16, strategy=0, S=0, len_hint=-1)
+    a.update(kw)
+    st = kvattn.lib().kvattn_paged_decode(ALIGNED, ALIGNED, ALIGNED, None, a["table"], a["max_pages"],
+                                          a["page_rows"], a["num_pages"], 1, 12, 64, None, 0, a["len_hint"],
+                                          ALIGNED, 1 << 30, a["S"], a["strategy"], 1, 0, None)
+    assert st == status, kvattn.strerror(st)
+    if "strategy" not in kw and "S" not in kw and "len_hint" not in kw:
+        st = kvattn.lib().kvattn_paged_cache_write(ALIGNED, None, a["table"], a["max_pages"], a["page_rows"],
+                                                   a["num_pages"], ALIGNED, 1, 12, 64, None, 0, 1, None)
+        assert st == status, kvattn.strerror(st)
