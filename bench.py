@@ -287,6 +287,54 @@ class C5:
                 "rows_per_segment": self.plan[2]}
 
 
+class C5Paged:
+    """C5's lengths and shape with a paged cache: 256-row pages, a pool holding only the
+    pages in use, shuffled, addressed through a block table."""
+    B, NH, maxT, P = 64, 12, 8192, 256
+
+    def __init__(self, args, torch, kvattn, dev):
+        import numpy as np
+        self.torch, self.kvattn, self.args = torch, kvattn, args
+        g = torch.Generator(device=dev)
+        g.manual_seed(5)
+        self.lens = torch.randint(1, self.maxT + 1, (self.B,), generator=g, device=dev, dtype=torch.int32)
+        self.cur = (self.lens - 1).contiguous()
+        lens_h = [int(x) for x in self.lens.cpu().tolist()]
+        need = [(L + self.P - 1) // self.P for L in lens_h]
+        self.num_pages = sum(need)
+        perm = np.random.RandomState(3).permutation(self.num_pages)
+        table = np.full((self.B, self.maxT // self.P), -1, np.int32)
+        k = 0
+        for b in range(self.B):
+            table[b, :need[b]] = perm[k:k + need[b]]
+            k += need[b]
+        self.table = torch.from_numpy(table).to(dev)
+        self.pages = torch.empty(self.num_pages * 2 * self.NH * self.P * HD, device=dev, dtype=torch.bfloat16)
+        chunk = 1 << 26
+        for i in range(0, self.pages.numel(), chunk):
+            n = min(chunk, self.pages.numel() - i)
+            self.pages[i:i + n] = torch.randn(n, generator=g, device=dev).to(torch.bfloat16)
+        self.qkv = torch.randn(self.B * 3 * self.NH * HD, generator=g, device=dev).to(torch.bfloat16)
+        self.out = torch.empty(self.B * self.NH * HD, device=dev, dtype=torch.bfloat16)
+        self.cache = kvattn.PagedCache(self.pages, self.table, self.maxT // self.P, self.P, self.num_pages)
+        self.ws = kvattn.Workspace(self.B, self.NH, self.maxT, 0)
+        self.lens_h = lens_h
+
+    def call(self):
+        self.kvattn.paged_decode(self.out, self.qkv, self.cache, self.B, self.NH, HD, kv_dtype="bf16",
+                                 cur_len=self.cur, lens_per_seq=True, **self.ws.kwargs())
+
+    def measure(self):
+        for _ in range(5):
+            self.call()
+        us = timed(self.torch, self.call, self.args.c5_reps) * 1000.0
+        nbytes = bytes_per_call(self.lens_h, self.NH, 2, 2, self.B)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        return {"workload": "C5 with a paged cache: 256-row pages, shuffled pool of the pages in use",
+                "pool_bytes": self.pages.numel() * 2, "bytes_per_call": nbytes, "us_per_call": round(us, 3),
+                "GBps": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def small_config(torch, kvattn, dev, dtype, NH, maxT, T, strategy, S, reps=200):
     """One (B=1) decode-attention call on a warm cache: microseconds per call, measured over
     `reps` back-to-back calls replayed from a HIP graph (eager for the cooperative launch,
@@ -519,6 +567,8 @@ def main():
         k5, t5 = lookup(traffic, kernel_key(c5o.plan, c5o.B, c5o.NH))
         c5["kernel"] = k5
         c5["traffic_bytes_split_kernel"] = t5
+        del c5o
+        c5["paged"] = C5Paged(args, torch, kvattn, dev).measure()
     configs = None if args.no_configs else other_configs(torch, kvattn, dev)
     gemv = None if args.no_configs else gemv_configs(torch, kvattn, dev)
     gemv_cpu = None if (args.no_configs or args.no_cpu) else gemv_cpu_baseline()
