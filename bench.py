@@ -29,6 +29,8 @@ it first copies 256 MiB device to device as the counters' calibration dispatch.
 from __future__ import annotations
 
 import argparse
+import contextlib
+import ctypes
 import json
 import os
 import platform
@@ -65,6 +67,37 @@ def parse():
 def bytes_per_call(lengths, NH, kv_bytes, act_bytes, B):
     """Algorithmic HBM bytes: K+V rows actually attended, plus q in and out."""
     return int(sum(2 * NH * L * HD * kv_bytes for L in lengths) + B * NH * HD * 2 * act_bytes)
+
+
+class _Phases:
+    """roctx ranges around the timed regions, so that a `rocprofv3 --marker-trace` run can
+    attribute kernel dispatches to the workload that made them (no-op without the library)."""
+
+    def __init__(self):
+        self.lib = None
+        for name in ("librocprofiler-sdk-roctx.so.1", "/opt/rocm/lib/librocprofiler-sdk-roctx.so.1"):
+            try:
+                self.lib = ctypes.CDLL(name)
+                break
+            except OSError:
+                continue
+        if self.lib is not None:
+            self.lib.roctxRangePushA.argtypes = [ctypes.c_char_p]
+            self.lib.roctxRangePushA.restype = ctypes.c_int
+            self.lib.roctxRangePop.restype = ctypes.c_int
+
+    @contextlib.contextmanager
+    def __call__(self, name: str):
+        if self.lib is not None:
+            self.lib.roctxRangePushA(name.encode())
+        try:
+            yield
+        finally:
+            if self.lib is not None:
+                self.lib.roctxRangePop()
+
+
+phase = _Phases()
 
 
 def timed(torch, fn, reps):
@@ -106,7 +139,8 @@ class C2:
         torch, a = self.torch, self.args
         for _ in range(a.warmup):
             self.step()
-        eager_ms = timed(torch, self.step, a.steps)
+        with phase("c2_eager_T1024"):
+            eager_ms = timed(torch, self.step, a.steps)
         s = torch.cuda.Stream()
         graph = torch.cuda.CUDAGraph()
         torch.cuda.synchronize()
@@ -115,7 +149,8 @@ class C2:
                 self.step()
         for _ in range(a.warmup):
             graph.replay()
-        graph_ms = timed(torch, graph.replay, a.steps)
+        with phase("c2_graph_T1024"):
+            graph_ms = timed(torch, graph.replay, a.steps)
         return graph_ms, eager_ms
 
     def sweep(self, lengths=(1, 64, 128, 150, 255, 256, 257, 384, 512, 768, 1023, 1024), reps=50):
@@ -276,7 +311,8 @@ class C5:
     def measure(self):
         for _ in range(5):
             self.call()
-        us = timed(self.torch, self.call, self.args.c5_reps) * 1000.0
+        with phase("c5"):
+            us = timed(self.torch, self.call, self.args.c5_reps) * 1000.0
         lh = [int(x) for x in self.lens.cpu().tolist()]
         nbytes = bytes_per_call(lh, self.NH, 2, 2, self.B)
         gbs = nbytes / (us * 1e-6) / 1e9
@@ -327,7 +363,8 @@ class C5Paged:
     def measure(self):
         for _ in range(5):
             self.call()
-        us = timed(self.torch, self.call, self.args.c5_reps) * 1000.0
+        with phase("c5_paged"):
+            us = timed(self.torch, self.call, self.args.c5_reps) * 1000.0
         nbytes = bytes_per_call(self.lens_h, self.NH, 2, 2, self.B)
         gbs = nbytes / (us * 1e-6) / 1e9
         return {"workload": "C5 with a paged cache: 256-row pages, shuffled pool of the pages in use",
@@ -445,7 +482,8 @@ def gemv_configs(torch, kvattn, dev, layers=12, reps=100):
                 with torch.cuda.graph(graph, stream=s):
                     step()
             graph.replay()
-            us = timed(torch, graph.replay, reps) * 1000.0 / layers
+            with phase(f"gemv_{name}_{w_dtype}"):
+                us = timed(torch, graph.replay, reps) * 1000.0 / layers
             nbytes = wbytes + K * 2 + 2 * M * 2
             gbs = nbytes / (us * 1e-6) / 1e9
             res[f"{name}_{w_dtype}_{M}x{K}"] = {"us_per_call": round(us, 3), "bytes_per_call": nbytes,
@@ -467,14 +505,16 @@ def gemv_cpu_baseline(seconds=3.0):
             "kind": "port", "sample": f"oracle_gemv FP32 768x768, B=1, median of {reps} calls"}
 
 
-def kernel_key(plan, B, NH):
-    """(name prefix, grid suffix) of the split kernel a plan launches (BF16 = dtype 1), as
-    keyed in the rocprof summaries: `split_kernel<1, MODE, WAVES, TILE> grid=WORKITEMS`."""
+def kernel_key(plan, B, NH, append=False, paged=False):
+    """(name prefix, grid suffix) of the BF16 split kernel a plan launches, as keyed in the
+    rocprof summaries: `split_kernel<1, MODE, WAVES, TILE, APPEND, PAGED> grid=WORKITEMS`
+    (4 waves and 8-row-chunk tiles for BF16 in both shapes of this build)."""
     st, slots, _ = plan
     mode = {2: 0, 4: 0, 5: 1, 3: 2}.get(st)
     if mode is None:
         return None
-    return f"split_kernel<1, {mode},", f"grid={B * NH * slots * 256}"
+    flags = f"{'true' if append else 'false'}, {'true' if paged else 'false'}"
+    return f"split_kernel<1, {mode}, 4, 8, {flags}>", f"grid={B * NH * slots * 256}"
 
 
 def lookup(traffic, key):
@@ -483,7 +523,7 @@ def lookup(traffic, key):
     for k, v in traffic.items():
         if k.startswith(key[0]) and k.endswith(key[1]):
             return k, v
-    return f"{key[0]} ...> {key[1]}", None
+    return f"{key[0]} {key[1]}", None
 
 
 def cpu_baseline(seconds, c2):
@@ -520,10 +560,36 @@ def pmc_pass(args, torch, kvattn, dev):
     for _ in range(3):
         c2.step()
     torch.cuda.synchronize()
+    # The 12-layer stack with the append fused into the attention launch.
+    ws = kvattn.Workspace(c2.B, c2.NH, c2.maxT, 0)
+    for _ in range(3):
+        for l in range(c2.L):
+            kvattn.append_decode(c2.outs[l], c2.qkvs[l], c2.caches[l], c2.B, c2.NH, HD, c2.maxT, kv_dtype="bf16",
+                                 cur_len=c2.cur, **ws.kwargs())
+    torch.cuda.synchronize()
+    del c2
+    # The fully connected layer: attention output projection (BF16, INT8) and MLP up (BF16).
+    for name, M, K, gelu in GEMV_SHAPES:
+        if name not in ("attproj", "fc"):
+            continue
+        x = torch.randn(K, device=dev).to(torch.bfloat16)
+        out = torch.empty(M, device=dev, dtype=torch.bfloat16)
+        Wb = torch.randn(M * K, device=dev).to(torch.bfloat16)
+        W8 = torch.randint(0, 126, (M * K,), device=dev, dtype=torch.int32).to(torch.uint8)
+        sc = torch.full((M,), 1e-3, device=dev)
+        for _ in range(3):
+            kvattn.gemv(out, Wb, x, 1, M, K, w_dtype="bf16", gelu=gelu)
+            kvattn.gemv(out, W8, x, 1, M, K, w_dtype="int8", w_scale=sc, gelu=gelu)
+        torch.cuda.synchronize()
     if not args.no_c5:
         c5 = C5(args, torch, kvattn, dev)
         for _ in range(3):
             c5.call()
+        torch.cuda.synchronize()
+        del c5
+        c5p = C5Paged(args, torch, kvattn, dev)
+        for _ in range(3):
+            c5p.call()
         torch.cuda.synchronize()
     print("pmc pass done")
 
@@ -569,6 +635,9 @@ def main():
         c5["traffic_bytes_split_kernel"] = t5
         del c5o
         c5["paged"] = C5Paged(args, torch, kvattn, dev).measure()
+        c5["paged"]["kernel"], c5["paged"]["traffic_bytes_split_kernel"] = lookup(
+            traffic, kernel_key(kvattn.plan(C5Paged.B, C5Paged.NH, HD, C5Paged.maxT, kv_dtype="bf16"), C5Paged.B,
+                                C5Paged.NH, paged=True))
     configs = None if args.no_configs else other_configs(torch, kvattn, dev)
     gemv = None if args.no_configs else gemv_configs(torch, kvattn, dev)
     gemv_cpu = None if (args.no_configs or args.no_cpu) else gemv_cpu_baseline()

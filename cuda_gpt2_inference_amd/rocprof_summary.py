@@ -52,22 +52,54 @@ def _key(row) -> str:
     return f"{short_name(row['Kernel_Name'])} grid={grid}"
 
 
-OWN_KERNELS = ("split_kernel", "merge_kernel", "fused_single_kernel", "cache_write")
+OWN_KERNELS = ("split_kernel", "merge_kernel", "fused_single_kernel", "cache_write", "gemv_kernel",
+               "set_len_kernel")
+
+
+def _phases(d: str):
+    """(name, start_ns, end_ns) of the roctx ranges of a --marker-trace run, or []."""
+    files = sorted(glob.glob(os.path.join(d, "**", "*marker_api_trace.csv"), recursive=True))
+    res = []
+    for f in files:
+        with open(f, newline="") as fh:
+            for r in csv.DictReader(fh):
+                name = r.get("Message") or r.get("Marker_Name") or r.get("Function") or ""
+                if not name or name.startswith("roctx"):
+                    continue
+                res.append((name, int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
+    return res
+
+
+def _table(durs) -> list:
+    out = ["| kernel (grid = work-items) | dispatches | avg µs | median µs | min µs | max µs |",
+           "|---|---|---|---|---|---|"]
+    for k, v in sorted(durs.items(), key=lambda kv: -sum(kv[1])):
+        out.append(f"| `{k}` | {len(v)} | {statistics.mean(v):.2f} | {statistics.median(v):.2f} | "
+                   f"{min(v):.2f} | {max(v):.2f} |")
+    return out
 
 
 def trace(d: str, title: str, cmd: str, all_kernels: bool = False) -> str:
     rows = _csv(os.path.join(d, "**", "*kernel_trace.csv"))
     durs = defaultdict(list)
+    spans = []
     for r in rows:
         if not all_kernels and not any(k in r["Kernel_Name"] for k in OWN_KERNELS):
             continue
-        durs[_key(r)].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
-    out = [f"# {title}", "", f"Command: `{cmd}`", "",
-           "| kernel (grid = work-items) | dispatches | avg µs | median µs | min µs | max µs |",
-           "|---|---|---|---|---|---|"]
-    for k, v in sorted(durs.items(), key=lambda kv: -sum(kv[1])):
-        out.append(f"| `{k}` | {len(v)} | {statistics.mean(v):.2f} | {statistics.median(v):.2f} | "
-                   f"{min(v):.2f} | {max(v):.2f} |")
+        t0, t1 = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+        durs[_key(r)].append((t1 - t0) / 1000.0)
+        spans.append((t0, t1, _key(r)))
+    out = [f"# {title}", "", f"Command: `{cmd}`", "", "## All dispatches", ""] + _table(durs)
+    phases = _phases(d)
+    if phases:
+        out += ["", "## Per timed region (roctx ranges around the benchmark's timed loops)", ""]
+        for name, p0, p1 in phases:
+            pd = defaultdict(list)
+            for t0, t1, k in spans:
+                if t0 >= p0 and t1 <= p1:
+                    pd[k].append((t1 - t0) / 1000.0)
+            if pd:
+                out += [f"### `{name}` ({(p1 - p0) / 1000.0:.1f} µs)", ""] + _table(pd) + [""]
     return "\n".join(out) + "\n"
 
 
