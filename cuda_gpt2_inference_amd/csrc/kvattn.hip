@@ -33,6 +33,7 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <tuple>
@@ -1134,6 +1135,11 @@ __global__ __launch_bounds__(kBlock) void cache_write_w8_kernel(uint8_t* __restr
 
 __device__ int g_cur_len = 0;
 
+// Zero n 32-bit words (grid-stride).
+__global__ __launch_bounds__(kBlock) void zero_words_kernel(uint32_t* __restrict__ p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (size_t)gridDim.x * kBlock) p[i] = 0u;
+}
+
 // Stream-ordered write of the device length (one lane, one vector store).
 __global__ __launch_bounds__(kWave) void set_len_kernel(int* __restrict__ p, int v) {
     if (threadIdx.x == 0) *p = v;
@@ -1788,7 +1794,14 @@ size_t kvattn_workspace_bytes(int B, int NH, int hs, int maxT, int S) {
 
 int kvattn_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
     if (!workspace) return KVATTN_ERR_NULL_POINTER;
-    KV_HIP(hipMemsetAsync(workspace, 0, workspace_bytes, (hipStream_t)stream));
+    if (!aligned16(workspace)) return KVATTN_ERR_MISALIGNED;
+    // A fill kernel rather than hipMemsetAsync, so that the call may also sit in a graph.
+    const size_t words = workspace_bytes / 4;
+    if (words == 0) return KVATTN_OK;
+    const size_t blocks = std::min<size_t>((words + kBlock - 1) / kBlock, 4096);
+    hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, (hipStream_t)stream,
+                       (uint32_t*)workspace, words);
+    KV_HIP(hipGetLastError());
     return KVATTN_OK;
 }
 

@@ -148,8 +148,8 @@ int kvattn_merge(void* out, const float* part_out, const float* part_lse,
 size_t kvattn_workspace_bytes(int B, int NH, int hs, int maxT, int S);
 
 /* Zero the workspace's merge counters.  Call once after allocating a workspace and
- * before the first kvattn_decode on it (outside any graph capture); the kernels leave the
- * counters at zero after every call. */
+ * before the first kvattn_decode on it; the kernels leave the counters at zero after
+ * every call.  Enqueues one fill kernel (no hipMemsetAsync), so it may also be captured. */
 int kvattn_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
 
 /* The launch plan kvattn_decode would use for these arguments, without launching:

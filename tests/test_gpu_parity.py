@@ -326,6 +326,35 @@ def test_graph_capture_replay_tracks_device_length(dev):
         out.fill_(float("nan"))
 
 
+def test_workspace_init_zeroes_eager_and_in_graph(dev):
+    """kvattn_workspace_init zeroes exactly the bytes it is given (not the guard bytes after
+    them) with a fill kernel, so it may also be captured: the graph is replayed several
+    times, the buffer dirtied again by eager work between replays, and every replay checked."""
+    import torch
+    kvattn = _kv()
+    n = kvattn.workspace_bytes(3, 5, HS, 777, 0) + 4     # not a multiple of 256
+    buf = torch.full((n + 256,), 0x5A, dtype=torch.uint8, device=dev)
+
+    def check(where):
+        torch.cuda.synchronize()
+        assert int(buf[:n].count_nonzero()) == 0, f"{where}: workspace not zeroed"
+        assert bool((buf[n:] == 0x5A).all()), f"{where}: wrote past the workspace"
+
+    kvattn.workspace_init(buf, n)
+    check("eager")
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            kvattn.workspace_init(buf, n, stream=s)
+    for i in range(3):
+        buf[:n].fill_(0x5A)
+        torch.cuda.synchronize()
+        g.replay()
+        check(f"replay {i}")
+
+
 def test_coop_refused_inside_capture(dev):
     import torch
     kvattn = _kv()
