@@ -25,6 +25,8 @@ Inputs are synthetic (seeded N(0,1)) and resident in HBM before any timed region
 Modes: default = the measurement above.  `--mode pmc` runs the workloads a few times
 without timing, for `rocprofv3 --pmc FETCH_SIZE|WRITE_SIZE -- python3 bench.py --mode pmc`;
 it first copies 256 MiB device to device as the counters' calibration dispatch.
+`--mode cache` prints the working-set sweep of cache_sweep() (the Infinity Cache regime,
+measured by timing the same calls over more and more distinct KV copies).
 """
 from __future__ import annotations
 
@@ -51,7 +53,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200, help="timed decode steps (12 calls each)")
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--mode", choices=["full", "pmc"], default="full")
+    p.add_argument("--mode", choices=["full", "pmc", "cache"], default="full")
     p.add_argument("--strategy", default="auto")
     p.add_argument("--S", type=int, default=0, help="0 auto, >0 reference partition, <0 rows/segment")
     p.add_argument("--c5-reps", type=int, default=50)
@@ -594,6 +596,107 @@ def pmc_pass(args, torch, kvattn, dev):
     print("pmc pass done")
 
 
+def cache_sweep(torch, kvattn, dev, reps=40):
+    """Infinity Cache regime, from timing: MI355X exposes no MALL counter to rocprofv3 here,
+    so the same calls are replayed over N distinct copies of their KV caches and the bytes
+    one replay touches grow past the L2 (4 MB per XCD, 32 MB in all) and the 256 MB
+    Infinity Cache into HBM.
+      stack  the GPT-2 12-layer BF16 stack at T=1024 (37.8 MB of KV per copy): one graph of N
+             decode steps, step i over copy i; microseconds per call
+      batch  B=16 sequences x NH=12 at T=1024, BF16 (50.3 MB per call): one graph of N calls,
+             call i over copy i; microseconds per call and GB/s
+    Each also reports single calls after a 512 MiB flush (cold: HBM only)."""
+    def graph_of(fn):
+        s = torch.cuda.Stream()
+        g = torch.cuda.CUDAGraph()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                fn()
+        return g
+
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+
+    def cold(call, n=30):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ts = []
+        for r in range(n):
+            flush.fill_(r & 0xFF)
+            e0.record()
+            call()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1000.0)
+        ts.sort()
+        return ts[len(ts) // 2]
+
+    out = {}
+    g = torch.Generator(device=dev)
+    g.manual_seed(9)
+    # The 12-layer stack.
+    L, B, NH, maxT, T = 12, 1, 12, 1024, 1024
+    ns = (1, 2, 4, 6, 8, 12, 16)
+    per_layer = 2 * B * NH * maxT * HD
+    caches = [[torch.randn(per_layer, generator=g, device=dev).to(torch.bfloat16) for _ in range(L)]
+              for _ in range(max(ns))]
+    qkvs = [torch.randn(B * 3 * NH * HD, generator=g, device=dev).to(torch.bfloat16) for _ in range(L)]
+    outs = [torch.empty(B * NH * HD, device=dev, dtype=torch.bfloat16) for _ in range(L)]
+    cur = torch.tensor([T - 1], dtype=torch.int32, device=dev)
+    ws = kvattn.Workspace(B, NH, maxT, 0)
+
+    def stack_call(c, l):
+        kvattn.decode(outs[l], qkvs[l], caches[c][l], B, NH, HD, maxT, kv_dtype="bf16", cur_len=cur,
+                      len_hint=T - 1, **ws.kwargs())
+
+    rows = []
+    for n in ns:
+        graph = graph_of(lambda: [stack_call(c, l) for c in range(n) for l in range(L)])
+        for _ in range(5):
+            graph.replay()
+        with phase(f"cache_stack_N{n}"):
+            ms = timed(torch, graph.replay, reps)
+        rows.append({"copies": n, "working_set_MB": round(n * L * per_layer * 2 / 1e6, 1),
+                     "us_per_call": round(ms * 1000.0 / (n * L), 3)})
+        del graph
+    with phase("cache_stack_cold"):
+        stack_cold = cold(lambda: stack_call(0, 0))
+    out["stack"] = {"rows": rows, "cold_us_per_call": round(stack_cold, 3),
+                    "plan": list(kvattn.plan(B, NH, HD, maxT, kv_dtype="bf16", len_hint=T - 1))}
+    del caches
+    # The bandwidth-bound batch.
+    B = 16
+    ns = (1, 2, 3, 4, 5, 6, 8, 12, 16, 24)
+    per_call = 2 * B * NH * maxT * HD
+    caches = [torch.randn(per_call, generator=g, device=dev).to(torch.bfloat16) for _ in range(max(ns))]
+    qkv = torch.randn(B * 3 * NH * HD, generator=g, device=dev).to(torch.bfloat16)
+    o = torch.empty(B * NH * HD, device=dev, dtype=torch.bfloat16)
+    ws = kvattn.Workspace(B, NH, maxT, 0)
+    nbytes = bytes_per_call([T] * B, NH, 2, 2, B)
+
+    def batch_call(c):
+        kvattn.decode(o, qkv, caches[c], B, NH, HD, maxT, kv_dtype="bf16", cur_len=cur, len_hint=T - 1,
+                      **ws.kwargs())
+
+    rows = []
+    for n in ns:
+        graph = graph_of(lambda: [batch_call(c) for c in range(n)])
+        for _ in range(5):
+            graph.replay()
+        with phase(f"cache_batch_N{n}"):
+            ms = timed(torch, graph.replay, reps)
+        us = ms * 1000.0 / n
+        rows.append({"copies": n, "working_set_MB": round(n * per_call * 2 / 1e6, 1), "us_per_call": round(us, 3),
+                     "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)})
+        del graph
+    with phase("cache_batch_cold"):
+        batch_cold = cold(lambda: batch_call(0))
+    out["batch"] = {"rows": rows, "bytes_per_call": nbytes, "cold_us_per_call": round(batch_cold, 3),
+                    "cold_GBps": round(nbytes / (batch_cold * 1e-6) / 1e9, 1),
+                    "plan": list(kvattn.plan(B, NH, HD, maxT, kv_dtype="bf16", len_hint=T - 1))}
+    del caches, flush
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -610,6 +713,10 @@ def main():
     torch.cuda.set_device(dev)
     if args.mode == "pmc":
         pmc_pass(args, torch, kvattn, dev)
+        return
+    if args.mode == "cache":
+        print(json.dumps({"mode": "cache", "cache_sweep": cache_sweep(torch, kvattn, dev),
+                          "gpu": torch.cuda.get_device_name(dev)}))
         return
 
     from cuda_gpt2_inference_amd.rocprof_summary import read_traffic

@@ -57,6 +57,7 @@ constexpr int kMaxPagedSegRows = 4096;  // paged caches: at most 64 tiles per wa
 constexpr int kMaxSegments = 1 << 16;   // upper bound on segments per (b,h)
 constexpr int kMaxT = 1 << 23;          // keeps per-slot byte offsets inside 32 bits
 constexpr size_t kFusedMaxLds = 64 * 1024;  // dynamic LDS of fused_single (scores)
+constexpr int kMaxDesignatedSegments = 64;  // the designated merger follows one segment per lane
 
 // ------------------------------------------------------------------------------------
 // Per-dtype row geometry.
@@ -725,7 +726,7 @@ __global__ __launch_bounds__(kThreads) void fused_single_kernel(
 // ------------------------------------------------------------------------------------
 // Split kernels.
 // ------------------------------------------------------------------------------------
-enum SplitMode { kPartialsOnly = 0, kLastBlockMerge = 1, kCoopMerge = 2 };
+enum SplitMode { kPartialsOnly = 0, kLastBlockMerge = 1, kCoopMerge = 2, kDesignated = 3 };
 
 struct SplitArgs {
     void* out;
@@ -733,6 +734,11 @@ struct SplitArgs {
     float* part_lse;
     float* part_max;
     unsigned* counters;
+    // Designated merger: the tagged partials (64-bit words: the value in the low half, 1 in
+    // the high half once written in the current call, 0 otherwise):
+    // tag_ml[2 * slot] = {max (natural log units), exp-sum}, tag_out[slot * 64 + c].
+    unsigned long long* tag_ml;
+    unsigned long long* tag_out;
     const void* qkv;
     const uint8_t* kv;
     const float* kv_scale;
@@ -758,7 +764,9 @@ struct Item {
 
 __host__ __device__ __forceinline__ int ceil_div_i(int a, int b) { return (a + b - 1) / b; }
 
-constexpr int kDevicePlan = -1;
+constexpr int kDevicePlan = -1;     // rows from planned_rows() of the device length
+constexpr int kDevicePlanDes = -2;  // rows from designated_rows() of the device length
+constexpr int kDesignatedRows = 128;
 
 // Rows per segment for an attended length of `total`: the whole length in one segment up
 // to kFusedMaxRows positions, otherwise about four segments of a power-of-two length
@@ -773,10 +781,21 @@ __host__ __device__ __forceinline__ int planned_rows(int total) {
     return r;
 }
 
+// Rows per segment for the designated merger: the whole length in one segment up to
+// kFusedMaxRows positions, otherwise 128-row segments (more segments cut the streaming
+// time per workgroup and cost the merger nothing extra while they fit one poll), longer
+// ones (powers of two) only where 128 rows would make more than 64 segments.
+__host__ __device__ __forceinline__ int designated_rows(int total) {
+    if (total <= kFusedMaxRows) return total > 0 ? total : 1;
+    int r = kDesignatedRows;
+    while ((long long)r * kMaxDesignatedSegments < total) r <<= 1;
+    return r;
+}
+
 // Segments of a (b,h) whose length is `total` under fixed or device-planned rows
 // (seg_rows != 0); `rows` receives the segment length.
 __device__ __forceinline__ int seg_count(int seg_rows, int total, int& rows) {
-    rows = seg_rows > 0 ? seg_rows : planned_rows(total);
+    rows = seg_rows > 0 ? seg_rows : (seg_rows == kDevicePlanDes ? designated_rows(total) : planned_rows(total));
     return ceil_div_i(total, rows);
 }
 
@@ -829,6 +848,20 @@ __device__ __forceinline__ bool locate(const SplitArgs& a, int x, Item& it) {
     }
     return false;
 }
+
+// Tagged partial words of the designated merger (agent-scope relaxed atomics, emitted as
+// coherent sc1 stores and loads on gfx950).
+constexpr unsigned long long kWordValid = 1ull << 32;
+constexpr int kMergePolls = 1 << 22;  // bound on the designated merger's polls (seconds)
+__device__ __forceinline__ void put_word(unsigned long long* p, unsigned long long w) {
+    __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long get_word(const unsigned long long* p) {
+    return __hip_atomic_load(const_cast<unsigned long long*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long valid_word(float v) { return kWordValid | __float_as_uint(v); }
+__device__ __forceinline__ bool word_valid(unsigned long long w) { return (w >> 32) == 1u; }
+__device__ __forceinline__ float word_value(unsigned long long w) { return __uint_as_float((uint32_t)w); }
 
 // Partials of the in-kernel merge travel between workgroups that may sit on different
 // XCDs (each with its own L2).  They are written and read as agent-scope relaxed atomics,
@@ -946,20 +979,28 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
     const int bh = it.b * a.NH + it.h;
     const size_t pidx = (size_t)bh * a.S + it.s;
     constexpr bool kCoh = kMode == kLastBlockMerge;
+    constexpr bool kDes = kMode == kDesignated;
 
-    if (active) {
-        int j0, j1;
+    // Rows [sj0, sj1) of segment s of this (b,h).
+    auto seg_range = [&](int s, int& sj0, int& sj1) {
         if (a.seg_rows != 0) {
-            j0 = it.s * it.rows;
-            j1 = min(j0 + it.rows, it.total);
+            sj0 = s * it.rows;
+            sj1 = min(sj0 + it.rows, it.total);
         } else {
             const int chunk = ceil_div_i(it.total, a.S);
-            j0 = it.s * chunk;
-            j1 = min(j0 + chunk, it.total);
+            sj0 = s * chunk;
+            sj1 = min(sj0 + chunk, it.total);
         }
+    };
+    int j0 = 0, j1 = 0;
+    if (active) seg_range(it.s, j0, j1);
+
+
+    if (active) {
         if (j1 <= j0) {
-            // Empty segment (reference partition with total < S): neutral partial.
-            if (wave == 0) {
+            // Empty segment (reference partition with total < S): neutral partial (the
+            // designated merger skips empty segments instead).
+            if (!kDes && wave == 0) {
                 put<kCoh>(a.part_out + pidx * kHeadDim + lane, 0.0f);
                 if (lane == 0) { put<kCoh>(a.part_max + pidx, kEmptyMax); put<kCoh>(a.part_lse + pidx, 0.0f); }
             }
@@ -968,14 +1009,17 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
             float m = kStartMax, l = 0.0f, acc[R::kElems];
 #pragma unroll
             for (int e = 0; e < R::kElems; ++e) acc[e] = 0.0f;
+            Slot sl{};
+            FreshDst fd{};
+            PagedView pv{};
             if constexpr (kPaged) {
                 q0 = load_q<DT>(a.qkv, it.b, it.h, a.NH, slice);
                 if constexpr (kFresh) fr = load_fresh<DT>(a.qkv, it.b, it.h, a.NH, slice);
-                const PagedView pv{a.kv, a.kv_scale, a.table, a.max_pages, a.page_rows, a.num_pages, a.NH};
+                pv = PagedView{a.kv, a.kv_scale, a.table, a.max_pages, a.page_rows, a.num_pages, a.NH};
                 online_tiles_paged<DT, kU, kW, kFresh>(pv, it.b, it.h, j0, j1, wave, slot_row, slice, q0, a.qscale,
                                                        fr, a.kv_out, a.kv_scale_out, cur, m, l, acc);
             } else {
-                const Slot sl = make_slot<DT>(a.kv, a.kv_scale, a.B, a.NH, a.maxT, bh, slice);
+                sl = make_slot<DT>(a.kv, a.kv_scale, a.B, a.NH, a.maxT, bh, slice);
                 if (spec) {
                     w1 = min(w1, j1);
                 } else {
@@ -986,7 +1030,6 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                     q0 = load_q<DT>(a.qkv, it.b, it.h, a.NH, slice);
                     if constexpr (kFresh) fr = load_fresh<DT>(a.qkv, it.b, it.h, a.NH, slice);
                 }
-                FreshDst fd{};
                 if constexpr (kFresh)
                     fd = fresh_dst(a.kv_out, a.kv_scale_out, a.B, a.NH, a.maxT, bh, slice, cur);
                 online_rows_from<DT, kU, kFresh>(t0, q0, sl, w0, w1, slot_row, a.qscale, fr, fd, cur, m, l, acc);
@@ -1015,9 +1058,90 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                     L = fmaf(g, s_l[w], L);
                     A = fmaf(g, s_acc[w][lane], A);
                 }
-                if (kMode == kLastBlockMerge && it.n_seg == 1) {
+                if ((kMode == kLastBlockMerge || kDes) && it.n_seg == 1) {
                     // The only segment of its (b,h): the result needs no merge.
                     store_out<DT>(a.out, (size_t)bh * kHeadDim + lane, A / L);
+                } else if constexpr (kDes) {
+                    if (it.s != 0) {
+                        // Producer: publish the tagged partial and finish; nothing waits.
+                        put_word(a.tag_out + pidx * kHeadDim + lane, valid_word(A));
+                        if (lane == 0) {
+                            put_word(a.tag_ml + 2 * pidx, valid_word(Mb * kLn2));
+                            put_word(a.tag_ml + 2 * pidx + 1, valid_word(L));
+                        }
+                    } else {
+                        // Designated merger (segment 0): lane u follows segment u.  A head's
+                        // segments have consecutive workgroup ids with segment 0 first, and
+                        // workgroups are dispatched in id order, so the producers waited for are
+                        // already resident or next in line behind workgroups that do not wait:
+                        // the polls end.  The bound only guards against that order failing.
+                        const int n = it.n_seg;
+                        const size_t p0 = (size_t)bh * a.S;
+                        bool lost = n > kMaxDesignatedSegments;
+                        int uj0 = 0, uj1 = 0;
+                        if (lane < n) seg_range(lane, uj0, uj1);
+                        const bool need = lane >= 1 && lane < n && uj1 > uj0 && !lost;
+                        const unsigned long long prod = __ballot(need);   // segments a producer publishes
+                        // Channel words of up to 16 segments per batch; the first batch is
+                        // requested together with the maxima and exp-sums, so up to 17
+                        // segments merge after one memory round trip.
+                        constexpr int kBatch = 16;
+                        auto load_batch = [&](int k, unsigned long long (&w)[kBatch]) {
+#pragma unroll
+                            for (int u = 0; u < kBatch; ++u)
+                                w[u] = k + u < n && ((prod >> (k + u)) & 1ull)
+                                           ? get_word(a.tag_out + (p0 + k + u) * kHeadDim + lane)
+                                           : kWordValid;
+                        };
+                        auto batch_valid = [&](const unsigned long long (&w)[kBatch]) {
+                            bool ok = true;
+#pragma unroll
+                            for (int u = 0; u < kBatch; ++u) ok = ok && word_valid(w[u]);
+                            return ok;
+                        };
+                        unsigned long long wm = kWordValid, wl = kWordValid, w[kBatch];
+                        for (int r = 0;; ++r) {
+                            if (need) {
+                                wm = get_word(a.tag_ml + 2 * (p0 + lane));
+                                wl = get_word(a.tag_ml + 2 * (p0 + lane) + 1);
+                            }
+                            load_batch(1, w);
+                            if (__all(word_valid(wm) && word_valid(wl) && batch_valid(w))) break;
+                            if (r >= kMergePolls) { lost = true; break; }
+                        }
+                        // Merge this wave's partial (segment 0) and the producers' partials, in
+                        // segment order, with merge_partials' arithmetic.
+                        const float pm = lane == 0 ? Mb * kLn2 : (need ? word_value(wm) : kEmptyMax);
+                        const float pl = lane == 0 ? L : (need ? word_value(wl) : 0.0f);
+                        const float Mx = wave_max(pm);
+                        const float LL = wave_sum(exp2_fast((pm - Mx) * kLog2e) * pl);
+                        const float e = exp2_fast((pm - Mx) * kLog2e);
+                        float O = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), 0)) * A;
+                        for (int k = 1; k < n && !lost; k += kBatch) {
+                            if (k > 1) {
+                                for (int r = 0;; ++r) {
+                                    load_batch(k, w);
+                                    if (__all(batch_valid(w))) break;
+                                    if (r >= kMergePolls) { lost = true; break; }
+                                }
+                            }
+#pragma unroll
+                            for (int u = 0; u < kBatch; ++u)
+                                if (k + u < n)
+                                    O = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), k + u)),
+                                             word_value(w[u]), O);
+                        }
+                        store_out<DT>(a.out, (size_t)bh * kHeadDim + lane, lost ? __builtin_nanf("") : O / LL);
+                        // Leave the producers' slots empty for the next call.
+                        for (unsigned long long clr = prod; clr; clr &= clr - 1) {
+                            const int u = __ffsll((long long)clr) - 1;
+                            put_word(a.tag_out + (p0 + u) * kHeadDim + lane, 0ull);
+                        }
+                        if (need) {
+                            put_word(a.tag_ml + 2 * (p0 + lane), 0ull);
+                            put_word(a.tag_ml + 2 * (p0 + lane) + 1, 0ull);
+                        }
+                    }
                 } else {
                     put<kCoh>(a.part_out + pidx * kHeadDim + lane, A);
                     if (lane == 0) { put<kCoh>(a.part_max + pidx, Mb * kLn2); put<kCoh>(a.part_lse + pidx, L); }
@@ -1245,6 +1369,7 @@ template <int DT, int W, int U, bool kFresh, bool kPaged>
 const void* split_ptr_mode(int mode) {
     if (mode == kPartialsOnly) return (const void*)&split_kernel<DT, kPartialsOnly, W, U, kFresh, kPaged>;
     if (mode == kLastBlockMerge) return (const void*)&split_kernel<DT, kLastBlockMerge, W, U, kFresh, kPaged>;
+    if (mode == kDesignated) return (const void*)&split_kernel<DT, kDesignated, W, U, kFresh, kPaged>;
     if constexpr (kPaged) return nullptr;
     else return (const void*)&split_kernel<DT, kCoopMerge, W, U, kFresh, false>;
 }
@@ -1403,12 +1528,18 @@ int launch_graph_pair(const SplitArgs& a, int kv_dtype, bool lat, hipStream_t st
     return KVATTN_OK;
 }
 
-// Workspace: [counters B*NH u32][part_max][part_lse][part_out], each 256-byte aligned.
+// Workspace, every region 256-byte aligned:
+//   counters [B*NH] u32                       last-block merge
+//   part_max, part_lse [B*NH*S] f32, part_out [B*NH*S*64] f32   reference-format partials
+//   tag_ml [B*NH*S*2] u64, tag_out [B*NH*S*64] u64   designated merger
+// kvattn_workspace_init zeroes it once; every kernel leaves the counters and tags at 0.
 struct Workspace {
     unsigned* counters;
     float* part_max;
     float* part_lse;
     float* part_out;
+    unsigned long long* tag_ml;
+    unsigned long long* tag_out;
     size_t bytes;
 };
 
@@ -1417,13 +1548,17 @@ Workspace carve(void* base, int B, int NH, int S) {
     const size_t nc = align_up(bh * sizeof(unsigned), 256);
     const size_t nm = align_up(bh * S * sizeof(float), 256);
     const size_t no = align_up(bh * S * kHeadDim * sizeof(float), 256);
+    const size_t ntm = align_up(bh * S * 2 * sizeof(unsigned long long), 256);
+    const size_t nto = align_up(bh * S * kHeadDim * sizeof(unsigned long long), 256);
     Workspace w;
     uint8_t* p = (uint8_t*)base;
     w.counters = (unsigned*)p;
     w.part_max = (float*)(p + nc);
     w.part_lse = (float*)(p + nc + nm);
     w.part_out = (float*)(p + nc + 2 * nm);
-    w.bytes = nc + 2 * nm + no;
+    w.tag_ml = (unsigned long long*)(p + nc + 2 * nm + no);
+    w.tag_out = (unsigned long long*)(p + nc + 2 * nm + no + ntm);
+    w.bytes = nc + 2 * nm + no + ntm + nto;
     return w;
 }
 
@@ -1458,6 +1593,12 @@ int auto_seg_rows(int total_hint) {
 // Segment slots that cover planned_rows() at every length up to maxT: one segment up to
 // kFusedMaxRows positions, at most four while planned_rows(total) >= total / 4, and
 // ceil(total / kMaxSegRows) beyond.
+// Segment slots covering designated_rows() at every length up to maxT.
+int designated_slots(int maxT) {
+    if (maxT <= kFusedMaxRows) return 1;
+    return std::min(kMaxDesignatedSegments, ceil_div_i(maxT, kDesignatedRows));
+}
+
 int planned_slots(int maxT) {
     if (maxT <= kFusedMaxRows) return 1;
     const int s = ceil_div_i(maxT, kMaxSegRows);
@@ -1481,13 +1622,14 @@ bool latency_bound(int B, int NH, int total_rows) { return (long long)B * NH * t
 // segments start at multiples of 64 rows (the tile), so rows per segment are planned on
 // the device unless S < 0 gives a multiple of 64.
 int make_plan(int B, int NH, int maxT, int len_hint, int S, int strategy, Plan& p, bool paged = false) {
-    if (strategy < KVATTN_AUTO || strategy > KVATTN_SPLIT_LASTBLOCK) return KVATTN_ERR_STRATEGY;
+    if (strategy < KVATTN_AUTO || strategy > KVATTN_SPLIT_DESIGNATED) return KVATTN_ERR_STRATEGY;
     if (len_hint >= maxT || len_hint < -1) return KVATTN_ERR_LENGTH;
     if (paged) {
         if (strategy == KVATTN_FUSED_SINGLE || strategy == KVATTN_SINGLE_LAUNCH_COOP) return KVATTN_ERR_STRATEGY;
         if (S > 0 || (S < 0 && ((-S) % kMinSegRows != 0 || -S > kMaxPagedSegRows))) return KVATTN_ERR_SPLIT;
     }
     const int total_hint = (len_hint < 0 ? maxT - 1 : len_hint) + 1;
+    const bool auto_strategy = strategy == KVATTN_AUTO;
     if (strategy == KVATTN_AUTO) {
         // Short contexts: one workgroup per (b,h).  Otherwise split; a single launch with
         // the in-kernel merge while the whole call is latency bound, and split + merge
@@ -1495,7 +1637,7 @@ int make_plan(int B, int NH, int maxT, int len_hint, int S, int strategy, Plan& 
         const bool fits = (size_t)maxT * sizeof(float) <= kFusedMaxLds;
         if (!paged && fits && total_hint <= kFusedMaxRows) strategy = KVATTN_FUSED_SINGLE;
         else if ((long long)B * NH * total_hint >= kStreamRows) strategy = KVATTN_SPLIT_MERGE;
-        else strategy = KVATTN_SPLIT_LASTBLOCK;
+        else strategy = KVATTN_SPLIT_DESIGNATED;
     }
     p.strategy = strategy;
     p.lat = latency_bound(B, NH, total_hint);
@@ -1505,14 +1647,25 @@ int make_plan(int B, int NH, int maxT, int len_hint, int S, int strategy, Plan& 
         return KVATTN_OK;
     }
     KV_TRY(segment_slots(maxT, S, p.slots, p.seg_rows));
+    const bool des = strategy == KVATTN_SPLIT_DESIGNATED;
     if (S == 0 && (len_hint < 0 || paged)) {
-        p.seg_rows = kDevicePlan;
-        p.slots = planned_slots(maxT);
+        p.seg_rows = des ? kDevicePlanDes : kDevicePlan;
+        p.slots = des ? designated_slots(maxT) : planned_slots(maxT);
     } else if (S == 0) {
-        p.seg_rows = auto_seg_rows(total_hint);
+        // Rows fixed from the hint; the grid covers every device length up to maxT, so the
+        // designated merger also needs rows >= maxT / 64.
+        p.seg_rows = des ? std::max(designated_rows(total_hint), designated_rows(maxT)) : auto_seg_rows(total_hint);
         p.slots = ceil_div_i(maxT, p.seg_rows);
     }
     if ((long long)B * NH * p.slots >= (1ll << 31)) return KVATTN_ERR_SHAPE;
+    const bool des_fits = p.slots <= kMaxDesignatedSegments &&
+                          !(paged && p.seg_rows == kDevicePlanDes && designated_rows(maxT) > kMaxPagedSegRows);
+    if (des && !des_fits) {
+        // More segments per (b,h) than the merger follows (or longer paged segments than a
+        // wave walks): AUTO takes the last-block merge with its own segmentation.
+        if (!auto_strategy) return KVATTN_ERR_SPLIT;
+        return make_plan(B, NH, maxT, len_hint, S, KVATTN_SPLIT_LASTBLOCK, p, paged);
+    }
     return KVATTN_OK;
 }
 
@@ -1549,6 +1702,8 @@ int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scal
     a.part_lse = w.part_lse;
     a.part_max = w.part_max;
     a.counters = w.counters;
+    a.tag_ml = w.tag_ml;
+    a.tag_out = w.tag_out;
     a.qkv = qkv;
     a.kv = (const uint8_t*)kv;
     a.kv_scale = kv_scale;
@@ -1575,6 +1730,7 @@ int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scal
             KV_TRY(launch_split(a, kv_dtype, kPartialsOnly, plan.lat, stream));
             return launch_merge(a, kv_dtype, stream);
         case KVATTN_SPLIT_LASTBLOCK: return launch_split(a, kv_dtype, kLastBlockMerge, plan.lat, stream);
+        case KVATTN_SPLIT_DESIGNATED: return launch_split(a, kv_dtype, kDesignated, plan.lat, stream);
         case KVATTN_SINGLE_LAUNCH_COOP: return launch_coop(a, kv_dtype, plan.lat, stream);
         case KVATTN_SINGLE_LAUNCH_GRAPH: return launch_graph_pair(a, kv_dtype, plan.lat, stream);
         default: return KVATTN_ERR_STRATEGY;
@@ -1815,7 +1971,7 @@ int kvattn_plan(int B, int NH, int hs, int maxT, int len_hint, int S, int strate
     KV_TRY(make_plan(B, NH, maxT, len_hint, S, strategy, p));
     *strategy_out = p.strategy;
     *segments_out = p.slots;
-    *seg_rows_out = p.seg_rows;
+    *seg_rows_out = p.seg_rows < 0 ? -1 : p.seg_rows;
     return KVATTN_OK;
 }
 

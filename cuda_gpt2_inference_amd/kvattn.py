@@ -53,6 +53,7 @@ SPLIT_MERGE = 2
 SINGLE_LAUNCH_COOP = 3
 SINGLE_LAUNCH_GRAPH = 4
 SPLIT_LASTBLOCK = 5
+SPLIT_DESIGNATED = 6
 STRATEGIES = {
     "auto": AUTO,
     "fused_single": FUSED_SINGLE,
@@ -60,6 +61,7 @@ STRATEGIES = {
     "coop": SINGLE_LAUNCH_COOP,
     "graph": SINGLE_LAUNCH_GRAPH,
     "lastblock": SPLIT_LASTBLOCK,
+    "designated": SPLIT_DESIGNATED,
 }
 
 HEAD_DIM = 64

@@ -68,8 +68,13 @@ typedef enum kvattn_strategy {
     KVATTN_SPLIT_MERGE = 2,         /* flash-decoding: split kernel + merge kernel */
     KVATTN_SINGLE_LAUNCH_COOP = 3,  /* split + grid barrier + merge, cooperative launch */
     KVATTN_SINGLE_LAUNCH_GRAPH = 4, /* split + merge pair replayed as one hipGraph launch */
-    KVATTN_SPLIT_LASTBLOCK = 5      /* split kernel whose last finishing segment of each
+    KVATTN_SPLIT_LASTBLOCK = 5,     /* split kernel whose last finishing segment of each
                                        (b,h) merges: one ordinary launch, capturable */
+    KVATTN_SPLIT_DESIGNATED = 6     /* split kernel in which segment 0 of each (b,h) merges:
+                                       the other segments publish tagged partials and finish,
+                                       segment 0 polls for them; one ordinary launch,
+                                       capturable; at most 64 segments per (b,h).  AUTO's
+                                       choice for latency-bound calls. */
 } kvattn_strategy;
 
 /* Human-readable text of a status code. */

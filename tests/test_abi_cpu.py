@@ -51,11 +51,13 @@ def test_strerror_covers_every_status():
 
 def test_workspace_bytes():
     kvattn = _kv()
-    # counters (B*NH u32), part_max, part_lse (B*NH*S f32), part_out (B*NH*S*64 f32),
-    # every region rounded up to 256 bytes.
+    # counters (B*NH u32), part_max, part_lse (B*NH*S f32), part_out (B*NH*S*64 f32), the
+    # designated merger's tagged words (B*NH*S*2 and B*NH*S*64 u64), every region rounded up
+    # to 256 bytes.
     def expect(B, NH, S):
         up = lambda x: (x + 255) // 256 * 256  # noqa: E731
-        return up(B * NH * 4) + 2 * up(B * NH * S * 4) + up(B * NH * S * 64 * 4)
+        return (up(B * NH * 4) + 2 * up(B * NH * S * 4) + up(B * NH * S * 64 * 4)
+                + up(B * NH * S * 2 * 8) + up(B * NH * S * 64 * 8))
     assert kvattn.workspace_bytes(1, 12, 64, 1024, 8) == expect(1, 12, 8)
     assert kvattn.workspace_bytes(64, 12, 64, 8192, 0) == expect(64, 12, 8192 // 64)
     assert kvattn.workspace_bytes(2, 3, 64, 1000, -100) == expect(2, 3, 10)

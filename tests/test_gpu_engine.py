@@ -38,7 +38,7 @@ def test_device_plan_uniform_length(dev, dtype):
     qkv, cache, scale, _ = to_device(case, dev)
     cur = torch.zeros(1, dtype=torch.int32, device=dev)
     ws = kvattn.Workspace(B, NH, maxT, 0)
-    for strategy in ("auto", "lastblock", "split_merge", "graph", "coop"):
+    for strategy in ("auto", "lastblock", "designated", "split_merge", "graph", "coop"):
         assert kvattn.plan(B, NH, HS, maxT, kv_dtype=dtype, strategy=strategy)[2] == -1
         for total in PLAN_EDGES:
             cur.fill_(total - 1)
@@ -60,7 +60,7 @@ def test_device_plan_ragged_lengths(dev, dtype):
     qkv, cache, scale, cur = to_device(case, dev)
     ref = case.reference()
     ws = kvattn.Workspace(B, NH, maxT, 0)
-    for strategy in ("auto", "lastblock", "split_merge", "graph", "coop"):
+    for strategy in ("auto", "lastblock", "designated", "split_merge", "graph", "coop"):
         out = out_tensor(case, dev)
         kvattn.decode(out, qkv, cache, B, NH, HS, maxT, kv_dtype=dtype, kv_scale=scale, cur_len=cur,
                       lens_per_seq=True, strategy=strategy, **ws.kwargs())
@@ -106,7 +106,8 @@ def test_append_decode_equals_append_then_decode(dev, dtype, lens):
     totals = [[1, 1], [100, 100], [256, 256], [257, 257], [600, 600]] if lens == "uniform" else \
         [[600, 131], [1, 257], [256, 64]]
     runs = [("auto", 0, True), ("auto", 0, False), ("fused_single", 0, True), ("split_merge", 8, True),
-            ("split_merge", 0, False), ("lastblock", 0, False), ("lastblock", -64, True), ("graph", 0, False),
+            ("split_merge", 0, False), ("lastblock", 0, False), ("lastblock", -64, True), ("designated", 0, False),
+            ("designated", -64, True), ("designated", 8, True), ("graph", 0, False),
             ("coop", 8, True), ("coop", 0, False)]
     for tt in totals:
         case = make_case(dtype, B, NH, maxT, np.array(tt, np.int32) - 1, seed=50 + tt[0])

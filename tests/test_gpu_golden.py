@@ -19,7 +19,7 @@ def _dev_tensor(a, dev):
 
 
 @pytest.mark.parametrize("name,dtype", [("g_f32", "f32"), ("g_bf16", "bf16")])
-@pytest.mark.parametrize("strategy", ["fused_single", "split_merge", "lastblock", "graph", "coop"])
+@pytest.mark.parametrize("strategy", ["fused_single", "split_merge", "lastblock", "designated", "graph", "coop"])
 def test_golden_attention(dev, name, dtype, strategy):
     import torch
     from cuda_gpt2_inference_amd import kvattn
@@ -28,7 +28,7 @@ def test_golden_attention(dev, name, dtype, strategy):
     qkv, cache = _dev_tensor(g["qkv"], dev), _dev_tensor(g["cache"], dev)
     cur = torch.from_numpy(g["totals"] - 1).to(dev)
     out = torch.empty(B * NH * HS, dtype=torch.float32 if dtype == "f32" else torch.bfloat16, device=dev)
-    S = 0 if strategy in ("fused_single", "split_merge", "lastblock") else 5
+    S = 0 if strategy in ("fused_single", "split_merge", "lastblock", "designated") else 5
     ws = kvattn.Workspace(B, NH, maxT, S)
     kvattn.decode(out, qkv, cache, B, NH, HS, maxT, kv_dtype=dtype, cur_len=cur, lens_per_seq=True, S=S,
                   strategy=strategy, **ws.kwargs())
@@ -54,7 +54,8 @@ def test_golden_w8_append_and_attention(dev, fmt):
     assert np.array_equal(codes.cpu().numpy(), g["codes"])
     assert np.array_equal(scales.cpu().numpy().view(np.uint32), g["scales"].view(np.uint32))
     qkv = _dev_tensor(np.ascontiguousarray(src[maxT - 1]), dev)
-    for strategy, S in (("fused_single", 0), ("split_merge", 4), ("lastblock", 0), ("coop", 3)):
+    for strategy, S in (("fused_single", 0), ("split_merge", 4), ("lastblock", 0), ("designated", 0),
+                        ("designated", 3), ("coop", 3)):
         out = torch.empty(B * NH * HS, dtype=torch.bfloat16, device=dev)
         ws = kvattn.Workspace(B, NH, maxT, S)
         kvattn.decode(out, qkv, codes, B, NH, HS, maxT, kv_dtype=fmt, kv_scale=scales, cur_len=cur, S=S,

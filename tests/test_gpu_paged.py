@@ -105,7 +105,7 @@ def test_paged_decode_matches_oracle(dev, dtype, P):
         qkv = torch.from_numpy(case.qkv_raw.view(np.int16 if dtype != "f32" else np.float32)).to(dev)
         if dtype != "f32":
             qkv = qkv.view(torch.bfloat16)
-        for strategy in ("auto", "lastblock", "split_merge", "graph"):
+        for strategy in ("auto", "lastblock", "designated", "split_merge", "graph"):
             for S in (0, -64, -128 if P == 64 else -256):
                 for hint in (-1, max(lens) - 1):
                     ws = kvattn.Workspace(B, NH, maxT, S)
@@ -151,8 +151,8 @@ def test_paged_append_and_fused(dev, dtype):
         used = ~np.isnan(ws_pool)
         assert np.array_equal(got[used].view(np.uint32), ws_pool[used].view(np.uint32)), "paged append scales"
 
-    for strategy, S, hint in (("auto", 0, -1), ("lastblock", -64, max(lens) - 1), ("split_merge", 0, -1),
-                              ("graph", -128, -1)):
+    for strategy, S, hint in (("auto", 0, -1), ("lastblock", -64, max(lens) - 1), ("designated", -64, -1),
+                              ("designated", 0, max(lens) - 1), ("split_merge", 0, -1), ("graph", -128, -1)):
         pa, pb = Paged(case, P, dev, seed=9), Paged(case, P, dev, seed=9)
         wsp = kvattn.Workspace(B, NH, maxT, S)
         oa, ob = out_tensor(case, dev), out_tensor(case, dev)

@@ -13,7 +13,7 @@ from oracle import oracle
 pytestmark = pytest.mark.gpu
 
 ALL_DT = ["f32", "bf16", "int8", "fp8"]
-SPLIT_STRATS = ["split_merge", "lastblock", "graph", "coop"]
+SPLIT_STRATS = ["split_merge", "lastblock", "designated", "graph", "coop"]
 
 
 def _kv():
@@ -230,7 +230,7 @@ def test_c2_bf16_sweep_auto(dev):
 
 def test_c3_int8_outliers_8way(dev):
     case = make_case("int8", 1, 12, 1024, 1023, seed=3, outliers=0.01)
-    for strategy in ("split_merge", "lastblock"):
+    for strategy in ("split_merge", "lastblock", "designated"):
         got = _run(case, dev, strategy, S=8)
         assert_close(got, case.reference(), "int8", f"C3 {strategy}")
 
@@ -238,7 +238,7 @@ def test_c3_int8_outliers_8way(dev):
 @pytest.mark.parametrize("total", [512, 1024])
 def test_c4_fp8_single_launch(dev, total):
     case = make_case("fp8", 1, 12, 1024, total - 1, seed=4)
-    for strategy in ("coop", "graph", "lastblock"):
+    for strategy in ("coop", "graph", "lastblock", "designated"):
         got = _run(case, dev, strategy, S=8)
         assert_close(got, case.reference(), "fp8", f"C4 {strategy} T={total}")
 
@@ -258,7 +258,7 @@ def test_c5_ragged_64_sequences(dev):
     cache = torch.randn(2 * B * NH * maxT * HS, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
     qkv = torch.randn(B * 3 * NH * HS, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
     outs = {}
-    for strategy in ("auto", "split_merge", "lastblock"):
+    for strategy in ("auto", "split_merge", "lastblock", "designated"):
         out = torch.empty(B * NH * HS, dtype=torch.bfloat16, device=dev)
         ws = kvattn.Workspace(B, NH, maxT, 0)
         kvattn.decode(out, qkv, cache, B, NH, HS, maxT, kv_dtype="bf16", cur_len=cur, lens_per_seq=True,
@@ -324,6 +324,57 @@ def test_graph_capture_replay_tracks_device_length(dev):
         case.cur_lens[:] = total - 1
         assert_close(out.float().cpu().numpy(), case.reference(), "bf16", f"graph replay T={total}")
         out.fill_(float("nan"))
+
+
+def test_designated_merger_workspace_reuse(dev):
+    """The designated merger leaves its tagged slots empty after every call: one workspace
+    serves calls that alternate strategy, segment count and inputs, each checked against
+    the oracle (a stale slot would hand a later call an old partial)."""
+    import torch
+    kvattn = _kv()
+    B, NH, maxT = 2, 3, 700
+    ws = kvattn.Workspace(B, NH, maxT, 8)
+    for i, (strategy, S, totals) in enumerate([
+            ("designated", 8, [700, 650]), ("split_merge", 8, [600, 20]), ("designated", 8, [699, 5]),
+            ("lastblock", 8, [300, 700]), ("designated", 4, [700, 700]), ("designated", 8, [3, 2]),
+            ("designated", 8, [512, 700])]):
+        case = make_case("bf16", B, NH, maxT, np.array(totals, np.int32) - 1, seed=90 + i)
+        qkv, cache, _, cur = to_device(case, dev)
+        out = out_tensor(case, dev)
+        kvattn.decode(out, qkv, cache, B, NH, HS, maxT, kv_dtype="bf16", cur_len=cur, lens_per_seq=True, S=S,
+                      strategy=strategy, **ws.kwargs())
+        torch.cuda.synchronize()
+        assert_close(out.float().cpu().numpy(), case.reference(), "bf16", f"call {i} {strategy} S={S}")
+
+
+def test_designated_merger_grid_beyond_residency(dev):
+    """12,288 workgroups, far more than the GPU holds at once: segment 0 of each (b,h) waits
+    for segments dispatched after it, which relies on in-order dispatch of workgroups.
+    Repeated calls, every output finite, a subset of sequences against the oracle."""
+    import torch
+    kvattn = _kv()
+    B, NH, maxT = 64, 12, 1024
+    lens = np.full(B, maxT, np.int32)
+    lens[::5] = np.arange(1, B + 1, 5, dtype=np.int32) * 15
+    case = make_case("bf16", B, NH, maxT, lens - 1, seed=97)
+    qkv, cache, _, cur = to_device(case, dev)
+    out = out_tensor(case, dev)
+    S = -64
+    assert kvattn.plan(B, NH, HS, maxT, kv_dtype="bf16", S=S, strategy="designated") == \
+        (kvattn.SPLIT_DESIGNATED, 16, 64)
+    ws = kvattn.Workspace(B, NH, maxT, S)
+    for _ in range(3):
+        out.fill_(float("nan"))
+        kvattn.decode(out, qkv, cache, B, NH, HS, maxT, kv_dtype="bf16", cur_len=cur, lens_per_seq=True, S=S,
+                      strategy="designated", **ws.kwargs())
+        torch.cuda.synchronize()
+        got = out.float().cpu().numpy().reshape(B, NH, HS)
+        assert np.isfinite(got).all()
+    sub = [0, 1, 5, 10, 63]
+    q = np.ascontiguousarray(case.qkv_host.reshape(B, 3, NH, HS)[sub]).reshape(-1)
+    c = np.ascontiguousarray(case.cache_host.reshape(2, B, NH, maxT, HS)[:, sub]).reshape(-1)
+    ref = oracle.attention_f32(q, c, lens[sub], len(sub), NH, HS, maxT)
+    assert_close(got[sub].reshape(-1), ref, "bf16", "designated, grid beyond residency")
 
 
 def test_workspace_init_zeroes_eager_and_in_graph(dev):
@@ -398,7 +449,7 @@ def test_device_length_out_of_range_is_clamped(dev):
     qkv, cache, _, cur = to_device(case, dev)
     for bad in (40, 1 << 30):
         cur.fill_(bad)
-        for strategy in ("fused_single", "lastblock"):
+        for strategy in ("fused_single", "lastblock", "designated"):
             from cuda_gpt2_inference_amd import kvattn
             out = out_tensor(case, dev)
             ws = kvattn.Workspace(1, 2, 32, 0)

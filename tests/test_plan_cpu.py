@@ -13,7 +13,8 @@ def up(x):
 
 
 def carve_bytes(B, NH, slots):
-    return up(B * NH * 4) + 2 * up(B * NH * slots * 4) + up(B * NH * slots * 64 * 4)
+    return (up(B * NH * 4) + 2 * up(B * NH * slots * 4) + up(B * NH * slots * 64 * 4)
+            + up(B * NH * slots * 2 * 8) + up(B * NH * slots * 64 * 8))
 
 
 def test_auto_short_context_is_fused_single():
@@ -22,10 +23,27 @@ def test_auto_short_context_is_fused_single():
 
 
 def test_auto_gpt2_layer_is_single_launch_split():
-    # T = 1024 at B=1, NH=12: about four 256-row segments per head, merged in-kernel.
-    assert kvattn.plan(1, 12, 64, 1024, kv_dtype="bf16", len_hint=1023) == (kvattn.SPLIT_LASTBLOCK, 4, 256)
-    # 257 positions: four segments would be 65 rows; rows per segment are a power of two.
-    assert kvattn.plan(1, 12, 64, 1024, kv_dtype="int8", len_hint=256) == (kvattn.SPLIT_LASTBLOCK, 8, 128)
+    # T = 1024 at B=1, NH=12: 128-row segments (8 per head), merged in-kernel by segment 0
+    # (the designated merger).
+    assert kvattn.plan(1, 12, 64, 1024, kv_dtype="bf16", len_hint=1023) == (kvattn.SPLIT_DESIGNATED, 8, 128)
+    # 257 positions: three 128-row segments used; the grid covers every length up to maxT.
+    assert kvattn.plan(1, 12, 64, 1024, kv_dtype="int8", len_hint=256) == (kvattn.SPLIT_DESIGNATED, 8, 128)
+    # The lastblock strategy keeps its own segmentation (about four segments).
+    assert kvattn.plan(1, 12, 64, 1024, kv_dtype="bf16", len_hint=1023, strategy="lastblock") == \
+        (kvattn.SPLIT_LASTBLOCK, 4, 256)
+
+
+def test_designated_follows_at_most_64_segments():
+    # Explicitly requested with more than 64 segments per (b,h): refused; AUTO falls back to
+    # the last-block merge instead.
+    with pytest.raises(kvattn.KvAttnError) as ei:
+        kvattn.plan(1, 12, 64, 8192, kv_dtype="bf16", S=-64, strategy="designated")
+    assert ei.value.status == kvattn.ERR_SPLIT
+    assert kvattn.plan(1, 12, 64, 4096, kv_dtype="bf16", S=-64, strategy="designated") == \
+        (kvattn.SPLIT_DESIGNATED, 64, 64)
+    # Long contexts: longer segments keep the count at 64 or fewer.
+    assert kvattn.plan(1, 1, 64, 40000, kv_dtype="bf16", len_hint=39999) == (kvattn.SPLIT_DESIGNATED, 40, 1024)
+    assert kvattn.plan(1, 1, 64, 40000, kv_dtype="bf16") == (kvattn.SPLIT_DESIGNATED, 64, -1)
 
 
 def test_auto_large_batch_streams_with_split_merge():
@@ -36,8 +54,9 @@ def test_auto_large_batch_streams_with_split_merge():
 def test_auto_without_hint_plans_on_the_device():
     # No length hint (a graph replayed at every length): the kernels pick the rows per
     # segment from the device length; the grid holds the most segments any length needs.
-    assert kvattn.plan(1, 12, 64, 1024, kv_dtype="bf16") == (kvattn.SPLIT_LASTBLOCK, 4, -1)
-    assert kvattn.plan(1, 12, 64, 300, kv_dtype="bf16") == (kvattn.SPLIT_LASTBLOCK, 4, -1)
+    assert kvattn.plan(1, 12, 64, 1024, kv_dtype="bf16") == (kvattn.SPLIT_DESIGNATED, 8, -1)
+    assert kvattn.plan(1, 12, 64, 300, kv_dtype="bf16") == (kvattn.SPLIT_DESIGNATED, 3, -1)
+    assert kvattn.plan(1, 12, 64, 1024, kv_dtype="bf16", strategy="lastblock") == (kvattn.SPLIT_LASTBLOCK, 4, -1)
     assert kvattn.plan(64, 12, 64, 8192, kv_dtype="bf16") == (kvattn.SPLIT_MERGE, 16, -1)
     assert kvattn.plan(1, 12, 64, 20000, kv_dtype="fp8", strategy="lastblock") == (kvattn.SPLIT_LASTBLOCK, 40, -1)
     # Every length fits fused_single: no split at all.
@@ -66,8 +85,13 @@ def test_explicit_strategies_and_partitions():
 def test_workspace_for_S0_covers_every_auto_plan(B, NH, maxT):
     ws = kvattn.workspace_bytes(B, NH, 64, maxT, 0)
     for hint in sorted(h for h in {-1, 0, 1, maxT // 7, maxT // 2, maxT - 1} if h < maxT):
-        for strategy in ("auto", "split_merge", "lastblock", "graph"):
-            _, slots, _ = kvattn.plan(B, NH, 64, maxT, kv_dtype="bf16", len_hint=hint, strategy=strategy)
+        for strategy in ("auto", "split_merge", "lastblock", "designated", "graph"):
+            try:
+                _, slots, _ = kvattn.plan(B, NH, 64, maxT, kv_dtype="bf16", len_hint=hint, strategy=strategy)
+            except kvattn.KvAttnError as e:
+                # The designated merger follows at most 64 segments per (b,h).
+                assert strategy == "designated" and e.status == kvattn.ERR_SPLIT
+                continue
             assert carve_bytes(B, NH, slots) <= ws
 
 
