@@ -438,11 +438,15 @@ def other_configs(torch, kvattn, dev):
         "c1_f32_fused_single_T256": small_config(torch, kvattn, dev, "f32", 12, 256, 256, "fused_single", 0),
         "c3_int8_T1024_split_merge_S8": small_config(torch, kvattn, dev, "int8", 12, 1024, 1024, "split_merge", 8),
         "c3_int8_T1024_lastblock_S8": small_config(torch, kvattn, dev, "int8", 12, 1024, 1024, "lastblock", 8),
+        "c3_int8_T1024_designated_S8": small_config(torch, kvattn, dev, "int8", 12, 1024, 1024, "designated", 8),
+        "c3_int8_T1024_auto": small_config(torch, kvattn, dev, "int8", 12, 1024, 1024, "auto", 0),
         "c4_fp8_T512_coop_S8": small_config(torch, kvattn, dev, "fp8", 12, 1024, 512, "coop", 8, reps=50),
         "c4_fp8_T512_graph_S8": small_config(torch, kvattn, dev, "fp8", 12, 1024, 512, "graph", 8),
         "c4_fp8_T1024_coop_S8": small_config(torch, kvattn, dev, "fp8", 12, 1024, 1024, "coop", 8, reps=50),
         "c4_fp8_T1024_graph_S8": small_config(torch, kvattn, dev, "fp8", 12, 1024, 1024, "graph", 8),
         "c4_fp8_T1024_lastblock_S8": small_config(torch, kvattn, dev, "fp8", 12, 1024, 1024, "lastblock", 8),
+        "c4_fp8_T512_designated_S8": small_config(torch, kvattn, dev, "fp8", 12, 1024, 512, "designated", 8),
+        "c4_fp8_T1024_designated_S8": small_config(torch, kvattn, dev, "fp8", 12, 1024, 1024, "designated", 8),
     }
 
 
@@ -512,7 +516,7 @@ def kernel_key(plan, B, NH, append=False, paged=False):
     rocprof summaries: `split_kernel<1, MODE, WAVES, TILE, APPEND, PAGED> grid=WORKITEMS`
     (4 waves and 8-row-chunk tiles for BF16 in both shapes of this build)."""
     st, slots, _ = plan
-    mode = {2: 0, 4: 0, 5: 1, 3: 2}.get(st)
+    mode = {2: 0, 4: 0, 5: 1, 3: 2, 6: 3}.get(st)
     if mode is None:
         return None
     flags = f"{'true' if append else 'false'}, {'true' if paged else 'false'}"
@@ -601,11 +605,12 @@ def cache_sweep(torch, kvattn, dev, reps=40):
     so the same calls are replayed over N distinct copies of their KV caches and the bytes
     one replay touches grow past the L2 (4 MB per XCD, 32 MB in all) and the 256 MB
     Infinity Cache into HBM.
-      stack  the GPT-2 12-layer BF16 stack at T=1024 (37.8 MB of KV per copy): one graph of N
-             decode steps, step i over copy i; microseconds per call
-      batch  B=16 sequences x NH=12 at T=1024, BF16 (50.3 MB per call): one graph of N calls,
-             call i over copy i; microseconds per call and GB/s
-    Each also reports single calls after a 512 MiB flush (cold: HBM only)."""
+      stack  the GPT-2 12-layer BF16 stack at T=1024 (37.8 MB of KV per copy): one graph of 16
+             decode steps, step i over copy i mod N; microseconds per call
+      batch  B=16 sequences x NH=12 at T=1024, BF16 (50.3 MB per call): one graph of 24 calls,
+             call i over copy i mod N; microseconds per call and GB/s
+    Every graph holds the same number of calls whatever N, so the graph launch weighs the
+    same in every row.  Each also reports single calls after a 512 MiB flush (cold: HBM only)."""
     def graph_of(fn):
         s = torch.cuda.Stream()
         g = torch.cuda.CUDAGraph()
@@ -650,13 +655,13 @@ def cache_sweep(torch, kvattn, dev, reps=40):
 
     rows = []
     for n in ns:
-        graph = graph_of(lambda: [stack_call(c, l) for c in range(n) for l in range(L)])
+        graph = graph_of(lambda: [stack_call(i % n, l) for i in range(max(ns)) for l in range(L)])
         for _ in range(5):
             graph.replay()
         with phase(f"cache_stack_N{n}"):
             ms = timed(torch, graph.replay, reps)
         rows.append({"copies": n, "working_set_MB": round(n * L * per_layer * 2 / 1e6, 1),
-                     "us_per_call": round(ms * 1000.0 / (n * L), 3)})
+                     "us_per_call": round(ms * 1000.0 / (max(ns) * L), 3)})
         del graph
     with phase("cache_stack_cold"):
         stack_cold = cold(lambda: stack_call(0, 0))
@@ -679,12 +684,12 @@ def cache_sweep(torch, kvattn, dev, reps=40):
 
     rows = []
     for n in ns:
-        graph = graph_of(lambda: [batch_call(c) for c in range(n)])
+        graph = graph_of(lambda: [batch_call(i % n) for i in range(max(ns))])
         for _ in range(5):
             graph.replay()
         with phase(f"cache_batch_N{n}"):
             ms = timed(torch, graph.replay, reps)
-        us = ms * 1000.0 / n
+        us = ms * 1000.0 / max(ns)
         rows.append({"copies": n, "working_set_MB": round(n * per_call * 2 / 1e6, 1), "us_per_call": round(us, 3),
                      "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)})
         del graph

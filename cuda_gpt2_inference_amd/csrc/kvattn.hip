@@ -766,7 +766,7 @@ __host__ __device__ __forceinline__ int ceil_div_i(int a, int b) { return (a + b
 
 constexpr int kDevicePlan = -1;     // rows from planned_rows() of the device length
 constexpr int kDevicePlanDes = -2;  // rows from designated_rows() of the device length
-constexpr int kDesignatedRows = 128;
+constexpr int kDesignatedMaxGrid = 256;  // AUTO: designated merger while heads x segments <= this
 
 // Rows per segment for an attended length of `total`: the whole length in one segment up
 // to kFusedMaxRows positions, otherwise about four segments of a power-of-two length
@@ -781,21 +781,24 @@ __host__ __device__ __forceinline__ int planned_rows(int total) {
     return r;
 }
 
-// Rows per segment for the designated merger: the whole length in one segment up to
-// kFusedMaxRows positions, otherwise 128-row segments (more segments cut the streaming
-// time per workgroup and cost the merger nothing extra while they fit one poll), longer
-// ones (powers of two) only where 128 rows would make more than 64 segments.
-__host__ __device__ __forceinline__ int designated_rows(int total) {
+// Rows per segment for the designated merger over `heads` = B*NH slots: the whole length
+// in one segment up to kFusedMaxRows positions; otherwise 128-row segments for up to 16
+// heads and 256 rows beyond (shorter segments cut each workgroup's streaming time, longer
+// ones keep the grid within what the GPU runs at once), doubled only where a (b,h) would
+// get more than 64 segments.
+__host__ __device__ __forceinline__ int designated_base_rows(int heads) { return heads <= 16 ? 128 : 256; }
+__host__ __device__ __forceinline__ int designated_rows(int total, int heads) {
     if (total <= kFusedMaxRows) return total > 0 ? total : 1;
-    int r = kDesignatedRows;
+    int r = designated_base_rows(heads);
     while ((long long)r * kMaxDesignatedSegments < total) r <<= 1;
     return r;
 }
 
 // Segments of a (b,h) whose length is `total` under fixed or device-planned rows
 // (seg_rows != 0); `rows` receives the segment length.
-__device__ __forceinline__ int seg_count(int seg_rows, int total, int& rows) {
-    rows = seg_rows > 0 ? seg_rows : (seg_rows == kDevicePlanDes ? designated_rows(total) : planned_rows(total));
+__device__ __forceinline__ int seg_count(int seg_rows, int total, int heads, int& rows) {
+    rows = seg_rows > 0 ? seg_rows
+                        : (seg_rows == kDevicePlanDes ? designated_rows(total, heads) : planned_rows(total));
     return ceil_div_i(total, rows);
 }
 
@@ -812,7 +815,7 @@ __device__ __forceinline__ bool locate(const SplitArgs& a, int x, Item& it) {
         if (it.b >= a.B) return false;
         it.total = seq_total(a.cur_len, a.lens_per_seq, it.b, a.maxT);
         it.rows = 0;
-        it.n_seg = a.seg_rows != 0 ? seg_count(a.seg_rows, it.total, it.rows) : a.S;
+        it.n_seg = a.seg_rows != 0 ? seg_count(a.seg_rows, it.total, a.B * a.NH, it.rows) : a.S;
         return it.s < it.n_seg;
     }
     const int lane = threadIdx.x & (kWave - 1);
@@ -823,7 +826,7 @@ __device__ __forceinline__ bool locate(const SplitArgs& a, int x, Item& it) {
         if (b < a.B) {
             int rows;
             tot = seq_total(a.cur_len, 1, b, a.maxT);
-            cnt = a.NH * seg_count(a.seg_rows, tot, rows);
+            cnt = a.NH * seg_count(a.seg_rows, tot, a.B * a.NH, rows);
         }
         int incl = cnt;
 #pragma unroll
@@ -838,7 +841,7 @@ __device__ __forceinline__ bool locate(const SplitArgs& a, int x, Item& it) {
             const int excl = __shfl(incl - cnt, L);
             it.b = b0 + L;
             it.total = __shfl(tot, L);
-            it.n_seg = seg_count(a.seg_rows, it.total, it.rows);
+            it.n_seg = seg_count(a.seg_rows, it.total, a.B * a.NH, it.rows);
             const int local = x - base - excl;
             it.h = local / it.n_seg;
             it.s = local - it.h * it.n_seg;
@@ -1182,7 +1185,7 @@ __global__ __launch_bounds__(kWave) void merge_kernel(SplitArgs a) {
     const int bh = blockIdx.x;
     const int b = bh / a.NH;
     int n_seg = a.S, rows;
-    if (a.seg_rows != 0) n_seg = seg_count(a.seg_rows, seq_total(a.cur_len, a.lens_per_seq, b, a.maxT), rows);
+    if (a.seg_rows != 0) n_seg = seg_count(a.seg_rows, seq_total(a.cur_len, a.lens_per_seq, b, a.maxT), a.B * a.NH, rows);
     merge_partials<DT, false>(a.out, a.part_out, a.part_lse, a.part_max, a.S, n_seg, bh, threadIdx.x);
 }
 
@@ -1594,9 +1597,9 @@ int auto_seg_rows(int total_hint) {
 // kFusedMaxRows positions, at most four while planned_rows(total) >= total / 4, and
 // ceil(total / kMaxSegRows) beyond.
 // Segment slots covering designated_rows() at every length up to maxT.
-int designated_slots(int maxT) {
+int designated_slots(int maxT, int heads) {
     if (maxT <= kFusedMaxRows) return 1;
-    return std::min(kMaxDesignatedSegments, ceil_div_i(maxT, kDesignatedRows));
+    return std::min(kMaxDesignatedSegments, ceil_div_i(maxT, designated_base_rows(heads)));
 }
 
 int planned_slots(int maxT) {
@@ -1637,7 +1640,9 @@ int make_plan(int B, int NH, int maxT, int len_hint, int S, int strategy, Plan& 
         const bool fits = (size_t)maxT * sizeof(float) <= kFusedMaxLds;
         if (!paged && fits && total_hint <= kFusedMaxRows) strategy = KVATTN_FUSED_SINGLE;
         else if ((long long)B * NH * total_hint >= kStreamRows) strategy = KVATTN_SPLIT_MERGE;
-        else strategy = KVATTN_SPLIT_DESIGNATED;
+        else if ((long long)B * NH * ceil_div_i(total_hint, designated_rows(total_hint, B * NH)) <= kDesignatedMaxGrid)
+            strategy = KVATTN_SPLIT_DESIGNATED;
+        else strategy = KVATTN_SPLIT_LASTBLOCK;
     }
     p.strategy = strategy;
     p.lat = latency_bound(B, NH, total_hint);
@@ -1650,16 +1655,17 @@ int make_plan(int B, int NH, int maxT, int len_hint, int S, int strategy, Plan& 
     const bool des = strategy == KVATTN_SPLIT_DESIGNATED;
     if (S == 0 && (len_hint < 0 || paged)) {
         p.seg_rows = des ? kDevicePlanDes : kDevicePlan;
-        p.slots = des ? designated_slots(maxT) : planned_slots(maxT);
+        p.slots = des ? designated_slots(maxT, B * NH) : planned_slots(maxT);
     } else if (S == 0) {
         // Rows fixed from the hint; the grid covers every device length up to maxT, so the
         // designated merger also needs rows >= maxT / 64.
-        p.seg_rows = des ? std::max(designated_rows(total_hint), designated_rows(maxT)) : auto_seg_rows(total_hint);
+        p.seg_rows = des ? std::max(designated_rows(total_hint, B * NH), designated_rows(maxT, B * NH))
+                         : auto_seg_rows(total_hint);
         p.slots = ceil_div_i(maxT, p.seg_rows);
     }
     if ((long long)B * NH * p.slots >= (1ll << 31)) return KVATTN_ERR_SHAPE;
     const bool des_fits = p.slots <= kMaxDesignatedSegments &&
-                          !(paged && p.seg_rows == kDevicePlanDes && designated_rows(maxT) > kMaxPagedSegRows);
+                          !(paged && p.seg_rows == kDevicePlanDes && designated_rows(maxT, B * NH) > kMaxPagedSegRows);
     if (des && !des_fits) {
         // More segments per (b,h) than the merger follows (or longer paged segments than a
         // wave walks): AUTO takes the last-block merge with its own segmentation.

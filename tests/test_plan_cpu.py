@@ -28,6 +28,10 @@ def test_auto_gpt2_layer_is_single_launch_split():
     assert kvattn.plan(1, 12, 64, 1024, kv_dtype="bf16", len_hint=1023) == (kvattn.SPLIT_DESIGNATED, 8, 128)
     # 257 positions: three 128-row segments used; the grid covers every length up to maxT.
     assert kvattn.plan(1, 12, 64, 1024, kv_dtype="int8", len_hint=256) == (kvattn.SPLIT_DESIGNATED, 8, 128)
+    # More heads: 256-row segments while heads x segments stays within 256 workgroups; a
+    # larger grid takes the last-block merge.
+    assert kvattn.plan(2, 12, 64, 1024, kv_dtype="bf16", len_hint=1023) == (kvattn.SPLIT_DESIGNATED, 4, 256)
+    assert kvattn.plan(16, 12, 64, 1024, kv_dtype="bf16", len_hint=1023) == (kvattn.SPLIT_LASTBLOCK, 4, 256)
     # The lastblock strategy keeps its own segmentation (about four segments).
     assert kvattn.plan(1, 12, 64, 1024, kv_dtype="bf16", len_hint=1023, strategy="lastblock") == \
         (kvattn.SPLIT_LASTBLOCK, 4, 256)
