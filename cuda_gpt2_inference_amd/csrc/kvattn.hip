@@ -726,7 +726,10 @@ __global__ __launch_bounds__(kThreads) void fused_single_kernel(
 // ------------------------------------------------------------------------------------
 // Split kernels.
 // ------------------------------------------------------------------------------------
-enum SplitMode { kPartialsOnly = 0, kLastBlockMerge = 1, kCoopMerge = 2, kDesignated = 3 };
+// kDesignatedDev: the designated merger over segments planned on the device (seg_rows ==
+// kDevicePlanDes), a separate instance so that its speculative first tile leaves the
+// host-planned instance's code as it is.
+enum SplitMode { kPartialsOnly = 0, kLastBlockMerge = 1, kCoopMerge = 2, kDesignated = 3, kDesignatedDev = 4 };
 
 struct SplitArgs {
     void* out;
@@ -952,22 +955,38 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
     // range, and its q slice, before reading the device length, so the three memory
     // round trips overlap; rows beyond the true length are masked afterwards.  Otherwise
     // the same first tile is requested once the length is known.
+    // Designated segments planned on the device (kDesignatedDev) are designated_base_rows()
+    // long at every length from kFusedMaxRows + 1 up to 64 segments' worth, so every
+    // workgroup guesses that length (there is no hint to go by).  Segment 0 is also the
+    // whole length up to kFusedMaxRows, so its waves split that range, and only those whose
+    // share lies inside the first designated_base_rows() rows request it early; the others
+    // request theirs once the length shows that they have rows.  A segment the length plans
+    // otherwise (doubled rows) drops the guess and requests its true first tile.
+    constexpr bool kDev = kMode == kDesignatedDev;
     Tile<DT, kU> t0;
     QRaw<DT> q0;
     FreshRaw<DT> fr{};
-    bool spec = false;
-    int w0 = 0, w1 = 0;
-    if (!kPaged && !a.lens_per_seq && a.seg_rows > 0) {
+    bool spec = false, spec_tile = true;
+    int w0 = 0, w1 = 0, spec_j0 = 0, spec_end = 0;
+    if (!kPaged && !a.lens_per_seq && (kDev || a.seg_rows > 0)) {
+        const int nom = kDev ? designated_base_rows(a.B * a.NH) : a.seg_rows;
         const int bh0 = blockIdx.x / a.S;
-        const int j0 = (blockIdx.x - bh0 * a.S) * a.seg_rows;
-        const int nend = min(j0 + a.seg_rows, a.maxT);
-        if (j0 < a.spec_rows && j0 < nend) {
+        const int j0 = (blockIdx.x - bh0 * a.S) * nom;
+        const bool first = kDev && j0 == 0 && nom < kFusedMaxRows;
+        const int nend = min(j0 + (first ? kFusedMaxRows : nom), a.maxT);
+        // 8-bit caches guess only in segment 0's early share: measured, the producers' early
+        // tiles cost 8-bit calls more than the length's round trip they hide.
+        const bool guess = !(R::k8bit && kDev && !first);
+        if (guess && (kDev || j0 < a.spec_rows) && j0 < nend) {
             const int per = ceil_div_i(nend - j0, kW);
             w0 = min(j0 + wave * per, nend);
             w1 = min(w0 + per, nend);
+            spec_j0 = j0;
+            spec_end = nend;
+            spec_tile = !first || w1 <= j0 + nom;
             const int b0 = bh0 / a.NH;
             const Slot sl0 = make_slot<DT>(a.kv, a.kv_scale, a.B, a.NH, a.maxT, bh0, slice);
-            load_tile<DT, kU, true>(t0, sl0, w0, w1, slot_row);
+            if (spec_tile) load_tile<DT, kU, true>(t0, sl0, w0, w1, slot_row);
             q0 = load_q<DT>(a.qkv, b0, bh0 - b0 * a.NH, a.NH, slice);
             if constexpr (kFresh) fr = load_fresh<DT>(a.qkv, b0, bh0 - b0 * a.NH, a.NH, slice);
             spec = true;
@@ -982,7 +1001,7 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
     const int bh = it.b * a.NH + it.h;
     const size_t pidx = (size_t)bh * a.S + it.s;
     constexpr bool kCoh = kMode == kLastBlockMerge;
-    constexpr bool kDes = kMode == kDesignated;
+    constexpr bool kDes = kMode == kDesignated || kDev;
 
     // Rows [sj0, sj1) of segment s of this (b,h).
     auto seg_range = [&](int s, int& sj0, int& sj1) {
@@ -1023,8 +1042,9 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                                                        fr, a.kv_out, a.kv_scale_out, cur, m, l, acc);
             } else {
                 sl = make_slot<DT>(a.kv, a.kv_scale, a.B, a.NH, a.maxT, bh, slice);
-                if (spec) {
+                if (spec && (!kDev || (j0 == spec_j0 && j1 <= spec_end))) {
                     w1 = min(w1, j1);
+                    if (kDev && !spec_tile && w0 < w1) load_tile<DT, kU, true>(t0, sl, w0, w1, slot_row);
                 } else {
                     const int per_wave = ceil_div_i(j1 - j0, kW);
                     w0 = min(j0 + wave * per_wave, j1);
@@ -1367,13 +1387,15 @@ int launch_fused_single(void* out, const void* qkv, const void* kv, const float*
 
 // Split kernel instance for a mode, a shape (`lat`: the latency shape, else the streaming
 // shape) and whether the launch also appends the current row.
-// (Paged caches have no cooperative instance: the host never plans one.)
+// (Paged caches have no cooperative instance, which the host never plans for them, and no
+// kDesignatedDev instance: their first tile is never requested before the length.)
 template <int DT, int W, int U, bool kFresh, bool kPaged>
 const void* split_ptr_mode(int mode) {
     if (mode == kPartialsOnly) return (const void*)&split_kernel<DT, kPartialsOnly, W, U, kFresh, kPaged>;
     if (mode == kLastBlockMerge) return (const void*)&split_kernel<DT, kLastBlockMerge, W, U, kFresh, kPaged>;
     if (mode == kDesignated) return (const void*)&split_kernel<DT, kDesignated, W, U, kFresh, kPaged>;
     if constexpr (kPaged) return nullptr;
+    else if (mode == kDesignatedDev) return (const void*)&split_kernel<DT, kDesignatedDev, W, U, kFresh, false>;
     else return (const void*)&split_kernel<DT, kCoopMerge, W, U, kFresh, false>;
 }
 
@@ -1736,7 +1758,9 @@ int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scal
             KV_TRY(launch_split(a, kv_dtype, kPartialsOnly, plan.lat, stream));
             return launch_merge(a, kv_dtype, stream);
         case KVATTN_SPLIT_LASTBLOCK: return launch_split(a, kv_dtype, kLastBlockMerge, plan.lat, stream);
-        case KVATTN_SPLIT_DESIGNATED: return launch_split(a, kv_dtype, kDesignated, plan.lat, stream);
+        case KVATTN_SPLIT_DESIGNATED:
+            return launch_split(a, kv_dtype, plan.seg_rows == kDevicePlanDes && !pm ? kDesignatedDev : kDesignated,
+                                plan.lat, stream);
         case KVATTN_SINGLE_LAUNCH_COOP: return launch_coop(a, kv_dtype, plan.lat, stream);
         case KVATTN_SINGLE_LAUNCH_GRAPH: return launch_graph_pair(a, kv_dtype, plan.lat, stream);
         default: return KVATTN_ERR_STRATEGY;

@@ -18,8 +18,11 @@ from oracle import oracle
 pytestmark = pytest.mark.gpu
 
 # Lengths around every change of the device plan: one segment up to 256 positions, then
-# 128-row segments (257..512), 256-row (513..1024), 512-row (1025..).
-PLAN_EDGES = (1, 2, 63, 64, 255, 256, 257, 300, 511, 512, 513, 1000, 1024, 1025, 2048, 2049, 2100)
+# 128-row segments (257..512), 256-row (513..1024), 512-row (1025..); for the designated
+# merger, 128-row segments from 257 on, and the quarters of the first 256 rows that segment 0
+# splits among its waves (64/65, 128/129, 192/193).
+PLAN_EDGES = (1, 2, 63, 64, 65, 127, 128, 129, 192, 193, 255, 256, 257, 300, 511, 512, 513, 1000, 1024, 1025,
+              2048, 2049, 2100)
 
 
 def _kv():
@@ -48,6 +51,41 @@ def test_device_plan_uniform_length(dev, dtype):
                           strategy=strategy, **ws.kwargs())
             torch.cuda.synchronize()
             assert_close(out.float().cpu().numpy(), case.reference(), dtype, f"{strategy} T={total}")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "fp8"])
+def test_designated_device_plan_doubled_rows(dev, dtype):
+    """The designated merger planned on the device beyond 64 segments of the base length:
+    rows double (256 from 8193 positions, 512 from 16385 for 2 heads), so every segment but
+    the first starts away from the first tile each workgroup requests before reading the
+    length, and segment 0 outgrows it; the append path substitutes the fresh row there too."""
+    import torch
+    kvattn = _kv()
+    B, NH, maxT = 1, 2, 16500
+    case = make_case(dtype, B, NH, maxT, 0, seed=35)
+    qkv, cache, scale, _ = to_device(case, dev)
+    cur = torch.zeros(1, dtype=torch.int32, device=dev)
+    ws = kvattn.Workspace(B, NH, maxT, 0)
+    assert kvattn.plan(B, NH, HS, maxT, kv_dtype=dtype, strategy="designated")[1:] == (64, -1)
+    for total in (256, 257, 8192, 8193, 8300, 16384, 16385, 16500):
+        cur.fill_(total - 1)
+        case.cur_lens[:] = total - 1
+        kw = dict(kv_dtype=dtype, cur_len=cur, strategy="designated", **ws.kwargs())
+        out = out_tensor(case, dev)
+        kvattn.decode(out, qkv, cache, B, NH, HS, maxT, kv_scale=scale, **kw)
+        torch.cuda.synchronize()
+        assert_close(out.float().cpu().numpy(), case.reference(), dtype, f"designated T={total}")
+        # Append and attend in one launch against the append followed by the attention.
+        c_a, c_b = cache.clone(), cache.clone()
+        s_a = scale.clone() if scale is not None else None
+        s_b = scale.clone() if scale is not None else None
+        o_a, o_b = out_tensor(case, dev), out_tensor(case, dev)
+        kvattn.kv_cache_write(c_a, qkv, B, NH, HS, maxT, kv_dtype=dtype, kv_scale=s_a, cur_len=cur)
+        kvattn.decode(o_a, qkv, c_a, B, NH, HS, maxT, kv_scale=s_a, **kw)
+        kvattn.append_decode(o_b, qkv, c_b, B, NH, HS, maxT, kv_scale=s_b, **kw)
+        torch.cuda.synchronize()
+        assert np.array_equal(_cache_bytes(c_a), _cache_bytes(c_b)), f"append T={total}: cache"
+        assert np.array_equal(o_a.float().cpu().numpy(), o_b.float().cpu().numpy()), f"append T={total}: out"
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "int8"])
@@ -103,7 +141,7 @@ def test_append_decode_equals_append_then_decode(dev, dtype, lens):
     import torch
     kvattn = _kv()
     B, NH, maxT = 2, 3, 600
-    totals = [[1, 1], [100, 100], [256, 256], [257, 257], [600, 600]] if lens == "uniform" else \
+    totals = [[1, 1], [100, 100], [129, 129], [200, 200], [256, 256], [257, 257], [600, 600]] if lens == "uniform" else \
         [[600, 131], [1, 257], [256, 64]]
     runs = [("auto", 0, True), ("auto", 0, False), ("fused_single", 0, True), ("split_merge", 8, True),
             ("split_merge", 0, False), ("lastblock", 0, False), ("lastblock", -64, True), ("designated", 0, False),
