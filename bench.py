@@ -374,10 +374,28 @@ class C5Paged:
                 "GBps": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
 
 
-def small_config(torch, kvattn, dev, dtype, NH, maxT, T, strategy, S, reps=200):
+def cold_median_us(torch, call, flush, reps=30):
+    """Median microseconds of `reps` single eager calls, each after writing `flush` (512 MiB:
+    more than the 256 MiB Infinity Cache and the 32 MiB of L2), as the reference lab flushes
+    L2 before each timed call (attention_kvcache.cu:1095)."""
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ts = []
+    for r in range(reps):
+        flush.fill_(r & 0xFF)
+        e0.record()
+        call()
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1) * 1000.0)
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
+def small_config(torch, kvattn, dev, dtype, NH, maxT, T, strategy, S, reps=200, flush=None):
     """One (B=1) decode-attention call on a warm cache: microseconds per call, measured over
     `reps` back-to-back calls replayed from a HIP graph (eager for the cooperative launch,
-    which cannot be captured)."""
+    which cannot be captured).  With `flush`, also the median single eager call on a cold
+    cache (`us_per_call_cold`)."""
     B = 1
     g = torch.Generator(device=dev)
     g.manual_seed(7)
@@ -425,29 +443,36 @@ def small_config(torch, kvattn, dev, dtype, NH, maxT, T, strategy, S, reps=200):
     nbytes = bytes_per_call([T], NH, kv_bytes, act, B) + (2 * NH * T * 4 if scale is not None else 0)
     us = graph_us if graph_us is not None else eager_us
     gbs = nbytes / (us * 1e-6) / 1e9
+    cold = None if flush is None else round(cold_median_us(torch, call, flush, 30 if strategy != "coop" else 10), 3)
     return {"dtype": dtype, "B": B, "NH": NH, "T": T, "maxT": maxT,
             "strategy": kvattn.STRATEGY_NAMES[plan[0]], "segments_per_head": plan[1], "rows_per_segment": plan[2],
             "bytes_per_call": nbytes, "us_per_call_graph": None if graph_us is None else round(graph_us, 3),
-            "us_per_call_eager": round(eager_us, 3), "GBps": round(gbs, 1),
+            "us_per_call_eager": round(eager_us, 3), "us_per_call_cold": cold, "GBps": round(gbs, 1),
             "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 def other_configs(torch, kvattn, dev):
-    """The remaining GPT-2-shaped configurations, single layer, warm cache."""
-    return {
-        "c1_f32_fused_single_T256": small_config(torch, kvattn, dev, "f32", 12, 256, 256, "fused_single", 0),
-        "c3_int8_T1024_split_merge_S8": small_config(torch, kvattn, dev, "int8", 12, 1024, 1024, "split_merge", 8),
-        "c3_int8_T1024_lastblock_S8": small_config(torch, kvattn, dev, "int8", 12, 1024, 1024, "lastblock", 8),
-        "c3_int8_T1024_designated_S8": small_config(torch, kvattn, dev, "int8", 12, 1024, 1024, "designated", 8),
-        "c3_int8_T1024_auto": small_config(torch, kvattn, dev, "int8", 12, 1024, 1024, "auto", 0),
-        "c4_fp8_T512_coop_S8": small_config(torch, kvattn, dev, "fp8", 12, 1024, 512, "coop", 8, reps=50),
-        "c4_fp8_T512_graph_S8": small_config(torch, kvattn, dev, "fp8", 12, 1024, 512, "graph", 8),
-        "c4_fp8_T1024_coop_S8": small_config(torch, kvattn, dev, "fp8", 12, 1024, 1024, "coop", 8, reps=50),
-        "c4_fp8_T1024_graph_S8": small_config(torch, kvattn, dev, "fp8", 12, 1024, 1024, "graph", 8),
-        "c4_fp8_T1024_lastblock_S8": small_config(torch, kvattn, dev, "fp8", 12, 1024, 1024, "lastblock", 8),
-        "c4_fp8_T512_designated_S8": small_config(torch, kvattn, dev, "fp8", 12, 1024, 512, "designated", 8),
-        "c4_fp8_T1024_designated_S8": small_config(torch, kvattn, dev, "fp8", 12, 1024, 1024, "designated", 8),
+    """The remaining GPT-2-shaped configurations, single layer: warm cache (graph replay) and
+    cold cache (single eager calls after a 512 MiB flush)."""
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    cfg = lambda *a, **k: small_config(torch, kvattn, dev, *a, flush=flush, **k)  # noqa: E731
+    res = {
+        "c1_f32_fused_single_T256": cfg("f32", 12, 256, 256, "fused_single", 0),
+        "c3_int8_T1024_split_merge_S8": cfg("int8", 12, 1024, 1024, "split_merge", 8),
+        "c3_int8_T1024_lastblock_S8": cfg("int8", 12, 1024, 1024, "lastblock", 8),
+        "c3_int8_T1024_designated_S8": cfg("int8", 12, 1024, 1024, "designated", 8),
+        "c3_int8_T1024_auto": cfg("int8", 12, 1024, 1024, "auto", 0),
+        "c4_fp8_T512_coop_S8": cfg("fp8", 12, 1024, 512, "coop", 8, reps=50),
+        "c4_fp8_T512_graph_S8": cfg("fp8", 12, 1024, 512, "graph", 8),
+        "c4_fp8_T1024_coop_S8": cfg("fp8", 12, 1024, 1024, "coop", 8, reps=50),
+        "c4_fp8_T1024_graph_S8": cfg("fp8", 12, 1024, 1024, "graph", 8),
+        "c4_fp8_T1024_lastblock_S8": cfg("fp8", 12, 1024, 1024, "lastblock", 8),
+        "c4_fp8_T512_designated_S8": cfg("fp8", 12, 1024, 512, "designated", 8),
+        "c4_fp8_T1024_designated_S8": cfg("fp8", 12, 1024, 1024, "designated", 8),
+        "c4_fp8_T1024_auto": cfg("fp8", 12, 1024, 1024, "auto", 0),
     }
+    del flush
+    return res
 
 
 GEMV_SHAPES = (("qkv", 2304, 768, False), ("attproj", 768, 768, False), ("fc", 3072, 768, True),
