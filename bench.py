@@ -536,16 +536,23 @@ def gemv_cpu_baseline(seconds=3.0):
             "kind": "port", "sample": f"oracle_gemv FP32 768x768, B=1, median of {reps} calls"}
 
 
-def kernel_key(plan, B, NH, append=False, paged=False):
+def kernel_key(plan, B, NH, append=False, paged=False, ragged=False):
     """(name prefix, grid suffix) of the BF16 split kernel a plan launches, as keyed in the
     rocprof summaries: `split_kernel<1, MODE, WAVES, TILE, APPEND, PAGED> grid=WORKITEMS`
-    (4 waves and 8-row-chunk tiles for BF16 in both shapes of this build)."""
-    st, slots, _ = plan
+    (4 waves and 8-row-chunk tiles for BF16 in both shapes of this build).  Modes: 0 partials,
+    1 last-block, 2 cooperative, 3 designated, 4 designated planned on the device, 5 partials
+    of ragged lengths on half the grid (two packed segments per workgroup)."""
+    st, slots, rows = plan
     mode = {2: 0, 4: 0, 5: 1, 3: 2, 6: 3}.get(st)
     if mode is None:
         return None
+    blocks = B * NH * slots
+    if mode == 3 and rows == -2 and not paged:
+        mode = 4
+    elif mode == 0 and ragged and rows != 0 and B <= 256:
+        mode, blocks = 5, (blocks + 1) // 2
     flags = f"{'true' if append else 'false'}, {'true' if paged else 'false'}"
-    return f"split_kernel<1, {mode}, 4, 8, {flags}>", f"grid={B * NH * slots * 256}"
+    return f"split_kernel<1, {mode}, 4, 8, {flags}>", f"grid={blocks * 256}"
 
 
 def lookup(traffic, key):
@@ -767,14 +774,14 @@ def main():
     if not args.no_c5:
         c5o = C5(args, torch, kvattn, dev)
         c5 = c5o.measure()
-        k5, t5 = lookup(traffic, kernel_key(c5o.plan, c5o.B, c5o.NH))
+        k5, t5 = lookup(traffic, kernel_key(c5o.plan, c5o.B, c5o.NH, ragged=True))
         c5["kernel"] = k5
         c5["traffic_bytes_split_kernel"] = t5
         del c5o
         c5["paged"] = C5Paged(args, torch, kvattn, dev).measure()
         c5["paged"]["kernel"], c5["paged"]["traffic_bytes_split_kernel"] = lookup(
             traffic, kernel_key(kvattn.plan(C5Paged.B, C5Paged.NH, HD, C5Paged.maxT, kv_dtype="bf16"), C5Paged.B,
-                                C5Paged.NH, paged=True))
+                                C5Paged.NH, paged=True, ragged=True))
     configs = None if args.no_configs else other_configs(torch, kvattn, dev)
     gemv = None if args.no_configs else gemv_configs(torch, kvattn, dev)
     gemv_cpu = None if (args.no_configs or args.no_cpu) else gemv_cpu_baseline()

@@ -53,6 +53,8 @@ constexpr float kStartMax = -1.0e30f;   // finite start value of every running m
 constexpr int kMinSegRows = 64;         // smallest automatic segment length
 constexpr int kMaxSegRows = 512;        // largest automatic segment length
 constexpr int kFusedMaxRows = 256;      // automatic plans keep up to this many positions in one workgroup
+constexpr int kStridedMaxSeqs = 256;    // ragged batches up to this size take the strided grid
+constexpr int kStridedFactor = 2;       // segments per workgroup bound of the strided grid
 constexpr int kMaxPagedSegRows = 4096;  // paged caches: at most 64 tiles per wave and segment
 constexpr int kMaxSegments = 1 << 16;   // upper bound on segments per (b,h)
 constexpr int kMaxT = 1 << 23;          // keeps per-slot byte offsets inside 32 bits
@@ -728,8 +730,13 @@ __global__ __launch_bounds__(kThreads) void fused_single_kernel(
 // ------------------------------------------------------------------------------------
 // kDesignatedDev: the designated merger over segments planned on the device (seg_rows ==
 // kDevicePlanDes), a separate instance so that its speculative first tile leaves the
-// host-planned instance's code as it is.
-enum SplitMode { kPartialsOnly = 0, kLastBlockMerge = 1, kCoopMerge = 2, kDesignated = 3, kDesignatedDev = 4 };
+// host-planned instance's code as it is.  kPartialsStrided: kPartialsOnly for ragged lengths
+// on half the grid, each workgroup taking two (or more) packed segments (a separate instance:
+// sharing one kernel with the one-segment form costs the streaming kernel a third of its
+// occupancy).
+enum SplitMode {
+    kPartialsOnly = 0, kLastBlockMerge = 1, kCoopMerge = 2, kDesignated = 3, kDesignatedDev = 4, kPartialsStrided = 5
+};
 
 struct SplitArgs {
     void* out;
@@ -968,7 +975,7 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
     FreshRaw<DT> fr{};
     bool spec = false, spec_tile = true;
     int w0 = 0, w1 = 0, spec_j0 = 0, spec_end = 0;
-    if (!kPaged && !a.lens_per_seq && (kDev || a.seg_rows > 0)) {
+    if (!kPaged && kMode != kPartialsStrided && !a.lens_per_seq && (kDev || a.seg_rows > 0)) {
         const int nom = kDev ? designated_base_rows(a.B * a.NH) : a.seg_rows;
         const int bh0 = blockIdx.x / a.S;
         const int j0 = (blockIdx.x - bh0 * a.S) * nom;
@@ -993,209 +1000,272 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
         }
     }
 
-    Item it;
-    const bool active = locate(a, blockIdx.x, it);
-    if constexpr (kMode != kCoopMerge) {
-        if (!active) return;
-    }
-    const int bh = it.b * a.NH + it.h;
-    const size_t pidx = (size_t)bh * a.S + it.s;
-    constexpr bool kCoh = kMode == kLastBlockMerge;
-    constexpr bool kDes = kMode == kDesignated || kDev;
+    // The work of one segment `it` (active: the workgroup has one; the cooperative launch
+    // also runs it without, for the grid barrier).  The guess made above comes in through
+    // the parameters, so that the strided loop below passes its own (empty) guess and
+    // carries no tile from one segment to the next.
+    auto segment = [&](const Item& it, const bool active, Tile<DT, kU>& t0, QRaw<DT>& q0, FreshRaw<DT>& fr,
+                       const bool spec, const bool spec_tile, int w0, int w1, const int spec_j0,
+                       const int spec_end) {
+        const int bh = it.b * a.NH + it.h;
+        const size_t pidx = (size_t)bh * a.S + it.s;
+        constexpr bool kCoh = kMode == kLastBlockMerge;
+        constexpr bool kDes = kMode == kDesignated || kDev;
 
-    // Rows [sj0, sj1) of segment s of this (b,h).
-    auto seg_range = [&](int s, int& sj0, int& sj1) {
-        if (a.seg_rows != 0) {
-            sj0 = s * it.rows;
-            sj1 = min(sj0 + it.rows, it.total);
-        } else {
-            const int chunk = ceil_div_i(it.total, a.S);
-            sj0 = s * chunk;
-            sj1 = min(sj0 + chunk, it.total);
-        }
-    };
-    int j0 = 0, j1 = 0;
-    if (active) seg_range(it.s, j0, j1);
-
-
-    if (active) {
-        if (j1 <= j0) {
-            // Empty segment (reference partition with total < S): neutral partial (the
-            // designated merger skips empty segments instead).
-            if (!kDes && wave == 0) {
-                put<kCoh>(a.part_out + pidx * kHeadDim + lane, 0.0f);
-                if (lane == 0) { put<kCoh>(a.part_max + pidx, kEmptyMax); put<kCoh>(a.part_lse + pidx, 0.0f); }
-            }
-        } else {
-            const int cur = it.total - 1;
-            float m = kStartMax, l = 0.0f, acc[R::kElems];
-#pragma unroll
-            for (int e = 0; e < R::kElems; ++e) acc[e] = 0.0f;
-            Slot sl{};
-            FreshDst fd{};
-            PagedView pv{};
-            if constexpr (kPaged) {
-                q0 = load_q<DT>(a.qkv, it.b, it.h, a.NH, slice);
-                if constexpr (kFresh) fr = load_fresh<DT>(a.qkv, it.b, it.h, a.NH, slice);
-                pv = PagedView{a.kv, a.kv_scale, a.table, a.max_pages, a.page_rows, a.num_pages, a.NH};
-                online_tiles_paged<DT, kU, kW, kFresh>(pv, it.b, it.h, j0, j1, wave, slot_row, slice, q0, a.qscale,
-                                                       fr, a.kv_out, a.kv_scale_out, cur, m, l, acc);
+        // Rows [sj0, sj1) of segment s of this (b,h).
+        auto seg_range = [&](int s, int& sj0, int& sj1) {
+            if (a.seg_rows != 0) {
+                sj0 = s * it.rows;
+                sj1 = min(sj0 + it.rows, it.total);
             } else {
-                sl = make_slot<DT>(a.kv, a.kv_scale, a.B, a.NH, a.maxT, bh, slice);
-                if (spec && (!kDev || (j0 == spec_j0 && j1 <= spec_end))) {
-                    w1 = min(w1, j1);
-                    if (kDev && !spec_tile && w0 < w1) load_tile<DT, kU, true>(t0, sl, w0, w1, slot_row);
-                } else {
-                    const int per_wave = ceil_div_i(j1 - j0, kW);
-                    w0 = min(j0 + wave * per_wave, j1);
-                    w1 = min(w0 + per_wave, j1);
-                    load_tile<DT, kU, true>(t0, sl, w0, w1, slot_row);
+                const int chunk = ceil_div_i(it.total, a.S);
+                sj0 = s * chunk;
+                sj1 = min(sj0 + chunk, it.total);
+            }
+        };
+        int j0 = 0, j1 = 0;
+        if (active) seg_range(it.s, j0, j1);
+
+
+        if (active) {
+            if (j1 <= j0) {
+                // Empty segment (reference partition with total < S): neutral partial (the
+                // designated merger skips empty segments instead).
+                if (!kDes && wave == 0) {
+                    put<kCoh>(a.part_out + pidx * kHeadDim + lane, 0.0f);
+                    if (lane == 0) { put<kCoh>(a.part_max + pidx, kEmptyMax); put<kCoh>(a.part_lse + pidx, 0.0f); }
+                }
+            } else {
+                const int cur = it.total - 1;
+                float m = kStartMax, l = 0.0f, acc[R::kElems];
+#pragma unroll
+                for (int e = 0; e < R::kElems; ++e) acc[e] = 0.0f;
+                Slot sl{};
+                FreshDst fd{};
+                PagedView pv{};
+                if constexpr (kPaged) {
                     q0 = load_q<DT>(a.qkv, it.b, it.h, a.NH, slice);
                     if constexpr (kFresh) fr = load_fresh<DT>(a.qkv, it.b, it.h, a.NH, slice);
+                    pv = PagedView{a.kv, a.kv_scale, a.table, a.max_pages, a.page_rows, a.num_pages, a.NH};
+                    online_tiles_paged<DT, kU, kW, kFresh>(pv, it.b, it.h, j0, j1, wave, slot_row, slice, q0, a.qscale,
+                                                           fr, a.kv_out, a.kv_scale_out, cur, m, l, acc);
+                } else {
+                    sl = make_slot<DT>(a.kv, a.kv_scale, a.B, a.NH, a.maxT, bh, slice);
+                    if (spec && (!kDev || (j0 == spec_j0 && j1 <= spec_end))) {
+                        w1 = min(w1, j1);
+                        if (kDev && !spec_tile && w0 < w1) load_tile<DT, kU, true>(t0, sl, w0, w1, slot_row);
+                    } else {
+                        const int per_wave = ceil_div_i(j1 - j0, kW);
+                        w0 = min(j0 + wave * per_wave, j1);
+                        w1 = min(w0 + per_wave, j1);
+                        load_tile<DT, kU, true>(t0, sl, w0, w1, slot_row);
+                        q0 = load_q<DT>(a.qkv, it.b, it.h, a.NH, slice);
+                        if constexpr (kFresh) fr = load_fresh<DT>(a.qkv, it.b, it.h, a.NH, slice);
+                    }
+                    if constexpr (kFresh)
+                        fd = fresh_dst(a.kv_out, a.kv_scale_out, a.B, a.NH, a.maxT, bh, slice, cur);
+                    online_rows_from<DT, kU, kFresh>(t0, q0, sl, w0, w1, slot_row, a.qscale, fr, fd, cur, m, l, acc);
                 }
-                if constexpr (kFresh)
-                    fd = fresh_dst(a.kv_out, a.kv_scale_out, a.B, a.NH, a.maxT, bh, slice, cur);
-                online_rows_from<DT, kU, kFresh>(t0, q0, sl, w0, w1, slot_row, a.qscale, fr, fd, cur, m, l, acc);
-            }
 
-            // Combine the row slots of this wave, then the 4 waves.
-            const float mw = slot_reduce<R::kLanes, true>(m);
-            const float f = exp2_fast(m - mw);
-            l = slot_reduce<R::kLanes, false>(l * f);
+                // Combine the row slots of this wave, then the 4 waves.
+                const float mw = slot_reduce<R::kLanes, true>(m);
+                const float f = exp2_fast(m - mw);
+                l = slot_reduce<R::kLanes, false>(l * f);
 #pragma unroll
-            for (int e = 0; e < R::kElems; ++e) acc[e] = slot_reduce<R::kLanes, false>(acc[e] * f);
-            if (lane == 0) { s_m[wave] = mw; s_l[wave] = l; }
-            if (slot_row == 0) {
+                for (int e = 0; e < R::kElems; ++e) acc[e] = slot_reduce<R::kLanes, false>(acc[e] * f);
+                if (lane == 0) { s_m[wave] = mw; s_l[wave] = l; }
+                if (slot_row == 0) {
 #pragma unroll
-                for (int e = 0; e < R::kElems; ++e) s_acc[wave][slice * R::kElems + e] = acc[e];
-            }
-            __syncthreads();
-            if (wave == 0) {
-                float Mb = s_m[0];
-#pragma unroll
-                for (int w = 1; w < kW; ++w) Mb = fmaxf(Mb, s_m[w]);
-                float L = 0.0f, A = 0.0f;
-#pragma unroll
-                for (int w = 0; w < kW; ++w) {
-                    const float g = exp2_fast(s_m[w] - Mb);
-                    L = fmaf(g, s_l[w], L);
-                    A = fmaf(g, s_acc[w][lane], A);
+                    for (int e = 0; e < R::kElems; ++e) s_acc[wave][slice * R::kElems + e] = acc[e];
                 }
-                if ((kMode == kLastBlockMerge || kDes) && it.n_seg == 1) {
-                    // The only segment of its (b,h): the result needs no merge.
-                    store_out<DT>(a.out, (size_t)bh * kHeadDim + lane, A / L);
-                } else if constexpr (kDes) {
-                    if (it.s != 0) {
-                        // Producer: publish the tagged partial and finish; nothing waits.
-                        put_word(a.tag_out + pidx * kHeadDim + lane, valid_word(A));
-                        if (lane == 0) {
-                            put_word(a.tag_ml + 2 * pidx, valid_word(Mb * kLn2));
-                            put_word(a.tag_ml + 2 * pidx + 1, valid_word(L));
+                __syncthreads();
+                if (wave == 0) {
+                    float Mb = s_m[0];
+#pragma unroll
+                    for (int w = 1; w < kW; ++w) Mb = fmaxf(Mb, s_m[w]);
+                    float L = 0.0f, A = 0.0f;
+#pragma unroll
+                    for (int w = 0; w < kW; ++w) {
+                        const float g = exp2_fast(s_m[w] - Mb);
+                        L = fmaf(g, s_l[w], L);
+                        A = fmaf(g, s_acc[w][lane], A);
+                    }
+                    if ((kMode == kLastBlockMerge || kDes) && it.n_seg == 1) {
+                        // The only segment of its (b,h): the result needs no merge.
+                        store_out<DT>(a.out, (size_t)bh * kHeadDim + lane, A / L);
+                    } else if constexpr (kDes) {
+                        if (it.s != 0) {
+                            // Producer: publish the tagged partial and finish; nothing waits.
+                            put_word(a.tag_out + pidx * kHeadDim + lane, valid_word(A));
+                            if (lane == 0) {
+                                put_word(a.tag_ml + 2 * pidx, valid_word(Mb * kLn2));
+                                put_word(a.tag_ml + 2 * pidx + 1, valid_word(L));
+                            }
+                        } else {
+                            // Designated merger (segment 0): lane u follows segment u.  A head's
+                            // segments have consecutive workgroup ids with segment 0 first, and
+                            // workgroups are dispatched in id order, so the producers waited for are
+                            // already resident or next in line behind workgroups that do not wait:
+                            // the polls end.  The bound only guards against that order failing.
+                            const int n = it.n_seg;
+                            const size_t p0 = (size_t)bh * a.S;
+                            bool lost = n > kMaxDesignatedSegments;
+                            int uj0 = 0, uj1 = 0;
+                            if (lane < n) seg_range(lane, uj0, uj1);
+                            const bool need = lane >= 1 && lane < n && uj1 > uj0 && !lost;
+                            const unsigned long long prod = __ballot(need);   // segments a producer publishes
+                            // Channel words of up to 16 segments per batch; the first batch is
+                            // requested together with the maxima and exp-sums, so up to 17
+                            // segments merge after one memory round trip.
+                            constexpr int kBatch = 16;
+                            auto load_batch = [&](int k, unsigned long long (&w)[kBatch]) {
+#pragma unroll
+                                for (int u = 0; u < kBatch; ++u)
+                                    w[u] = k + u < n && ((prod >> (k + u)) & 1ull)
+                                               ? get_word(a.tag_out + (p0 + k + u) * kHeadDim + lane)
+                                               : kWordValid;
+                            };
+                            auto batch_valid = [&](const unsigned long long (&w)[kBatch]) {
+                                bool ok = true;
+#pragma unroll
+                                for (int u = 0; u < kBatch; ++u) ok = ok && word_valid(w[u]);
+                                return ok;
+                            };
+                            unsigned long long wm = kWordValid, wl = kWordValid, w[kBatch];
+                            for (int r = 0;; ++r) {
+                                if (need) {
+                                    wm = get_word(a.tag_ml + 2 * (p0 + lane));
+                                    wl = get_word(a.tag_ml + 2 * (p0 + lane) + 1);
+                                }
+                                load_batch(1, w);
+                                if (__all(word_valid(wm) && word_valid(wl) && batch_valid(w))) break;
+                                if (r >= kMergePolls) { lost = true; break; }
+                            }
+                            // Merge this wave's partial (segment 0) and the producers' partials, in
+                            // segment order, with merge_partials' arithmetic.
+                            const float pm = lane == 0 ? Mb * kLn2 : (need ? word_value(wm) : kEmptyMax);
+                            const float pl = lane == 0 ? L : (need ? word_value(wl) : 0.0f);
+                            const float Mx = wave_max(pm);
+                            const float LL = wave_sum(exp2_fast((pm - Mx) * kLog2e) * pl);
+                            const float e = exp2_fast((pm - Mx) * kLog2e);
+                            float O = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), 0)) * A;
+                            for (int k = 1; k < n && !lost; k += kBatch) {
+                                if (k > 1) {
+                                    for (int r = 0;; ++r) {
+                                        load_batch(k, w);
+                                        if (__all(batch_valid(w))) break;
+                                        if (r >= kMergePolls) { lost = true; break; }
+                                    }
+                                }
+#pragma unroll
+                                for (int u = 0; u < kBatch; ++u)
+                                    if (k + u < n)
+                                        O = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), k + u)),
+                                                 word_value(w[u]), O);
+                            }
+                            store_out<DT>(a.out, (size_t)bh * kHeadDim + lane, lost ? __builtin_nanf("") : O / LL);
+                            // Leave the producers' slots empty for the next call.
+                            for (unsigned long long clr = prod; clr; clr &= clr - 1) {
+                                const int u = __ffsll((long long)clr) - 1;
+                                put_word(a.tag_out + (p0 + u) * kHeadDim + lane, 0ull);
+                            }
+                            if (need) {
+                                put_word(a.tag_ml + 2 * (p0 + lane), 0ull);
+                                put_word(a.tag_ml + 2 * (p0 + lane) + 1, 0ull);
+                            }
                         }
                     } else {
-                        // Designated merger (segment 0): lane u follows segment u.  A head's
-                        // segments have consecutive workgroup ids with segment 0 first, and
-                        // workgroups are dispatched in id order, so the producers waited for are
-                        // already resident or next in line behind workgroups that do not wait:
-                        // the polls end.  The bound only guards against that order failing.
-                        const int n = it.n_seg;
-                        const size_t p0 = (size_t)bh * a.S;
-                        bool lost = n > kMaxDesignatedSegments;
-                        int uj0 = 0, uj1 = 0;
-                        if (lane < n) seg_range(lane, uj0, uj1);
-                        const bool need = lane >= 1 && lane < n && uj1 > uj0 && !lost;
-                        const unsigned long long prod = __ballot(need);   // segments a producer publishes
-                        // Channel words of up to 16 segments per batch; the first batch is
-                        // requested together with the maxima and exp-sums, so up to 17
-                        // segments merge after one memory round trip.
-                        constexpr int kBatch = 16;
-                        auto load_batch = [&](int k, unsigned long long (&w)[kBatch]) {
-#pragma unroll
-                            for (int u = 0; u < kBatch; ++u)
-                                w[u] = k + u < n && ((prod >> (k + u)) & 1ull)
-                                           ? get_word(a.tag_out + (p0 + k + u) * kHeadDim + lane)
-                                           : kWordValid;
-                        };
-                        auto batch_valid = [&](const unsigned long long (&w)[kBatch]) {
-                            bool ok = true;
-#pragma unroll
-                            for (int u = 0; u < kBatch; ++u) ok = ok && word_valid(w[u]);
-                            return ok;
-                        };
-                        unsigned long long wm = kWordValid, wl = kWordValid, w[kBatch];
-                        for (int r = 0;; ++r) {
-                            if (need) {
-                                wm = get_word(a.tag_ml + 2 * (p0 + lane));
-                                wl = get_word(a.tag_ml + 2 * (p0 + lane) + 1);
-                            }
-                            load_batch(1, w);
-                            if (__all(word_valid(wm) && word_valid(wl) && batch_valid(w))) break;
-                            if (r >= kMergePolls) { lost = true; break; }
-                        }
-                        // Merge this wave's partial (segment 0) and the producers' partials, in
-                        // segment order, with merge_partials' arithmetic.
-                        const float pm = lane == 0 ? Mb * kLn2 : (need ? word_value(wm) : kEmptyMax);
-                        const float pl = lane == 0 ? L : (need ? word_value(wl) : 0.0f);
-                        const float Mx = wave_max(pm);
-                        const float LL = wave_sum(exp2_fast((pm - Mx) * kLog2e) * pl);
-                        const float e = exp2_fast((pm - Mx) * kLog2e);
-                        float O = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), 0)) * A;
-                        for (int k = 1; k < n && !lost; k += kBatch) {
-                            if (k > 1) {
-                                for (int r = 0;; ++r) {
-                                    load_batch(k, w);
-                                    if (__all(batch_valid(w))) break;
-                                    if (r >= kMergePolls) { lost = true; break; }
-                                }
-                            }
-#pragma unroll
-                            for (int u = 0; u < kBatch; ++u)
-                                if (k + u < n)
-                                    O = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), k + u)),
-                                             word_value(w[u]), O);
-                        }
-                        store_out<DT>(a.out, (size_t)bh * kHeadDim + lane, lost ? __builtin_nanf("") : O / LL);
-                        // Leave the producers' slots empty for the next call.
-                        for (unsigned long long clr = prod; clr; clr &= clr - 1) {
-                            const int u = __ffsll((long long)clr) - 1;
-                            put_word(a.tag_out + (p0 + u) * kHeadDim + lane, 0ull);
-                        }
-                        if (need) {
-                            put_word(a.tag_ml + 2 * (p0 + lane), 0ull);
-                            put_word(a.tag_ml + 2 * (p0 + lane) + 1, 0ull);
-                        }
+                        put<kCoh>(a.part_out + pidx * kHeadDim + lane, A);
+                        if (lane == 0) { put<kCoh>(a.part_max + pidx, Mb * kLn2); put<kCoh>(a.part_lse + pidx, L); }
                     }
-                } else {
-                    put<kCoh>(a.part_out + pidx * kHeadDim + lane, A);
-                    if (lane == 0) { put<kCoh>(a.part_max + pidx, Mb * kLn2); put<kCoh>(a.part_lse + pidx, L); }
                 }
             }
         }
-    }
 
-    if constexpr (kMode == kLastBlockMerge) {
-        // Wave 0 wrote this segment's partial with coherent stores.  Once they are
-        // acknowledged it counts the segment; the wave that brings the (b,h) counter to
-        // n_seg reads every partial with coherent loads, merges them and re-arms the
-        // counter for the next call.  A (b,h) of one segment has already written out.
-        if (wave == 0 && it.n_seg > 1) {
-            wait_vm_stores();
-            unsigned prev = 0;
-            if (lane == 0)
-                prev = __hip_atomic_fetch_add(a.counters + bh, 1u, __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT);
-            prev = __shfl(prev, 0);
-            __atomic_signal_fence(__ATOMIC_SEQ_CST);
-            if (prev == (unsigned)(it.n_seg - 1)) {
-                merge_partials<DT, true>(a.out, a.part_out, a.part_lse, a.part_max, a.S, it.n_seg, bh, lane);
+        if constexpr (kMode == kLastBlockMerge) {
+            // Wave 0 wrote this segment's partial with coherent stores.  Once they are
+            // acknowledged it counts the segment; the wave that brings the (b,h) counter to
+            // n_seg reads every partial with coherent loads, merges them and re-arms the
+            // counter for the next call.  A (b,h) of one segment has already written out.
+            if (wave == 0 && it.n_seg > 1) {
+                wait_vm_stores();
+                unsigned prev = 0;
                 if (lane == 0)
-                    __hip_atomic_store(a.counters + bh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    prev = __hip_atomic_fetch_add(a.counters + bh, 1u, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+                prev = __shfl(prev, 0);
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                if (prev == (unsigned)(it.n_seg - 1)) {
+                    merge_partials<DT, true>(a.out, a.part_out, a.part_lse, a.part_max, a.S, it.n_seg, bh, lane);
+                    if (lane == 0)
+                        __hip_atomic_store(a.counters + bh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+        } else if constexpr (kMode == kCoopMerge) {
+            cooperative_groups::this_grid().sync();
+            if (active && it.s == 0 && wave == 0)
+                merge_partials<DT, false>(a.out, a.part_out, a.part_lse, a.part_max, a.S, it.n_seg, bh, lane);
+        }
+    };
+
+    if constexpr (kMode == kPartialsStrided) {
+        // Ragged lengths with fixed-size segments: the host cannot size the grid to the
+        // segments (the lengths are on the device), and a grid sized for maxT leaves
+        // thousands of workgroups that only read the lengths and exit (C5: 5,500 of 12,288,
+        // 3.5 % of the call).  Here the grid is 1/kStridedFactor of that bound and each
+        // workgroup takes segments blockIdx.x, blockIdx.x + gridDim.x, ... of the packed
+        // list: the empties halve, and the workgroups holding two segments are the first
+        // dispatched, so the hardware's dynamic dispatch still balances the tail.  Each
+        // workgroup counts the segments of every sequence once, into LDS, and finds
+        // (b, h, s) there for each of its segments.
+        __shared__ int s_seg_end[kStridedMaxSeqs];   // inclusive prefix of segment counts
+        __shared__ int s_total[kStridedMaxSeqs];     // attended length of each sequence
+        if (wave == 0) {
+            int base = 0;
+            for (int b0 = 0; b0 < a.B; b0 += kWave) {
+                const int b = b0 + lane;
+                int tot = 0, cnt = 0;
+                if (b < a.B) {
+                    int rows;
+                    tot = seq_total(a.cur_len, 1, b, a.maxT);
+                    cnt = a.NH * seg_count(a.seg_rows, tot, a.B * a.NH, rows);
+                }
+                int incl = cnt;
+#pragma unroll
+                for (int d = 1; d < kWave; d <<= 1) {
+                    const int v = __shfl_up(incl, d);
+                    if (lane >= d) incl += v;
+                }
+                if (b < a.B) { s_seg_end[b] = base + incl; s_total[b] = tot; }
+                base += __shfl(incl, kWave - 1);
             }
         }
-    } else if constexpr (kMode == kCoopMerge) {
-        cooperative_groups::this_grid().sync();
-        if (active && it.s == 0 && wave == 0)
-            merge_partials<DT, false>(a.out, a.part_out, a.part_lse, a.part_max, a.S, it.n_seg, bh, lane);
+        __syncthreads();
+        const int count = s_seg_end[a.B - 1];
+        for (int x = blockIdx.x; x < count; x += gridDim.x) {
+            Item it;
+            int b = -1;
+            for (int b0 = 0; b < 0; b0 += kWave) {
+                const int bb = b0 + lane;
+                const unsigned long long hit = __ballot(bb < a.B && s_seg_end[bb] > x);
+                if (hit) b = b0 + __ffsll((long long)hit) - 1;
+            }
+            it.b = b;
+            it.total = s_total[b];
+            it.n_seg = seg_count(a.seg_rows, it.total, a.B * a.NH, it.rows);
+            const int local = x - (b > 0 ? s_seg_end[b - 1] : 0);
+            it.h = local / it.n_seg;
+            it.s = local - it.h * it.n_seg;
+            segment(it, true, t0, q0, fr, false, true, 0, 0, 0, 0);
+            __syncthreads();   // the next segment reuses s_m, s_l, s_acc
+        }
+    } else {
+        Item it;
+        const bool active = locate(a, blockIdx.x, it);
+        if constexpr (kMode != kCoopMerge) {
+            if (!active) return;
+        }
+        segment(it, active, t0, q0, fr, spec, spec_tile, w0, w1, spec_j0, spec_end);
     }
 }
 
@@ -1392,6 +1462,10 @@ int launch_fused_single(void* out, const void* qkv, const void* kv, const float*
 template <int DT, int W, int U, bool kFresh, bool kPaged>
 const void* split_ptr_mode(int mode) {
     if (mode == kPartialsOnly) return (const void*)&split_kernel<DT, kPartialsOnly, W, U, kFresh, kPaged>;
+    if (mode == kPartialsStrided) {
+        if constexpr (W == kWaves) return (const void*)&split_kernel<DT, kPartialsStrided, W, U, kFresh, kPaged>;
+        else return nullptr;
+    }
     if (mode == kLastBlockMerge) return (const void*)&split_kernel<DT, kLastBlockMerge, W, U, kFresh, kPaged>;
     if (mode == kDesignated) return (const void*)&split_kernel<DT, kDesignated, W, U, kFresh, kPaged>;
     if constexpr (kPaged) return nullptr;
@@ -1427,8 +1501,17 @@ int launch_split(const SplitArgs& a, int kv_dtype, int mode, bool lat, hipStream
     const void* fn = split_ptr_for(a, kv_dtype, mode, lat);
     if (!fn) return KVATTN_ERR_DTYPE;
     SplitArgs args = a;
+    const int threads = split_threads(lat);
+    long long grid = (long long)a.B * a.NH * a.S;
+    // Ragged lengths with fixed-size segments on the streaming shape: half the grid, two
+    // packed segments per workgroup (kPartialsStrided).
+    if (mode == kPartialsOnly && !lat && a.lens_per_seq && a.seg_rows != 0 && a.B <= kStridedMaxSeqs) {
+        fn = split_ptr_for(a, kv_dtype, kPartialsStrided, lat);
+        if (!fn) return KVATTN_ERR_DTYPE;
+        grid = (grid + kStridedFactor - 1) / kStridedFactor;
+    }
     void* params[] = {&args};
-    KV_HIP(hipLaunchKernel(fn, dim3((unsigned)a.B * a.NH * a.S), dim3(split_threads(lat)), params, 0, stream));
+    KV_HIP(hipLaunchKernel(fn, dim3((unsigned)grid), dim3(threads), params, 0, stream));
     return KVATTN_OK;
 }
 
