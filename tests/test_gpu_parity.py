@@ -296,6 +296,73 @@ def test_c5_ragged_64_sequences(dev):
         assert float(d.max()) <= 1e-2, f"C5 {name} disagrees with split_merge ({float(d.max()):.3e})"
 
 
+@pytest.mark.parametrize("B", [130, 300])
+def test_ragged_many_sequences_strided_grid(dev, B):
+    """Ragged lengths with more sequences than one wave counts at once: B = 130 takes the
+    half grid whose workgroups count the segments of every sequence in passes of 64 (three
+    here) and take two packed segments each; B = 300 is beyond that kernel's 256-sequence
+    table and runs one segment per workgroup.  Sampled (b,h) slots against the oracle (the
+    last passes included), every slot inside the hull of its V rows, every strategy in
+    agreement, and the fused append identical to append + attention."""
+    import torch
+    kvattn = _kv()
+    NH, maxT = 4, 1024
+    g = torch.Generator(device=dev)
+    g.manual_seed(40 + B)
+    lens = torch.randint(1, maxT + 1, (B,), generator=g, device=dev, dtype=torch.int32)
+    lens[:4] = torch.tensor([1, 257, 512, maxT], dtype=torch.int32, device=dev)
+    cur = (lens - 1).contiguous()
+    cache = torch.randn(2 * B * NH * maxT * HS, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    qkv = torch.randn(B * 3 * NH * HS, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    assert kvattn.plan(B, NH, HS, maxT, kv_dtype="bf16")[0] == kvattn.STRATEGIES["split_merge"]
+    outs = {}
+    for strategy in ("auto", "split_merge", "lastblock"):
+        out = torch.empty(B * NH * HS, dtype=torch.bfloat16, device=dev)
+        ws = kvattn.Workspace(B, NH, maxT, 0)
+        kvattn.decode(out, qkv, cache, B, NH, HS, maxT, kv_dtype="bf16", cur_len=cur, lens_per_seq=True,
+                      strategy=strategy, **ws.kwargs())
+        torch.cuda.synchronize()
+        outs[strategy] = out.float()
+    lens_h = lens.cpu().numpy()
+    q_h = qkv.float().cpu().numpy().reshape(B, 3, NH, HS)
+    rng = np.random.RandomState(B)
+    picks = [(int(b), int(h)) for b, h in zip(rng.randint(0, B, 12), rng.randint(0, NH, 12))]
+    picks += [(0, 0), (3, NH - 1), (63, 1), (64, 2), (127, 0), (128, 3), (B - 1, NH - 1)]
+    kv5 = cache.view(2, B, NH, maxT, HS)
+    for b, h in picks:
+        T = int(lens_h[b])
+        k = kv5[0, b, h, :T].float().cpu().numpy()
+        v = kv5[1, b, h, :T].float().cpu().numpy()
+        q1 = np.zeros((1, 3, 1, HS), np.float32)
+        q1[0, 0, 0] = q_h[b, 0, h]
+        ref = oracle.attention_f32(q1.reshape(-1), np.stack([k, v]).reshape(-1), T, 1, 1, HS, T)
+        for name, o in outs.items():
+            assert_close(o.view(B, NH, HS)[b, h].cpu().numpy(), ref, "bf16", f"B={B} {name} b={b} h={h} T={T}")
+    pos = torch.arange(maxT, device=dev).view(1, 1, maxT, 1)
+    valid = pos < lens.view(B, 1, 1, 1)
+    vv = kv5[1].float()
+    vmin = torch.where(valid, vv, torch.full_like(vv, float("inf"))).amin(dim=2)
+    vmax = torch.where(valid, vv, torch.full_like(vv, float("-inf"))).amax(dim=2)
+    for name, o in outs.items():
+        o3 = o.view(B, NH, HS)
+        slack = 1e-2 * (vmax - vmin).abs() + 1e-3
+        assert bool(((o3 >= vmin - slack) & (o3 <= vmax + slack)).all()), f"B={B} {name} outside V hull"
+        d = (o3 - outs["lastblock"].view(B, NH, HS)).norm(dim=2) / outs["lastblock"].view(B, NH, HS).norm(dim=2)
+        assert float(d.max()) <= 1e-2, f"B={B} {name} disagrees with lastblock ({float(d.max()):.3e})"
+    # The fused append on the same grid: identical cache bytes and outputs to append + attention.
+    ws = kvattn.Workspace(B, NH, maxT, 0)
+    c_a, c_b = cache.clone(), cache.clone()
+    o_a = torch.empty(B * NH * HS, dtype=torch.bfloat16, device=dev)
+    o_b = torch.empty_like(o_a)
+    kw = dict(kv_dtype="bf16", cur_len=cur, lens_per_seq=True, strategy="split_merge", **ws.kwargs())
+    kvattn.kv_cache_write(c_a, qkv, B, NH, HS, maxT, kv_dtype="bf16", cur_len=cur, lens_per_seq=True)
+    kvattn.decode(o_a, qkv, c_a, B, NH, HS, maxT, **kw)
+    kvattn.append_decode(o_b, qkv, c_b, B, NH, HS, maxT, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(c_a.view(torch.int16), c_b.view(torch.int16)), f"B={B}: appended cache"
+    assert torch.equal(o_a.view(torch.int16), o_b.view(torch.int16)), f"B={B}: fused append output"
+
+
 # ---------------------------------------------------------------------------------
 # Graph capture with a device-resident length
 # ---------------------------------------------------------------------------------
