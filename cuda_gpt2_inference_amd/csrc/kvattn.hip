@@ -970,11 +970,13 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
     // request theirs once the length shows that they have rows.  A segment the length plans
     // otherwise (doubled rows) drops the guess and requests its true first tile.
     constexpr bool kDev = kMode == kDesignatedDev;
-    Tile<DT, kU> t0;
-    QRaw<DT> q0;
-    FreshRaw<DT> fr{};
-    bool spec = false, spec_tile = true;
-    int w0 = 0, w1 = 0, spec_j0 = 0, spec_end = 0;
+    // The guess: first tile, q slice and fresh row; whether it was made and holds this
+    // wave's tile; this wave's rows of the nominal range; the nominal range [g_j0, g_end).
+    Tile<DT, kU> g_tile;
+    QRaw<DT> g_q;
+    FreshRaw<DT> g_fresh{};
+    bool g_on = false, g_has_tile = true;
+    int g_w0 = 0, g_w1 = 0, g_j0 = 0, g_end = 0;
     if (!kPaged && kMode != kPartialsStrided && !a.lens_per_seq && (kDev || a.seg_rows > 0)) {
         const int nom = kDev ? designated_base_rows(a.B * a.NH) : a.seg_rows;
         const int bh0 = blockIdx.x / a.S;
@@ -983,27 +985,28 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
         const int nend = min(j0 + (first ? kFusedMaxRows : nom), a.maxT);
         // 8-bit caches guess only in segment 0's early share: measured, the producers' early
         // tiles cost 8-bit calls more than the length's round trip they hide.
-        const bool guess = !(R::k8bit && kDev && !first);
-        if (guess && (kDev || j0 < a.spec_rows) && j0 < nend) {
+        const bool allowed = !(R::k8bit && kDev && !first);
+        if (allowed && (kDev || j0 < a.spec_rows) && j0 < nend) {
             const int per = ceil_div_i(nend - j0, kW);
-            w0 = min(j0 + wave * per, nend);
-            w1 = min(w0 + per, nend);
-            spec_j0 = j0;
-            spec_end = nend;
-            spec_tile = !first || w1 <= j0 + nom;
+            g_w0 = min(j0 + wave * per, nend);
+            g_w1 = min(g_w0 + per, nend);
+            g_j0 = j0;
+            g_end = nend;
+            g_has_tile = !first || g_w1 <= j0 + nom;
             const int b0 = bh0 / a.NH;
             const Slot sl0 = make_slot<DT>(a.kv, a.kv_scale, a.B, a.NH, a.maxT, bh0, slice);
-            if (spec_tile) load_tile<DT, kU, true>(t0, sl0, w0, w1, slot_row);
-            q0 = load_q<DT>(a.qkv, b0, bh0 - b0 * a.NH, a.NH, slice);
-            if constexpr (kFresh) fr = load_fresh<DT>(a.qkv, b0, bh0 - b0 * a.NH, a.NH, slice);
-            spec = true;
+            if (g_has_tile) load_tile<DT, kU, true>(g_tile, sl0, g_w0, g_w1, slot_row);
+            g_q = load_q<DT>(a.qkv, b0, bh0 - b0 * a.NH, a.NH, slice);
+            if constexpr (kFresh) g_fresh = load_fresh<DT>(a.qkv, b0, bh0 - b0 * a.NH, a.NH, slice);
+            g_on = true;
         }
     }
 
     // The work of one segment `it` (active: the workgroup has one; the cooperative launch
-    // also runs it without, for the grid barrier).  The guess made above comes in through
-    // the parameters, so that the strided loop below passes its own (empty) guess and
-    // carries no tile from one segment to the next.
+    // also runs it without, for the grid barrier).  The guess comes in through the
+    // parameters (spec: made; spec_tile: holds this wave's tile; [spec_j0, spec_end): its
+    // nominal range), so that the strided loop below passes an empty one and carries no
+    // tile from one segment to the next.
     auto segment = [&](const Item& it, const bool active, Tile<DT, kU>& t0, QRaw<DT>& q0, FreshRaw<DT>& fr,
                        const bool spec, const bool spec_tile, int w0, int w1, const int spec_j0,
                        const int spec_end) {
@@ -1256,7 +1259,10 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
             const int local = x - (b > 0 ? s_seg_end[b - 1] : 0);
             it.h = local / it.n_seg;
             it.s = local - it.h * it.n_seg;
-            segment(it, true, t0, q0, fr, false, true, 0, 0, 0, 0);
+            Tile<DT, kU> t;
+            QRaw<DT> q;
+            FreshRaw<DT> f{};
+            segment(it, true, t, q, f, false, true, 0, 0, 0, 0);
             __syncthreads();   // the next segment reuses s_m, s_l, s_acc
         }
     } else {
@@ -1265,7 +1271,7 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
         if constexpr (kMode != kCoopMerge) {
             if (!active) return;
         }
-        segment(it, active, t0, q0, fr, spec, spec_tile, w0, w1, spec_j0, spec_end);
+        segment(it, active, g_tile, g_q, g_fresh, g_on, g_has_tile, g_w0, g_w1, g_j0, g_end);
     }
 }
 
