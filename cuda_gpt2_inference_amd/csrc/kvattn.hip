@@ -1511,7 +1511,9 @@ int launch_split(const SplitArgs& a, int kv_dtype, int mode, bool lat, hipStream
     long long grid = (long long)a.B * a.NH * a.S;
     // Ragged lengths with fixed-size segments on the streaming shape: half the grid, two
     // packed segments per workgroup (kPartialsStrided).
-    if (mode == kPartialsOnly && !lat && a.lens_per_seq && a.seg_rows != 0 && a.B <= kStridedMaxSeqs) {
+    // (Below 2^30 slots, so that x + gridDim.x in the kernel's walk stays within int.)
+    if (mode == kPartialsOnly && !lat && a.lens_per_seq && a.seg_rows != 0 && a.B <= kStridedMaxSeqs &&
+        grid < (1ll << 30)) {
         fn = split_ptr_for(a, kv_dtype, kPartialsStrided, lat);
         if (!fn) return KVATTN_ERR_DTYPE;
         grid = (grid + kStridedFactor - 1) / kStridedFactor;
