@@ -523,6 +523,45 @@ def gemv_configs(torch, kvattn, dev, layers=12, reps=100):
     return res
 
 
+def qkv_append_configs(torch, kvattn, dev, layers=12, reps=100):
+    """The QKV projection followed by the KV append, per layer of a 12-layer graph (B = 1,
+    NH = 12, BF16 weights and cache, maxT = 1024): two launches (kvattn_gemv then
+    kvattn_cache_write) against one (kvattn_gemv_qkv_append)."""
+    NH, K, maxT = 12, 768, 1024
+    M = 3 * NH * HD
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    Ws = [(torch.randn(M * K, generator=g, device=dev) / K ** 0.5).to(torch.bfloat16) for _ in range(layers)]
+    caches = [torch.zeros(2 * NH * maxT * HD, device=dev, dtype=torch.bfloat16) for _ in range(layers)]
+    x = torch.randn(K, generator=g, device=dev).to(torch.bfloat16)
+    bias = torch.randn(M, generator=g, device=dev).to(torch.bfloat16)
+    qkv = torch.empty(M, device=dev, dtype=torch.bfloat16)
+    cur = torch.tensor([maxT // 2], dtype=torch.int32, device=dev)
+
+    def separate():
+        for l in range(layers):
+            kvattn.gemv(qkv, Ws[l], x, 1, M, K, w_dtype="bf16", bias=bias)
+            kvattn.kv_cache_write(caches[l], qkv, 1, NH, HD, maxT, kv_dtype="bf16", cur_len=cur)
+
+    def fused():
+        for l in range(layers):
+            kvattn.gemv_qkv_append(qkv, Ws[l], x, 1, NH, HD, K, caches[l], maxT, w_dtype="bf16", bias=bias,
+                                   cur_len=cur)
+    res = {}
+    for name, step in (("gemv_then_append", separate), ("gemv_qkv_append", fused)):
+        s = torch.cuda.Stream()
+        graph = torch.cuda.CUDAGraph()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(graph, stream=s):
+                step()
+        graph.replay()
+        with phase(f"qkv_{name}"):
+            us = timed(torch, graph.replay, reps) * 1000.0 / layers
+        res[name] = {"us_per_layer": round(us, 3)}
+    return res
+
+
 def gemv_cpu_baseline(seconds=3.0):
     """oracle_gemv (FP32, one thread) at the attention output projection, 768 x 768."""
     from oracle import oracle
@@ -784,6 +823,7 @@ def main():
                                 C5Paged.NH, paged=True, ragged=True))
     configs = None if args.no_configs else other_configs(torch, kvattn, dev)
     gemv = None if args.no_configs else gemv_configs(torch, kvattn, dev)
+    qkv_append = None if args.no_configs else qkv_append_configs(torch, kvattn, dev)
     gemv_cpu = None if (args.no_configs or args.no_cpu) else gemv_cpu_baseline()
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds, c2)
 
@@ -814,7 +854,7 @@ def main():
                   "cold_us_per_call": round(cold_us, 3),
                   "c2_context_sweep": t_sweep,
                   "c2_token_sweep": tok_sweep,
-                  "gemv": gemv, "gemv_cpu_baseline": gemv_cpu,
+                  "gemv": gemv, "gemv_qkv_append": qkv_append, "gemv_cpu_baseline": gemv_cpu,
                   "rel_err_vs_f64": rel,
                   "gpu_vs_cpu_speedup": (round(cpu["value"] / us_call, 1) if cpu else None),
                   "c5": c5, "configs": configs, "gpu": torch.cuda.get_device_name(dev),

@@ -47,6 +47,12 @@ struct GemvArgs {
     const uint8_t* x;
     const void* bias;
     int B, M, K, gelu;
+    // QKV projection with the KV append in its epilogue (kv != nullptr): out is qkv
+    // [B][3][NH][64], and its K and V rows also go to column cur_len of the cache
+    // [2][B][NH][maxT][64] (activation type).
+    uint8_t* kv;
+    const int* cur_len;
+    int lens_per_seq, NH, maxT;
 };
 
 // Dot product of one 16-byte weight chunk with the x values it multiplies.
@@ -137,6 +143,21 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(GemvArgs a) {
             if (a.pre_gelu) store_act<WT>(a.pre_gelu, o, pre);
             if (a.gelu) pre = gelu_tanh(pre);
             store_act<WT>(a.out, o, pre);
+            if (a.kv) {
+                // Output m is channel c of head h of part q/k/v; K and V also land in the cache
+                // row of position cur_len, as the separate append would copy them.
+                constexpr int kHd = 64;
+                const int per_part = a.NH * kHd;
+                const int part = m / per_part;
+                if (part > 0) {
+                    const int h = (m - part * per_part) / kHd, c = m - part * per_part - h * kHd;
+                    int cl = a.cur_len[a.lens_per_seq ? b : 0];
+                    cl = cl < 0 ? 0 : (cl > a.maxT - 1 ? a.maxT - 1 : cl);
+                    size_t row = ((size_t)b * a.NH + h) * a.maxT + cl;
+                    if (part == 2) row += (size_t)a.B * a.NH * a.maxT;
+                    store_act<WT>(a.kv, row * kHd + c, pre);
+                }
+            }
         }
     }
 }
@@ -156,20 +177,23 @@ namespace kvattn_internal {
 void set_last_hip_error(int e);   // kvattn.hip: read back by kvattn_last_hip_error
 }
 
-extern "C" int kvattn_gemv(void* out, void* pre_gelu, const void* W, const float* w_scale, const void* x,
-                           const void* bias, int B, int M, int K, int w_dtype, int gelu, void* stream) {
+namespace {
+
+// Checks shared by both entry points, then the launch.
+int launch_gemv(GemvArgs a, int w_dtype, void* stream) {
     if (w_dtype < KVATTN_KV_F32 || w_dtype > KVATTN_KV_FP8_E4M3) return KVATTN_ERR_DTYPE;
     const bool w8 = w_dtype == KVATTN_KV_INT8 || w_dtype == KVATTN_KV_FP8_E4M3;
     const int wbytes = w_dtype == KVATTN_KV_F32 ? 4 : (w_dtype == KVATTN_KV_BF16 ? 2 : 1);
     const size_t act = w_dtype == KVATTN_KV_F32 ? 4 : 2;
+    const int B = a.B, M = a.M, K = a.K;
     if (B < 1 || M < 1 || K < 16 || K % 16 != 0) return KVATTN_ERR_SHAPE;
     if ((long long)K * wbytes > (long long)kGemvMaxChunks * kWave * 16) return KVATTN_ERR_SHAPE;
     if ((long long)B * M >= (1ll << 31) || (long long)M * K * wbytes >= (1ll << 40)) return KVATTN_ERR_SHAPE;
-    if (!out || !W || !x) return KVATTN_ERR_NULL_POINTER;
-    if (w8 && !w_scale) return KVATTN_ERR_DTYPE;
-    if (((uintptr_t)W & 15u) || ((uintptr_t)x & 15u)) return KVATTN_ERR_MISALIGNED;
-    if (((uintptr_t)out % act) || ((uintptr_t)pre_gelu % act) || ((uintptr_t)bias % act) ||
-        ((uintptr_t)w_scale & 3u))
+    if (!a.out || !a.W || !a.x) return KVATTN_ERR_NULL_POINTER;
+    if (w8 && !a.w_scale) return KVATTN_ERR_DTYPE;
+    if (((uintptr_t)a.W & 15u) || ((uintptr_t)a.x & 15u)) return KVATTN_ERR_MISALIGNED;
+    if (((uintptr_t)a.out % act) || ((uintptr_t)a.pre_gelu % act) || ((uintptr_t)a.bias % act) ||
+        ((uintptr_t)a.w_scale & 3u) || ((uintptr_t)a.kv % act))
         return KVATTN_ERR_MISALIGNED;
     const int nch = K * wbytes / 16;
     const int per_lane = (nch + kWave - 1) / kWave;
@@ -180,7 +204,6 @@ extern "C" int kvattn_gemv(void* out, void* pre_gelu, const void* W, const float
         case KVATTN_KV_INT8: fn = gemv_ptr<KVATTN_KV_INT8>(per_lane); break;
         default: fn = gemv_ptr<KVATTN_KV_FP8_E4M3>(per_lane); break;
     }
-    GemvArgs a{out, pre_gelu, (const uint8_t*)W, w_scale, (const uint8_t*)x, bias, B, M, K, gelu ? 1 : 0};
     void* params[] = {&a};
     const hipError_t e = hipLaunchKernel(fn, dim3((unsigned)((M + kGemvWaves - 1) / kGemvWaves)),
                                          dim3(kGemvWaves * kWave), params, 0, (hipStream_t)stream);
@@ -189,4 +212,30 @@ extern "C" int kvattn_gemv(void* out, void* pre_gelu, const void* W, const float
         return KVATTN_ERR_HIP;
     }
     return KVATTN_OK;
+}
+
+}  // namespace
+
+extern "C" int kvattn_gemv(void* out, void* pre_gelu, const void* W, const float* w_scale, const void* x,
+                           const void* bias, int B, int M, int K, int w_dtype, int gelu, void* stream) {
+    GemvArgs a{out, pre_gelu, (const uint8_t*)W, w_scale, (const uint8_t*)x, bias, B, M, K, gelu ? 1 : 0,
+               nullptr, nullptr, 0, 0, 0};
+    return launch_gemv(a, w_dtype, stream);
+}
+
+extern "C" int kvattn_gemv_qkv_append(void* qkv, const void* W, const float* w_scale, const void* x,
+                                      const void* bias, int B, int NH, int hs, int K, void* kv_cache, int maxT,
+                                      const int* d_cur_len, int lens_per_seq, int w_dtype, void* stream) {
+    if (hs != 64) return KVATTN_ERR_HEAD_DIM;
+    if (B < 1 || NH < 1 || maxT < 1 || (long long)B * NH > (1ll << 24) || maxT > (1 << 23)) return KVATTN_ERR_SHAPE;
+    if (!kv_cache) return KVATTN_ERR_NULL_POINTER;
+    if (!d_cur_len) {
+        int* sym = nullptr;
+        const int st = kvattn_cur_len_symbol(&sym);
+        if (st != KVATTN_OK) return st;
+        d_cur_len = sym;
+    }
+    GemvArgs a{qkv, nullptr, (const uint8_t*)W, w_scale, (const uint8_t*)x, bias, B, 3 * NH * hs, K, 0,
+               (uint8_t*)kv_cache, d_cur_len, lens_per_seq ? 1 : 0, NH, maxT};
+    return launch_gemv(a, w_dtype, stream);
 }

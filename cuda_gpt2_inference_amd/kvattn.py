@@ -89,6 +89,7 @@ SIGNATURES = {
     "kvattn_decode": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp, _sz, _i, _i, _i, _vp]),
     "kvattn_append_decode": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp, _sz, _i, _i, _i, _vp]),
     "kvattn_gemv": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
+    "kvattn_gemv_qkv_append": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _vp, _i, _i, _vp]),
     "kvattn_paged_cache_write": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _i, _i, _i, _vp, _i, _i, _vp]),
     "kvattn_paged_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _i, _i, _vp, _sz, _i, _i,
                                  _i, _i, _vp]),
@@ -265,6 +266,14 @@ def gemv(out, W, x, B, M, K, *, w_dtype, w_scale=None, bias=None, pre_gelu=None,
     """Decode-step fully connected layer out = [GELU](W x [* w_scale] + bias) (kvattn_gemv)."""
     _check(lib().kvattn_gemv(_ptr(out), _ptr(pre_gelu), _ptr(W), _ptr(w_scale), _ptr(x), _ptr(bias), B, M, K,
                              kv_dtype_code(w_dtype), int(bool(gelu)), _stream(stream)), "kvattn_gemv")
+
+
+def gemv_qkv_append(qkv, W, x, B, NH, hs, K, kv_cache, maxT, *, w_dtype, w_scale=None, bias=None, cur_len=None,
+                    lens_per_seq=False, stream=None) -> None:
+    """QKV projection with the KV append in its epilogue (kvattn_gemv_qkv_append)."""
+    _check(lib().kvattn_gemv_qkv_append(_ptr(qkv), _ptr(W), _ptr(w_scale), _ptr(x), _ptr(bias), B, NH, hs, K,
+                                        _ptr(kv_cache), maxT, _ptr(cur_len), int(bool(lens_per_seq)),
+                                        kv_dtype_code(w_dtype), _stream(stream)), "kvattn_gemv_qkv_append")
 
 
 class PagedCache:

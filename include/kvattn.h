@@ -253,6 +253,18 @@ int kvattn_paged_decode(void* out, const void* qkv, void* pages, float* page_sca
 int kvattn_gemv(void* out, void* pre_gelu, const void* W, const float* w_scale, const void* x,
                 const void* bias, int B, int M, int K, int w_dtype, int gelu, void* stream);
 
+/* The QKV projection with the KV append in its epilogue: kvattn_gemv with M = 3 * NH * hs
+ * (no GELU) into qkv [B][3][NH][hs], whose K and V rows also go to column cur_len of
+ * kv_cache [2][B][NH][maxT][hs] (the value kvattn_cache_write would copy, bit for bit).
+ * The cache holds the activation type: float for F32 weights, bf16 otherwise (8-bit caches,
+ * whose row scale needs the whole head row, are not covered: take kvattn_append_decode).
+ * d_cur_len as in kvattn_decode (NULL: the library's device length).  hs must be 64.
+ * Replaces the QKV GEMV followed by the append launch (inference_gpt2_opt.cu:290-303; the
+ * append kernel attention_kvcache.cuh:46-64), one launch fewer per layer. */
+int kvattn_gemv_qkv_append(void* qkv, const void* W, const float* w_scale, const void* x,
+                           const void* bias, int B, int NH, int hs, int K, void* kv_cache, int maxT,
+                           const int* d_cur_len, int lens_per_seq, int w_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

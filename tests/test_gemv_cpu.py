@@ -121,3 +121,29 @@ def test_gemv_argument_errors(kw, status):
     st = kvattn.lib().kvattn_gemv(a["out"], a["pre"], a["W"], a["w_scale"], a["x"], a["bias"], a["B"], a["M"],
                                   a["K"], a["w_dtype"], a["gelu"], None)
     assert st == status, kvattn.strerror(st)
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(hs=32), 3),                   # KVATTN_ERR_HEAD_DIM
+    (dict(B=0), 4),                     # KVATTN_ERR_SHAPE
+    (dict(NH=0), 4),
+    (dict(maxT=0), 4),
+    (dict(maxT=(1 << 23) + 1), 4),
+    (dict(K=24), 4),
+    (dict(kv=None), 1),                 # KVATTN_ERR_NULL_POINTER
+    (dict(W=None), 1),
+    (dict(w_dtype=7), 5),               # KVATTN_ERR_DTYPE
+    (dict(kv=ALIGNED + 1), 2),          # KVATTN_ERR_MISALIGNED (bf16 cache)
+    (dict(qkv=ALIGNED + 2, w_dtype=0), 2),
+])
+def test_gemv_qkv_append_argument_errors(kw, status):
+    """kvattn_gemv_qkv_append's checks, made before any HIP call (a device length is given,
+    so the library's own length symbol is not looked up)."""
+    from cuda_gpt2_inference_amd import kvattn
+    a = dict(qkv=ALIGNED, W=ALIGNED, w_scale=ALIGNED, x=ALIGNED, bias=None, B=1, NH=12, hs=64, K=768, kv=ALIGNED,
+             maxT=1024, cur=ALIGNED, lens=0, w_dtype=1)
+    a.update(kw)
+    st = kvattn.lib().kvattn_gemv_qkv_append(a["qkv"], a["W"], a["w_scale"], a["x"], a["bias"], a["B"], a["NH"],
+                                             a["hs"], a["K"], a["kv"], a["maxT"], a["cur"], a["lens"],
+                                             a["w_dtype"], None)
+    assert st == status, kvattn.strerror(st)

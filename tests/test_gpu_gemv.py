@@ -110,3 +110,45 @@ def test_gemv_ragged_shapes(dev, dtype, M, K):
     got, _ = _run(d, dtype, 2, M, K, False, False)
     ref = oracle.gemv(h["W"], h["x"], 2, M, K, w_scale=h["scale"])
     _check(got, ref, dtype, 2, M, f"M={M} K={K} {dtype}")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "int8"])
+@pytest.mark.parametrize("lens", ["uniform", "ragged", "library"])
+def test_gemv_qkv_append_equals_gemv_then_append(dev, dtype, lens):
+    """kvattn_gemv_qkv_append against kvattn_gemv + kvattn_cache_write on copies of the same
+    cache: identical qkv bytes and identical cache bytes (the appended K and V rows and every
+    other row), at GPT-2's QKV shape (NH = 12: 2304 x 768), with one device length, per-
+    sequence lengths (one of them beyond maxT, clamped), and the library's own length."""
+    import torch
+    kvattn = _kv()
+    NH, HS, K, maxT = 12, 64, 768, 96
+    B = 1 if lens == "uniform" else 3
+    M = 3 * NH * HS
+    d, _ = _make(dtype, B, M, K, seed=70 + B)
+    W, x = d["W"].to(dev), d["x"].to(dev).contiguous()
+    bias = None if d["bias"] is None else d["bias"].to(dev)
+    scale = None if d.get("scale") is None else d["scale"].to(dev)
+    act = torch.float32 if dtype == "f32" else torch.bfloat16
+    g = torch.Generator(device=dev)
+    g.manual_seed(71)
+    cache = torch.randn(2 * B * NH * maxT * HS, generator=g, device=dev).to(act)
+    if lens == "uniform":
+        cur, per_seq = torch.tensor([40], dtype=torch.int32, device=dev), False
+    elif lens == "ragged":
+        cur, per_seq = torch.tensor([0, maxT - 1, maxT + 10], dtype=torch.int32, device=dev), True
+    else:
+        kvattn.set_cur_len(17)
+        cur, per_seq = None, False
+    c_a, c_b = cache.clone(), cache.clone()
+    q_a = torch.empty(B * M, dtype=act, device=dev)
+    q_b = torch.empty_like(q_a)
+    kvattn.gemv(q_a, W, x, B, M, K, w_dtype=dtype, w_scale=scale, bias=bias)
+    kvattn.kv_cache_write(c_a, q_a, B, NH, HS, maxT, kv_dtype="f32" if dtype == "f32" else "bf16", cur_len=cur,
+                          lens_per_seq=per_seq)
+    kvattn.gemv_qkv_append(q_b, W, x, B, NH, HS, K, c_b, maxT, w_dtype=dtype, w_scale=scale, bias=bias,
+                           cur_len=cur, lens_per_seq=per_seq)
+    torch.cuda.synchronize()
+    iview = torch.int32 if dtype == "f32" else torch.int16
+    assert torch.equal(q_a.view(iview), q_b.view(iview)), f"{dtype} {lens}: qkv"
+    assert torch.equal(c_a.view(iview), c_b.view(iview)), f"{dtype} {lens}: cache"
+    assert not torch.equal(c_a.view(iview), cache.view(iview)), f"{dtype} {lens}: nothing appended"
