@@ -783,12 +783,21 @@ constexpr int kDesignatedMaxGrid = 256;  // AUTO: designated merger while heads 
 // between kMinSegRows and kMaxSegRows.  The host plans with it from its length hint; with
 // seg_rows == kDevicePlan every workgroup plans with it from the device length, so one
 // launch (or one captured graph) serves every length up to maxT.
+// Smallest power of two >= x (x >= 1), without a loop or branch, so that kernels can keep
+// loads issued before a plan is computed in flight across it.
+__host__ __device__ __forceinline__ int ceil_pow2(int x) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const int lz = __clz(x - 1);
+#else
+    const int lz = x > 1 ? __builtin_clz((unsigned)(x - 1)) : 32;
+#endif
+    return x > 1 ? 1 << (32 - lz) : 1;
+}
+
 __host__ __device__ __forceinline__ int planned_rows(int total) {
-    if (total <= kFusedMaxRows) return total > 0 ? total : 1;
     const int want = ceil_div_i(total, 4);
-    int r = kMinSegRows;
-    while (r < want && r < kMaxSegRows) r <<= 1;
-    return r;
+    const int r = min(max(kMinSegRows, ceil_pow2(max(want, 1))), kMaxSegRows);
+    return total <= kFusedMaxRows ? (total > 0 ? total : 1) : r;
 }
 
 // Rows per segment for the designated merger over `heads` = B*NH slots: the whole length
@@ -798,10 +807,8 @@ __host__ __device__ __forceinline__ int planned_rows(int total) {
 // get more than 64 segments.
 __host__ __device__ __forceinline__ int designated_base_rows(int heads) { return heads <= 16 ? 128 : 256; }
 __host__ __device__ __forceinline__ int designated_rows(int total, int heads) {
-    if (total <= kFusedMaxRows) return total > 0 ? total : 1;
-    int r = designated_base_rows(heads);
-    while ((long long)r * kMaxDesignatedSegments < total) r <<= 1;
-    return r;
+    const int r = max(designated_base_rows(heads), ceil_pow2(max(ceil_div_i(total, kMaxDesignatedSegments), 1)));
+    return total <= kFusedMaxRows ? (total > 0 ? total : 1) : r;
 }
 
 // Segments of a (b,h) whose length is `total` under fixed or device-planned rows
@@ -1280,9 +1287,38 @@ template <int DT>
 __global__ __launch_bounds__(kWave) void merge_kernel(SplitArgs a) {
     const int bh = blockIdx.x;
     const int b = bh / a.NH;
+    const int c = threadIdx.x;
+    constexpr int kBatch = 16;
     int n_seg = a.S, rows;
+    if (a.seg_rows != 0 && a.S <= kBatch) {
+        // The segment count follows from the device length.  Every slot's partial is
+        // requested together with that length (one memory round trip instead of two), and
+        // the slots beyond the count, whose words are stale, are dropped by selects.  The
+        // arithmetic is merge_partials' for one batch.
+        // Slot indices are clamped to S - 1 rather than branched on, so that no load sits
+        // behind a branch and all of them issue ahead of the length's wait.
+        const size_t p0 = (size_t)bh * a.S;
+        const int last = a.S - 1;
+        const float pm_all = a.part_max[p0 + min(c, last)];
+        const float pl_all = a.part_lse[p0 + min(c, last)];
+        float v[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) v[u] = a.part_out[(p0 + min(u, last)) * kHeadDim + c];
+        n_seg = seg_count(a.seg_rows, seq_total(a.cur_len, a.lens_per_seq, b, a.maxT), a.B * a.NH, rows);
+        const float pm = c < n_seg ? pm_all : kEmptyMax;
+        const float pl = c < n_seg ? pl_all : 0.0f;
+        const float M = fmaxf(kEmptyMax, wave_max(pm));
+        const float L = 0.0f * exp2_fast((kEmptyMax - M) * kLog2e) + wave_sum(exp2_fast((pm - M) * kLog2e) * pl);
+        const float e = exp2_fast((pm - M) * kLog2e);
+        float O = 0.0f;
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u)
+            O = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), u)), u < n_seg ? v[u] : 0.0f, O);
+        store_out<DT>(a.out, (size_t)bh * kHeadDim + c, O / L);
+        return;
+    }
     if (a.seg_rows != 0) n_seg = seg_count(a.seg_rows, seq_total(a.cur_len, a.lens_per_seq, b, a.maxT), a.B * a.NH, rows);
-    merge_partials<DT, false>(a.out, a.part_out, a.part_lse, a.part_max, a.S, n_seg, bh, threadIdx.x);
+    merge_partials<DT, false>(a.out, a.part_out, a.part_lse, a.part_max, a.S, n_seg, bh, c);
 }
 
 // ------------------------------------------------------------------------------------

@@ -127,3 +127,29 @@ def test_binding_raises_with_status_and_text():
     with pytest.raises(kvattn.KvAttnError) as ei:
         kvattn.decode(ALIGNED, ALIGNED, ALIGNED, 1, 12, 64, 1024, kv_dtype="bf16", len_hint=1023, stream=0)
     assert ei.value.status == kvattn.ERR_WORKSPACE     # split plan without a workspace
+
+
+def _designated_rows_loop(total, heads):
+    """The designated merger's segment length, as the rule reads: the whole length up to 256
+    positions; otherwise 128 rows (256 beyond 16 heads), doubled while 64 segments do not
+    cover the length."""
+    if total <= 256:
+        return max(total, 1)
+    r = 128 if heads <= 16 else 256
+    while r * 64 < total:
+        r <<= 1
+    return r
+
+
+@pytest.mark.parametrize("heads", [1, 16, 17])
+def test_designated_rows_closed_form_matches_the_rule(heads):
+    """The library computes the designated rows without a loop (a power of two from a count
+    of leading zeros); the host plan, with maxT = the hinted length, reports them."""
+    totals = sorted({t for e in (256, 8192, 16384, 32768, 1 << 20) for t in (e - 1, e, e + 1)} |
+                    {257, 300, 1000, 4097, 12345, 65536, 100000, 777777, (1 << 22) - 3, 1 << 22})
+    for total in totals:
+        rows = _designated_rows_loop(total, heads)
+        st, slots, got = kvattn.plan(1, heads, 64, total, kv_dtype="bf16", len_hint=total - 1,
+                                     strategy="designated")
+        assert (st, got) == (kvattn.SPLIT_DESIGNATED, rows if total > 256 else total), (total, heads)
+        assert slots == -(-total // got)
