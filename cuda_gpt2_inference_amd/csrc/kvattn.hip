@@ -1141,6 +1141,12 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                                 for (int u = 0; u < kBatch; ++u) ok = ok && word_valid(w[u]);
                                 return ok;
                             };
+                            auto clear_batch = [&](int k) {
+#pragma unroll
+                                for (int u = 0; u < kBatch; ++u)
+                                    if (k + u < n && ((prod >> (k + u)) & 1ull))
+                                        put_word(a.tag_out + (p0 + k + u) * kHeadDim + lane, 0ull);
+                            };
                             unsigned long long wm = kWordValid, wl = kWordValid, w[kBatch];
                             for (int r = 0;; ++r) {
                                 if (need) {
@@ -1150,6 +1156,13 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                                 load_batch(1, w);
                                 if (__all(word_valid(wm) && word_valid(wl) && batch_valid(w))) break;
                                 if (r >= kMergePolls) { lost = true; break; }
+                            }
+                            // The words just read are not needed again: empty their slots for the next
+                            // call now, so that these stores complete while the merge runs.
+                            clear_batch(1);
+                            if (need) {
+                                put_word(a.tag_ml + 2 * (p0 + lane), 0ull);
+                                put_word(a.tag_ml + 2 * (p0 + lane) + 1, 0ull);
                             }
                             // Merge this wave's partial (segment 0) and the producers' partials, in
                             // segment order, with merge_partials' arithmetic.
@@ -1166,6 +1179,7 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                                         if (__all(batch_valid(w))) break;
                                         if (r >= kMergePolls) { lost = true; break; }
                                     }
+                                    clear_batch(k);
                                 }
 #pragma unroll
                                 for (int u = 0; u < kBatch; ++u)
@@ -1174,14 +1188,12 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                                                  word_value(w[u]), O);
                             }
                             store_out<DT>(a.out, (size_t)bh * kHeadDim + lane, lost ? __builtin_nanf("") : O / LL);
-                            // Leave the producers' slots empty for the next call.
-                            for (unsigned long long clr = prod; clr; clr &= clr - 1) {
-                                const int u = __ffsll((long long)clr) - 1;
-                                put_word(a.tag_out + (p0 + u) * kHeadDim + lane, 0ull);
-                            }
-                            if (need) {
-                                put_word(a.tag_ml + 2 * (p0 + lane), 0ull);
-                                put_word(a.tag_ml + 2 * (p0 + lane) + 1, 0ull);
+                            if (lost) {
+                                // A merge that ran out of polls empties every slot of its head.
+                                for (unsigned long long clr = prod; clr; clr &= clr - 1) {
+                                    const int u = __ffsll((long long)clr) - 1;
+                                    put_word(a.tag_out + (p0 + u) * kHeadDim + lane, 0ull);
+                                }
                             }
                         }
                     } else {
