@@ -525,40 +525,60 @@ def gemv_configs(torch, kvattn, dev, layers=12, reps=100):
 
 def qkv_append_configs(torch, kvattn, dev, layers=12, reps=100):
     """The QKV projection followed by the KV append, per layer of a 12-layer graph (B = 1,
-    NH = 12, BF16 weights and cache, maxT = 1024): two launches (kvattn_gemv then
-    kvattn_cache_write) against one (kvattn_gemv_qkv_append)."""
+    NH = 12, maxT = 1024): two launches (kvattn_gemv then kvattn_cache_write) against one
+    (kvattn_gemv_qkv_append), for BF16 weights and cache and for INT8 weights and cache (the
+    reference's USE_KV_W8 + USE_INT8 build; the one launch quantises each appended row through
+    its workspace)."""
     NH, K, maxT = 12, 768, 1024
     M = 3 * NH * HD
     g = torch.Generator(device=dev)
     g.manual_seed(11)
-    Ws = [(torch.randn(M * K, generator=g, device=dev) / K ** 0.5).to(torch.bfloat16) for _ in range(layers)]
-    caches = [torch.zeros(2 * NH * maxT * HD, device=dev, dtype=torch.bfloat16) for _ in range(layers)]
-    x = torch.randn(K, generator=g, device=dev).to(torch.bfloat16)
-    bias = torch.randn(M, generator=g, device=dev).to(torch.bfloat16)
-    qkv = torch.empty(M, device=dev, dtype=torch.bfloat16)
-    cur = torch.tensor([maxT // 2], dtype=torch.int32, device=dev)
-
-    def separate():
-        for l in range(layers):
-            kvattn.gemv(qkv, Ws[l], x, 1, M, K, w_dtype="bf16", bias=bias)
-            kvattn.kv_cache_write(caches[l], qkv, 1, NH, HD, maxT, kv_dtype="bf16", cur_len=cur)
-
-    def fused():
-        for l in range(layers):
-            kvattn.gemv_qkv_append(qkv, Ws[l], x, 1, NH, HD, K, caches[l], maxT, w_dtype="bf16", bias=bias,
-                                   cur_len=cur)
     res = {}
-    for name, step in (("gemv_then_append", separate), ("gemv_qkv_append", fused)):
-        s = torch.cuda.Stream()
-        graph = torch.cuda.CUDAGraph()
-        torch.cuda.synchronize()
-        with torch.cuda.stream(s):
-            with torch.cuda.graph(graph, stream=s):
-                step()
-        graph.replay()
-        with phase(f"qkv_{name}"):
-            us = timed(torch, graph.replay, reps) * 1000.0 / layers
-        res[name] = {"us_per_layer": round(us, 3)}
+    for dt in ("bf16", "int8"):
+        w8 = dt == "int8"
+        if w8:
+            Ws = [torch.randint(0, 126, (M * K,), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
+                  for _ in range(layers)]
+            wsc = torch.full((M,), 1e-3, device=dev)
+            caches = [torch.zeros(2 * NH * maxT * HD, device=dev, dtype=torch.uint8) for _ in range(layers)]
+            kscales = [torch.zeros(2 * NH * maxT, device=dev) for _ in range(layers)]
+            ws_bytes = kvattn.gemv_qkv_append_workspace_bytes(1, NH)
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+            kvattn.workspace_init(ws, ws_bytes)
+        else:
+            Ws = [(torch.randn(M * K, generator=g, device=dev) / K ** 0.5).to(torch.bfloat16) for _ in range(layers)]
+            wsc = None
+            caches = [torch.zeros(2 * NH * maxT * HD, device=dev, dtype=torch.bfloat16) for _ in range(layers)]
+            kscales = [None] * layers
+            ws, ws_bytes = None, 0
+        x = torch.randn(K, generator=g, device=dev).to(torch.bfloat16)
+        bias = torch.randn(M, generator=g, device=dev).to(torch.bfloat16)
+        qkv = torch.empty(M, device=dev, dtype=torch.bfloat16)
+        cur = torch.tensor([maxT // 2], dtype=torch.int32, device=dev)
+
+        def separate():
+            for l in range(layers):
+                kvattn.gemv(qkv, Ws[l], x, 1, M, K, w_dtype=dt, w_scale=wsc, bias=bias)
+                kvattn.kv_cache_write(caches[l], qkv, 1, NH, HD, maxT, kv_dtype=dt, kv_scale=kscales[l], cur_len=cur)
+
+        def fused():
+            for l in range(layers):
+                kvattn.gemv_qkv_append(qkv, Ws[l], x, 1, NH, HD, K, caches[l], maxT, w_dtype=dt, kv_dtype=dt,
+                                       w_scale=wsc, bias=bias, kv_scale=kscales[l], cur_len=cur, workspace=ws,
+                                       workspace_nbytes=ws_bytes)
+        res[dt] = {}
+        for name, step in (("gemv_then_append", separate), ("gemv_qkv_append", fused)):
+            s = torch.cuda.Stream()
+            graph = torch.cuda.CUDAGraph()
+            torch.cuda.synchronize()
+            with torch.cuda.stream(s):
+                with torch.cuda.graph(graph, stream=s):
+                    step()
+            graph.replay()
+            with phase(f"qkv_{name}" + ("_int8" if w8 else "")):
+                us = timed(torch, graph.replay, reps) * 1000.0 / layers
+            res[dt][name] = {"us_per_layer": round(us, 3)}
+        del Ws, caches, kscales, ws
     return res
 
 

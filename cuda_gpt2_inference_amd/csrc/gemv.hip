@@ -49,10 +49,17 @@ struct GemvArgs {
     int B, M, K, gelu;
     // QKV projection with the KV append in its epilogue (kv != nullptr): out is qkv
     // [B][3][NH][64], and its K and V rows also go to column cur_len of the cache
-    // [2][B][NH][maxT][64] (activation type).
+    // [2][B][NH][maxT][64], in the activation type or (kv_dtype 8-bit) as codes with a row
+    // scale in kv_scale [2][B][NH][maxT].  8-bit rows pass through `stage` (float
+    // [B][2][NH][64]) and `arrivals` (u32 [B][2][NH] at a stride of kArrivalStride words,
+    // zero between calls).
     uint8_t* kv;
     const int* cur_len;
     int lens_per_seq, NH, maxT;
+    int kv_dtype;
+    float* kv_scale;
+    float* stage;
+    unsigned* arrivals;
 };
 
 // Dot product of one 16-byte weight chunk with the x values it multiplies.
@@ -111,12 +118,25 @@ __device__ __forceinline__ float gelu_tanh(float v) {
     return 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + cube)));
 }
 
+constexpr int kHd = 64;   // head size of the QKV epilogue
+constexpr int kArrivalStride = 64;   // u32 words between two rows' arrival words (256 bytes)
+
+// Cache row (in units of kHd elements) of part 1 (K) or 2 (V), head h, sequence b at the
+// position being appended: column cur_len, clamped to [0, maxT - 1] as the append does.
+__device__ __forceinline__ size_t cache_row(const GemvArgs& a, int b, int part, int h) {
+    int cl = a.cur_len[a.lens_per_seq ? b : 0];
+    cl = cl < 0 ? 0 : (cl > a.maxT - 1 ? a.maxT - 1 : cl);
+    size_t row = ((size_t)b * a.NH + h) * a.maxT + cl;
+    if (part == 2) row += (size_t)a.B * a.NH * a.maxT;
+    return row;
+}
+
 template <int WT, int kC>
 __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(GemvArgs a) {
     using F = WFmt<WT>;
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int m = blockIdx.x * kGemvWaves + wave;
-    if (m >= a.M) return;   // whole wave; the kernel has no workgroup barrier
+    if (m >= a.M) return;   // whole wave; the one barrier (8-bit QKV epilogue) has M % kGemvWaves == 0
     const int nch = a.K * F::kWBytes / 16;
     const uint8_t* wrow = a.W + (size_t)m * a.K * F::kWBytes;
     uint4 w[kC];
@@ -143,19 +163,64 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(GemvArgs a) {
             if (a.pre_gelu) store_act<WT>(a.pre_gelu, o, pre);
             if (a.gelu) pre = gelu_tanh(pre);
             store_act<WT>(a.out, o, pre);
-            if (a.kv) {
+            if (a.kv && a.kv_dtype == (F::kActF32 ? KVATTN_KV_F32 : KVATTN_KV_BF16)) {
                 // Output m is channel c of head h of part q/k/v; K and V also land in the cache
                 // row of position cur_len, as the separate append would copy them.
-                constexpr int kHd = 64;
-                const int per_part = a.NH * kHd;
-                const int part = m / per_part;
+                const int part = m / (a.NH * kHd);
                 if (part > 0) {
-                    const int h = (m - part * per_part) / kHd, c = m - part * per_part - h * kHd;
-                    int cl = a.cur_len[a.lens_per_seq ? b : 0];
-                    cl = cl < 0 ? 0 : (cl > a.maxT - 1 ? a.maxT - 1 : cl);
-                    size_t row = ((size_t)b * a.NH + h) * a.maxT + cl;
-                    if (part == 2) row += (size_t)a.B * a.NH * a.maxT;
-                    store_act<WT>(a.kv, row * kHd + c, pre);
+                    const int h = (m - part * a.NH * kHd) / kHd, c = m - part * a.NH * kHd - h * kHd;
+                    store_act<WT>(a.kv, cache_row(a, b, part, h) * kHd + c, pre);
+                }
+            }
+        }
+        if (a.kv && (a.kv_dtype == KVATTN_KV_INT8 || a.kv_dtype == KVATTN_KV_FP8_E4M3)) {
+            // An 8-bit row's scale needs the amax of the head's 64 channels, which 16
+            // workgroups compute (4 channels each; M = 3*NH*64 is a multiple of 4, so every
+            // wave of the workgroup is here and part/h are the same for all four).  The four
+            // values (the bf16 values the qkv output holds, which the append quantises) meet
+            // in LDS; wave 0 stages them (lanes 0-3, coherent stores), waits for them, and
+            // counts the workgroup in the row's arrival word, which has a 256-byte line of its
+            // own (arrivals of one line serialise at the memory side).  The 16th to arrive
+            // reads the row back, lane c channel c, quantises it with the append's arithmetic
+            // (the same function), and re-arms the word.  s_val is double-buffered by b: a
+            // wave can refill slot b&1 only after the next barrier, which wave 0 reaches after
+            // reading it.
+            __shared__ float s_val[2][kGemvWaves];
+            const int part = m / (a.NH * kHd);
+            if (part > 0) {
+                const int h = (m - part * a.NH * kHd) / kHd;
+                if (lane == 0) s_val[b & 1][wave] = bf16_to_f32(f32_to_bf16(acc * ws + bias));
+                __syncthreads();
+                if (wave == 0) {
+                    const size_t rid = ((size_t)b * 2 + (part - 1)) * a.NH + h;
+                    const int c0 = m - part * a.NH * kHd - h * kHd;   // channel of wave 0's row
+                    if (lane < kGemvWaves)
+                        __hip_atomic_store(a.stage + rid * kHd + c0 + lane, s_val[b & 1][lane], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                    wait_vm_stores();   // the staged values have landed (the count is per wave)
+                    unsigned prev = 0;
+                    if (lane == 0)
+                        prev = __hip_atomic_fetch_add(a.arrivals + rid * kArrivalStride, 1u, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+                    prev = __shfl(prev, 0);
+                    if (prev == kHd / kGemvWaves - 1) {
+                        const float x = __hip_atomic_load(a.stage + rid * kHd + lane, __ATOMIC_RELAXED,
+                                                          __HIP_MEMORY_SCOPE_AGENT);
+                        const float amax = wave_max(fabsf(x));
+                        const size_t row = cache_row(a, b, part, h);
+                        if (a.kv_dtype == KVATTN_KV_FP8_E4M3) {
+                            const float scale = amax / kW8Limit<KVATTN_KV_FP8_E4M3>;
+                            a.kv[row * kHd + lane] = w8_code<KVATTN_KV_FP8_E4M3>(x, scale);
+                            if (lane == 0) a.kv_scale[row] = scale;
+                        } else {
+                            const float scale = amax / kW8Limit<KVATTN_KV_INT8>;
+                            a.kv[row * kHd + lane] = w8_code<KVATTN_KV_INT8>(x, scale);
+                            if (lane == 0) a.kv_scale[row] = scale;
+                        }
+                        if (lane == 0)
+                            __hip_atomic_store(a.arrivals + rid * kArrivalStride, 0u, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+                    }
                 }
             }
         }
@@ -193,7 +258,8 @@ int launch_gemv(GemvArgs a, int w_dtype, void* stream) {
     if (w8 && !a.w_scale) return KVATTN_ERR_DTYPE;
     if (((uintptr_t)a.W & 15u) || ((uintptr_t)a.x & 15u)) return KVATTN_ERR_MISALIGNED;
     if (((uintptr_t)a.out % act) || ((uintptr_t)a.pre_gelu % act) || ((uintptr_t)a.bias % act) ||
-        ((uintptr_t)a.w_scale & 3u) || ((uintptr_t)a.kv % act))
+        ((uintptr_t)a.w_scale & 3u) ||
+        (a.kv && a.kv_dtype != KVATTN_KV_INT8 && a.kv_dtype != KVATTN_KV_FP8_E4M3 && ((uintptr_t)a.kv % act)))
         return KVATTN_ERR_MISALIGNED;
     const int nch = K * wbytes / 16;
     const int per_lane = (nch + kWave - 1) / kWave;
@@ -219,16 +285,37 @@ int launch_gemv(GemvArgs a, int w_dtype, void* stream) {
 extern "C" int kvattn_gemv(void* out, void* pre_gelu, const void* W, const float* w_scale, const void* x,
                            const void* bias, int B, int M, int K, int w_dtype, int gelu, void* stream) {
     GemvArgs a{out, pre_gelu, (const uint8_t*)W, w_scale, (const uint8_t*)x, bias, B, M, K, gelu ? 1 : 0,
-               nullptr, nullptr, 0, 0, 0};
+               nullptr, nullptr, 0, 0, 0, 0, nullptr, nullptr, nullptr};
     return launch_gemv(a, w_dtype, stream);
 }
 
+extern "C" size_t kvattn_gemv_qkv_append_workspace_bytes(int B, int NH) {
+    if (B < 1 || NH < 1 || (long long)B * NH > (1ll << 24)) return 0;
+    const size_t rows = (size_t)B * 2 * NH;
+    return rows * kHd * sizeof(float) + rows * kArrivalStride * sizeof(unsigned);
+}
+
 extern "C" int kvattn_gemv_qkv_append(void* qkv, const void* W, const float* w_scale, const void* x,
-                                      const void* bias, int B, int NH, int hs, int K, void* kv_cache, int maxT,
-                                      const int* d_cur_len, int lens_per_seq, int w_dtype, void* stream) {
-    if (hs != 64) return KVATTN_ERR_HEAD_DIM;
+                                      const void* bias, int B, int NH, int hs, int K, void* kv_cache,
+                                      float* kv_scale, int maxT, const int* d_cur_len, int lens_per_seq,
+                                      int w_dtype, int kv_dtype, void* workspace, size_t workspace_bytes,
+                                      void* stream) {
+    if (hs != kHd) return KVATTN_ERR_HEAD_DIM;
     if (B < 1 || NH < 1 || maxT < 1 || (long long)B * NH > (1ll << 24) || maxT > (1 << 23)) return KVATTN_ERR_SHAPE;
     if (!kv_cache) return KVATTN_ERR_NULL_POINTER;
+    const bool kv8 = kv_dtype == KVATTN_KV_INT8 || kv_dtype == KVATTN_KV_FP8_E4M3;
+    const int act = w_dtype == KVATTN_KV_F32 ? KVATTN_KV_F32 : KVATTN_KV_BF16;
+    if (!kv8 && kv_dtype != act) return KVATTN_ERR_DTYPE;          // the cache holds the activation type
+    if (kv8 && (w_dtype == KVATTN_KV_F32 || !kv_scale)) return KVATTN_ERR_DTYPE;
+    float* stage = nullptr;
+    unsigned* arrivals = nullptr;
+    if (kv8) {
+        const size_t need = kvattn_gemv_qkv_append_workspace_bytes(B, NH);
+        if (!workspace || workspace_bytes < need) return KVATTN_ERR_WORKSPACE;
+        if (((uintptr_t)workspace & 255u) || ((uintptr_t)kv_scale & 3u)) return KVATTN_ERR_MISALIGNED;
+        stage = (float*)workspace;
+        arrivals = (unsigned*)((uint8_t*)workspace + (size_t)B * 2 * NH * kHd * sizeof(float));
+    }
     if (!d_cur_len) {
         int* sym = nullptr;
         const int st = kvattn_cur_len_symbol(&sym);
@@ -236,6 +323,6 @@ extern "C" int kvattn_gemv_qkv_append(void* qkv, const void* W, const float* w_s
         d_cur_len = sym;
     }
     GemvArgs a{qkv, nullptr, (const uint8_t*)W, w_scale, (const uint8_t*)x, bias, B, 3 * NH * hs, K, 0,
-               (uint8_t*)kv_cache, d_cur_len, lens_per_seq ? 1 : 0, NH, maxT};
+               (uint8_t*)kv_cache, d_cur_len, lens_per_seq ? 1 : 0, NH, maxT, kv_dtype, kv_scale, stage, arrivals};
     return launch_gemv(a, w_dtype, stream);
 }

@@ -101,43 +101,6 @@ template <int DT> constexpr int kUnroll = Row<DT>::k8bit ? KVATTN_UNROLL_BYTE : 
 template <int DT> constexpr int kUnrollLat = KVATTN_LAT_ROWS / kRowsPerLoad<DT> > 0 ? KVATTN_LAT_ROWS / kRowsPerLoad<DT> : 1;
 constexpr int kWavesLat = KVATTN_LAT_WAVES;
 
-// OCP E4M3 ("FN": max 448, no infinities) encode of y, round to nearest even, finite
-// overflow saturates to +-448 (the reference's __NV_SATFINITE request).
-__device__ __forceinline__ uint8_t f32_to_e4m3_sat(float y) {
-    if (y != y) return 0x7F;
-    const uint32_t sign = (__float_as_uint(y) >> 24) & 0x80u;
-    const float a = fabsf(y);
-    if (a >= 448.0f) return (uint8_t)(sign | 0x7Eu);
-    if (a < 0.015625f) {                       // subnormal grid m * 2^-9; 8 -> 2^-6
-        return (uint8_t)(sign | (uint32_t)rintf(a * 512.0f));
-    }
-    const uint32_t u = __float_as_uint(a);
-    uint32_t keep = u >> 20;                   // exponent | top 3 mantissa bits
-    const uint32_t rem = u & 0xFFFFFu;
-    keep += (rem > 0x80000u || (rem == 0x80000u && (keep & 1u))) ? 1u : 0u;
-    uint32_t code = keep - (120u << 3);        // rebias 127 -> 7
-    code = code > 0x7Eu ? 0x7Eu : code;
-    return (uint8_t)(sign | code);
-}
-
-// 8-bit row quantisation of the append: scale = amax / limit (IEEE division), code of
-// x / scale (INT8: round half to even, clamp to +-127; FP8: saturating E4M3), and zero
-// codes when the scale is not positive (an all-zero row).
-template <int DT> constexpr float kW8Limit = DT == KVATTN_KV_FP8_E4M3 ? 448.0f : 127.0f;
-
-template <int DT>
-__device__ __forceinline__ uint8_t w8_code(float x, float scale) {
-    if (!(scale > 0.0f)) return 0;
-    const float y = x / scale;
-    if constexpr (DT == KVATTN_KV_FP8_E4M3) {
-        return f32_to_e4m3_sat(y);
-    } else {
-        int qv = (int)rintf(y);
-        qv = qv < -127 ? -127 : (qv > 127 ? 127 : qv);
-        return (uint8_t)(int8_t)qv;
-    }
-}
-
 // Decode one lane's 16-byte chunk of a row into kElems floats.
 template <int DT>
 __device__ __forceinline__ void decode(const uint4& d, float (&x)[Row<DT>::kElems]) {
@@ -869,20 +832,6 @@ __device__ __forceinline__ bool locate(const SplitArgs& a, int x, Item& it) {
     return false;
 }
 
-// Tagged partial words of the designated merger (agent-scope relaxed atomics, emitted as
-// coherent sc1 stores and loads on gfx950).
-constexpr unsigned long long kWordValid = 1ull << 32;
-constexpr int kMergePolls = 1 << 22;  // bound on the designated merger's polls (seconds)
-__device__ __forceinline__ void put_word(unsigned long long* p, unsigned long long w) {
-    __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ unsigned long long get_word(const unsigned long long* p) {
-    return __hip_atomic_load(const_cast<unsigned long long*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ unsigned long long valid_word(float v) { return kWordValid | __float_as_uint(v); }
-__device__ __forceinline__ bool word_valid(unsigned long long w) { return (w >> 32) == 1u; }
-__device__ __forceinline__ float word_value(unsigned long long w) { return __uint_as_float((uint32_t)w); }
-
 // Partials of the in-kernel merge travel between workgroups that may sit on different
 // XCDs (each with its own L2).  They are written and read as agent-scope relaxed atomics,
 // which the gfx950 code generator emits as write-through / coherent stores and loads
@@ -899,13 +848,21 @@ __device__ __forceinline__ float get(const float* p) {
     if constexpr (kCoherent) return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     else return *p;
 }
-// s_waitcnt vmcnt(0) (GFX9 encoding: expcnt and lgkmcnt fields left at their maximum),
-// fenced against compiler reordering on both sides.
-__device__ __forceinline__ void wait_vm_stores() {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0x0F70);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+
+// Tagged partial words of the designated merger (agent-scope relaxed atomics, emitted as
+// coherent sc1 stores and loads on gfx950).
+constexpr unsigned long long kWordValid = 1ull << 32;
+constexpr int kMergePolls = 1 << 22;  // bound on the designated merger's polls (seconds)
+__device__ __forceinline__ void put_word(unsigned long long* p, unsigned long long w) {
+    __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ unsigned long long get_word(const unsigned long long* p) {
+    return __hip_atomic_load(const_cast<unsigned long long*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long valid_word(float v) { return kWordValid | __float_as_uint(v); }
+__device__ __forceinline__ bool word_valid(unsigned long long w) { return (w >> 32) == 1u; }
+__device__ __forceinline__ float word_value(unsigned long long w) { return __uint_as_float((uint32_t)w); }
+
 
 // Merge the n_seg partials of (b,h) = bh into out; executed by one full wave, lane c
 // producing channel c.  Lane s holds the max and exp-sum of segment s (64 segments per

@@ -1,8 +1,11 @@
 // lanes.hpp -- wave64 building blocks shared by the gfx950 kernels of this library:
-// bfloat16 and 8-bit code conversion, 16-byte lane loads and DPP / permlane reductions.
+// bfloat16 and 8-bit code conversion, the append's 8-bit row quantiser, 16-byte lane loads
+// and DPP / permlane reductions.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "kvattn.h"
 
 namespace {
 
@@ -130,5 +133,51 @@ __device__ __forceinline__ float wave_sum(float x) {
 }
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+
+// OCP E4M3 ("FN": max 448, no infinities) encode of y, round to nearest even, finite
+// overflow saturates to +-448 (the reference's __NV_SATFINITE request).
+__device__ __forceinline__ uint8_t f32_to_e4m3_sat(float y) {
+    if (y != y) return 0x7F;
+    const uint32_t sign = (__float_as_uint(y) >> 24) & 0x80u;
+    const float a = fabsf(y);
+    if (a >= 448.0f) return (uint8_t)(sign | 0x7Eu);
+    if (a < 0.015625f) {                       // subnormal grid m * 2^-9; 8 -> 2^-6
+        return (uint8_t)(sign | (uint32_t)rintf(a * 512.0f));
+    }
+    const uint32_t u = __float_as_uint(a);
+    uint32_t keep = u >> 20;                   // exponent | top 3 mantissa bits
+    const uint32_t rem = u & 0xFFFFFu;
+    keep += (rem > 0x80000u || (rem == 0x80000u && (keep & 1u))) ? 1u : 0u;
+    uint32_t code = keep - (120u << 3);        // rebias 127 -> 7
+    code = code > 0x7Eu ? 0x7Eu : code;
+    return (uint8_t)(sign | code);
+}
+
+// 8-bit row quantisation of the append: scale = amax / limit (IEEE division), code of
+// x / scale (INT8: round half to even, clamp to +-127; FP8: saturating E4M3), and zero
+// codes when the scale is not positive (an all-zero row).
+template <int DT> constexpr float kW8Limit = DT == KVATTN_KV_FP8_E4M3 ? 448.0f : 127.0f;
+
+template <int DT>
+__device__ __forceinline__ uint8_t w8_code(float x, float scale) {
+    if (!(scale > 0.0f)) return 0;
+    const float y = x / scale;
+    if constexpr (DT == KVATTN_KV_FP8_E4M3) {
+        return f32_to_e4m3_sat(y);
+    } else {
+        int qv = (int)rintf(y);
+        qv = qv < -127 ? -127 : (qv > 127 ? 127 : qv);
+        return (uint8_t)(int8_t)qv;
+    }
+}
+
+// s_waitcnt vmcnt(0) (GFX9 encoding: expcnt and lgkmcnt fields left at their maximum),
+// fenced against compiler reordering on both sides.
+__device__ __forceinline__ void wait_vm_stores() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
 
 }  // namespace

@@ -89,7 +89,9 @@ SIGNATURES = {
     "kvattn_decode": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp, _sz, _i, _i, _i, _vp]),
     "kvattn_append_decode": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp, _sz, _i, _i, _i, _vp]),
     "kvattn_gemv": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
-    "kvattn_gemv_qkv_append": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _vp, _i, _i, _vp]),
+    "kvattn_gemv_qkv_append": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _i, _vp, _i, _i, _i, _vp,
+                                    _sz, _vp]),
+    "kvattn_gemv_qkv_append_workspace_bytes": (_sz, [_i, _i]),
     "kvattn_paged_cache_write": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _i, _i, _i, _vp, _i, _i, _vp]),
     "kvattn_paged_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _i, _i, _vp, _sz, _i, _i,
                                  _i, _i, _vp]),
@@ -268,12 +270,24 @@ def gemv(out, W, x, B, M, K, *, w_dtype, w_scale=None, bias=None, pre_gelu=None,
                              kv_dtype_code(w_dtype), int(bool(gelu)), _stream(stream)), "kvattn_gemv")
 
 
-def gemv_qkv_append(qkv, W, x, B, NH, hs, K, kv_cache, maxT, *, w_dtype, w_scale=None, bias=None, cur_len=None,
-                    lens_per_seq=False, stream=None) -> None:
-    """QKV projection with the KV append in its epilogue (kvattn_gemv_qkv_append)."""
+def gemv_qkv_append(qkv, W, x, B, NH, hs, K, kv_cache, maxT, *, w_dtype, kv_dtype=None, w_scale=None, bias=None,
+                    kv_scale=None, cur_len=None, lens_per_seq=False, workspace=None, workspace_nbytes=0,
+                    stream=None) -> None:
+    """QKV projection with the KV append in its epilogue (kvattn_gemv_qkv_append).  kv_dtype
+    defaults to the activation type (f32 for f32 weights, else bf16); 8-bit caches need
+    kv_scale and a workspace of gemv_qkv_append_workspace_bytes(B, NH), zeroed once."""
+    if kv_dtype is None:
+        kv_dtype = "f32" if kv_dtype_code(w_dtype) == KV_F32 else "bf16"
     _check(lib().kvattn_gemv_qkv_append(_ptr(qkv), _ptr(W), _ptr(w_scale), _ptr(x), _ptr(bias), B, NH, hs, K,
-                                        _ptr(kv_cache), maxT, _ptr(cur_len), int(bool(lens_per_seq)),
-                                        kv_dtype_code(w_dtype), _stream(stream)), "kvattn_gemv_qkv_append")
+                                        _ptr(kv_cache), _ptr(kv_scale), maxT, _ptr(cur_len),
+                                        int(bool(lens_per_seq)), kv_dtype_code(w_dtype), kv_dtype_code(kv_dtype),
+                                        _ptr(workspace), int(workspace_nbytes), _stream(stream)),
+           "kvattn_gemv_qkv_append")
+
+
+def gemv_qkv_append_workspace_bytes(B: int, NH: int) -> int:
+    """Workspace bytes gemv_qkv_append needs for an 8-bit cache."""
+    return int(lib().kvattn_gemv_qkv_append_workspace_bytes(B, NH))
 
 
 class PagedCache:

@@ -255,15 +255,26 @@ int kvattn_gemv(void* out, void* pre_gelu, const void* W, const float* w_scale, 
 
 /* The QKV projection with the KV append in its epilogue: kvattn_gemv with M = 3 * NH * hs
  * (no GELU) into qkv [B][3][NH][hs], whose K and V rows also go to column cur_len of
- * kv_cache [2][B][NH][maxT][hs] (the value kvattn_cache_write would copy, bit for bit).
- * The cache holds the activation type: float for F32 weights, bf16 otherwise (8-bit caches,
- * whose row scale needs the whole head row, are not covered: take kvattn_append_decode).
+ * kv_cache [2][B][NH][maxT][hs], as kvattn_cache_write would write them, bit for bit.
+ *   kv_dtype F32 / BF16: the cache holds the activation type (float for F32 weights, bf16
+ *     otherwise); kv_scale and the workspace are not used.
+ *   kv_dtype INT8 / FP8_E4M3 (bf16 activations): codes and one row scale per (b, K|V, h) in
+ *     kv_scale [2][B][NH][maxT], from the bf16 values in qkv with the append's quantiser.
+ *     The 64 channels of a row come from 16 workgroups, so they meet in the workspace:
+ *     kvattn_gemv_qkv_append_workspace_bytes(B, NH) bytes, 256-byte aligned, zeroed once
+ *     (kvattn_workspace_init); every call re-arms its arrival counters, so the workspace
+ *     needs no clearing between calls.  Calls sharing a workspace must be ordered (one
+ *     stream).
  * d_cur_len as in kvattn_decode (NULL: the library's device length).  hs must be 64.
- * Replaces the QKV GEMV followed by the append launch (inference_gpt2_opt.cu:290-303; the
- * append kernel attention_kvcache.cuh:46-64), one launch fewer per layer. */
+ * Replaces the QKV GEMV followed by the append launch (inference_gpt2_opt.cu:290-303, 329;
+ * the append kernels attention_kvcache.cuh:46-64, attention_kvcache_w8.cuh:115-155), one
+ * launch fewer per layer. */
+size_t kvattn_gemv_qkv_append_workspace_bytes(int B, int NH);
 int kvattn_gemv_qkv_append(void* qkv, const void* W, const float* w_scale, const void* x,
-                           const void* bias, int B, int NH, int hs, int K, void* kv_cache, int maxT,
-                           const int* d_cur_len, int lens_per_seq, int w_dtype, void* stream);
+                           const void* bias, int B, int NH, int hs, int K, void* kv_cache,
+                           float* kv_scale, int maxT, const int* d_cur_len, int lens_per_seq,
+                           int w_dtype, int kv_dtype, void* workspace, size_t workspace_bytes,
+                           void* stream);
 
 #ifdef __cplusplus
 }

@@ -133,17 +133,32 @@ def test_gemv_argument_errors(kw, status):
     (dict(kv=None), 1),                 # KVATTN_ERR_NULL_POINTER
     (dict(W=None), 1),
     (dict(w_dtype=7), 5),               # KVATTN_ERR_DTYPE
-    (dict(kv=ALIGNED + 1), 2),          # KVATTN_ERR_MISALIGNED (bf16 cache)
-    (dict(qkv=ALIGNED + 2, w_dtype=0), 2),
+    (dict(kv_dtype=0), 5),              # an FP32 cache behind bf16 activations
+    (dict(kv_dtype=2, kv_scale=None), 5),   # 8-bit cache without row scales
+    (dict(kv_dtype=3, w_dtype=0), 5),   # 8-bit cache behind FP32 activations
+    (dict(kv_dtype=2, ws=None), 7),     # KVATTN_ERR_WORKSPACE
+    (dict(kv_dtype=2, ws_bytes=64), 7),
+    (dict(kv_dtype=2, ws=ALIGNED + 16), 2),  # KVATTN_ERR_MISALIGNED (workspace below 256 B)
+    (dict(kv=ALIGNED + 1), 2),          # bf16 cache
+    (dict(qkv=ALIGNED + 2, w_dtype=0, kv_dtype=0), 2),
 ])
 def test_gemv_qkv_append_argument_errors(kw, status):
     """kvattn_gemv_qkv_append's checks, made before any HIP call (a device length is given,
     so the library's own length symbol is not looked up)."""
     from cuda_gpt2_inference_amd import kvattn
     a = dict(qkv=ALIGNED, W=ALIGNED, w_scale=ALIGNED, x=ALIGNED, bias=None, B=1, NH=12, hs=64, K=768, kv=ALIGNED,
-             maxT=1024, cur=ALIGNED, lens=0, w_dtype=1)
+             kv_scale=ALIGNED, maxT=1024, cur=ALIGNED, lens=0, w_dtype=1, kv_dtype=1, ws=ALIGNED, ws_bytes=1 << 20)
     a.update(kw)
     st = kvattn.lib().kvattn_gemv_qkv_append(a["qkv"], a["W"], a["w_scale"], a["x"], a["bias"], a["B"], a["NH"],
-                                             a["hs"], a["K"], a["kv"], a["maxT"], a["cur"], a["lens"],
-                                             a["w_dtype"], None)
+                                             a["hs"], a["K"], a["kv"], a["kv_scale"], a["maxT"], a["cur"], a["lens"],
+                                             a["w_dtype"], a["kv_dtype"], a["ws"], a["ws_bytes"], None)
     assert st == status, kvattn.strerror(st)
+
+
+def test_gemv_qkv_append_workspace_bytes():
+    """One float per channel of the 2*B*NH staged rows plus one arrival word per row on a
+    256-byte line of its own; 0 for shapes out of range."""
+    from cuda_gpt2_inference_amd import kvattn
+    for B, NH in ((1, 12), (3, 12), (64, 16), (1, 1)):
+        assert kvattn.gemv_qkv_append_workspace_bytes(B, NH) == 2 * B * NH * (64 * 4 + 256)
+    assert kvattn.gemv_qkv_append_workspace_bytes(0, 12) == 0

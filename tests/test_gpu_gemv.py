@@ -112,13 +112,16 @@ def test_gemv_ragged_shapes(dev, dtype, M, K):
     _check(got, ref, dtype, 2, M, f"M={M} K={K} {dtype}")
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16", "int8"])
+@pytest.mark.parametrize("dtype,kv", [("f32", "f32"), ("bf16", "bf16"), ("int8", "bf16"), ("bf16", "int8"),
+                                      ("bf16", "fp8"), ("int8", "int8"), ("fp8", "fp8")])
 @pytest.mark.parametrize("lens", ["uniform", "ragged", "library"])
-def test_gemv_qkv_append_equals_gemv_then_append(dev, dtype, lens):
+def test_gemv_qkv_append_equals_gemv_then_append(dev, dtype, kv, lens):
     """kvattn_gemv_qkv_append against kvattn_gemv + kvattn_cache_write on copies of the same
     cache: identical qkv bytes and identical cache bytes (the appended K and V rows and every
-    other row), at GPT-2's QKV shape (NH = 12: 2304 x 768), with one device length, per-
-    sequence lengths (one of them beyond maxT, clamped), and the library's own length."""
+    other row; for 8-bit caches the codes and the row scales), at GPT-2's QKV shape (NH = 12:
+    2304 x 768), with one device length, per-sequence lengths (one of them beyond maxT,
+    clamped), and the library's own length.  8-bit caches run two calls in a row on one
+    workspace, so the second finds the arrival words re-armed by the first."""
     import torch
     kvattn = _kv()
     NH, HS, K, maxT = 12, 64, 768, 96
@@ -129,9 +132,18 @@ def test_gemv_qkv_append_equals_gemv_then_append(dev, dtype, lens):
     bias = None if d["bias"] is None else d["bias"].to(dev)
     scale = None if d.get("scale") is None else d["scale"].to(dev)
     act = torch.float32 if dtype == "f32" else torch.bfloat16
+    w8 = kv in ("int8", "fp8")
     g = torch.Generator(device=dev)
     g.manual_seed(71)
-    cache = torch.randn(2 * B * NH * maxT * HS, generator=g, device=dev).to(act)
+    if w8:
+        cache = torch.randint(0, 256, (2 * B * NH * maxT * HS,), generator=g, device=dev, dtype=torch.uint8)
+        kscale = torch.rand(2 * B * NH * maxT, generator=g, device=dev)
+        ws_bytes = kvattn.gemv_qkv_append_workspace_bytes(B, NH)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        kvattn.workspace_init(ws, ws_bytes)
+    else:
+        cache = torch.randn(2 * B * NH * maxT * HS, generator=g, device=dev).to(act)
+        kscale, ws, ws_bytes = None, None, 0
     if lens == "uniform":
         cur, per_seq = torch.tensor([40], dtype=torch.int32, device=dev), False
     elif lens == "ragged":
@@ -139,16 +151,30 @@ def test_gemv_qkv_append_equals_gemv_then_append(dev, dtype, lens):
     else:
         kvattn.set_cur_len(17)
         cur, per_seq = None, False
-    c_a, c_b = cache.clone(), cache.clone()
-    q_a = torch.empty(B * M, dtype=act, device=dev)
-    q_b = torch.empty_like(q_a)
-    kvattn.gemv(q_a, W, x, B, M, K, w_dtype=dtype, w_scale=scale, bias=bias)
-    kvattn.kv_cache_write(c_a, q_a, B, NH, HS, maxT, kv_dtype="f32" if dtype == "f32" else "bf16", cur_len=cur,
-                          lens_per_seq=per_seq)
-    kvattn.gemv_qkv_append(q_b, W, x, B, NH, HS, K, c_b, maxT, w_dtype=dtype, w_scale=scale, bias=bias,
-                           cur_len=cur, lens_per_seq=per_seq)
-    torch.cuda.synchronize()
     iview = torch.int32 if dtype == "f32" else torch.int16
-    assert torch.equal(q_a.view(iview), q_b.view(iview)), f"{dtype} {lens}: qkv"
-    assert torch.equal(c_a.view(iview), c_b.view(iview)), f"{dtype} {lens}: cache"
-    assert not torch.equal(c_a.view(iview), cache.view(iview)), f"{dtype} {lens}: nothing appended"
+    cview = torch.uint8 if w8 else iview
+    c_a, c_b = cache.clone(), cache.clone()
+    s_a = None if kscale is None else kscale.clone()
+    s_b = None if kscale is None else kscale.clone()
+    for call in range(2 if w8 else 1):
+        xc = x if call == 0 else (x * -0.75).contiguous()
+        q_a = torch.empty(B * M, dtype=act, device=dev)
+        q_b = torch.empty_like(q_a)
+        kvattn.gemv(q_a, W, xc, B, M, K, w_dtype=dtype, w_scale=scale, bias=bias)
+        kvattn.kv_cache_write(c_a, q_a, B, NH, HS, maxT, kv_dtype=kv, kv_scale=s_a, cur_len=cur,
+                              lens_per_seq=per_seq)
+        kvattn.gemv_qkv_append(q_b, W, xc, B, NH, HS, K, c_b, maxT, w_dtype=dtype, kv_dtype=kv, w_scale=scale,
+                               bias=bias, kv_scale=s_b, cur_len=cur, lens_per_seq=per_seq, workspace=ws,
+                               workspace_nbytes=ws_bytes)
+        torch.cuda.synchronize()
+        tag = f"{dtype} weights, {kv} cache, {lens}, call {call}"
+        assert torch.equal(q_a.view(iview), q_b.view(iview)), f"{tag}: qkv"
+        assert torch.equal(c_a.view(cview), c_b.view(cview)), f"{tag}: cache"
+        if w8:
+            assert torch.equal(s_a.view(torch.int32), s_b.view(torch.int32)), f"{tag}: row scales"
+        assert not torch.equal(c_a.view(cview), cache.view(cview)), f"{tag}: nothing appended"
+    if w8:
+        # The arrival words (after the staged rows, one per 256 bytes) are back at zero.
+        off = 2 * B * NH * HS * 4
+        arrivals = ws[off:off + 2 * B * NH * 256].view(torch.int32)
+        assert int(arrivals.abs().sum()) == 0, f"{dtype} {kv} {lens}: arrival words left armed"
