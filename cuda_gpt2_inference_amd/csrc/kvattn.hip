@@ -1989,6 +1989,11 @@ int kvattn_cache_write(void* kv_cache, float* kv_scale, const void* qkv, int B, 
                               (hipStream_t)stream_v);
 }
 
+int kvattn_append(void* kv_cache, float* kv_scale, const void* qkv, int B, int NH, int hs, int maxT,
+                  const int* d_cur_len, int kv_dtype, void* stream) {
+    return kvattn_cache_write(kv_cache, kv_scale, qkv, B, NH, hs, maxT, d_cur_len, 0, kv_dtype, stream);
+}
+
 int kvattn_paged_cache_write(void* pages, float* page_scales, const int* block_table, int max_pages,
                              int page_rows, int num_pages, const void* qkv, int B, int NH, int hs,
                              const int* d_cur_len, int lens_per_seq, int kv_dtype, void* stream) {

@@ -78,6 +78,7 @@ SIGNATURES = {
     "kvattn_set_cur_len": (_i, [_i]),
     "kvattn_set_cur_len_async": (_i, [_vp, _i, _vp]),
     "kvattn_cache_write": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp]),
+    "kvattn_append": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _vp]),
     "kvattn_forward_small": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp]),
     "kvattn_forward_large": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _vp, _vp, _vp, _i, _i, _vp]),
     "kvattn_split": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _i, _i, _vp]),

@@ -110,6 +110,13 @@ int kvattn_cache_write(void* kv_cache, float* kv_scale, const void* qkv,
                        const int* d_cur_len, int lens_per_seq,
                        int kv_dtype, void* stream);
 
+/* kvattn_cache_write with one length for the whole batch (lens_per_seq = 0): the append
+ * with exactly the arguments of the reference's launch (kv_cache_write_kernel[_w8] at
+ * inference_gpt2_opt.cu:302-303, 329), plus the dtype and the stream. */
+int kvattn_append(void* kv_cache, float* kv_scale, const void* qkv,
+                  int B, int NH, int hs, int maxT, const int* d_cur_len,
+                  int kv_dtype, void* stream);
+
 /* Short-context path: one workgroup per (b,h), scores staged in LDS.
  * Replaces attention_forward_kv_small (Inference_gpt2/attention_kvcache.cuh:453-459) and
  * attention_forward_kv_small_w8 (Inference_gpt2/attention_kvcache_w8.cuh:529-536). */

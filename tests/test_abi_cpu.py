@@ -97,6 +97,9 @@ def test_other_entry_point_errors():
     L = kvattn.lib()
     assert L.kvattn_cache_write(ALIGNED, None, ALIGNED, 1, 12, 48, 1024, None, 0, 1, None) == kvattn.ERR_HEAD_DIM
     assert L.kvattn_cache_write(ALIGNED, None, ALIGNED, 1, 12, 64, 1024, None, 0, 3, None) == kvattn.ERR_DTYPE
+    assert L.kvattn_append(ALIGNED, None, ALIGNED, 1, 12, 48, 1024, None, 1, None) == kvattn.ERR_HEAD_DIM
+    assert L.kvattn_append(ALIGNED, None, ALIGNED, 1, 12, 64, 1024, None, 3, None) == kvattn.ERR_DTYPE
+    assert L.kvattn_append(None, None, ALIGNED, 1, 12, 64, 1024, None, 1, None) == kvattn.ERR_NULL_POINTER
     assert L.kvattn_forward_small(None, ALIGNED, ALIGNED, None, 1, 12, 64, 1024, None, 0, 1, None) == \
         kvattn.ERR_NULL_POINTER
     assert L.kvattn_forward_large(ALIGNED, ALIGNED, ALIGNED, None, 1, 12, 64, 1024, None, 0, ALIGNED, ALIGNED,

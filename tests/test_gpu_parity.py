@@ -51,6 +51,52 @@ def test_append_copy_bitexact(dev, dtype):
     assert np.array_equal(got.view(np.uint8), ref.view(np.uint8))
 
 
+@pytest.mark.parametrize("dtype", ALL_DT)
+def test_append_entry_point_one_length(dev, dtype):
+    """kvattn_append (the append with the reference launch's arguments: one length for the
+    batch) called through the C ABI: cache bytes, and 8-bit codes and scales, bit-exact
+    against the oracle's append at that length."""
+    import torch
+    kvattn = _kv()
+    B, NH, maxT, L = 2, 3, 48, 29
+    qkv_bits = oracle.bf16_round(oracle.gen_normal(31, B * 3 * NH * HS).astype(np.float32))
+    src = oracle.bf16_decode(qkv_bits).reshape(-1)
+    if dtype == "f32":
+        qkv = torch.from_numpy(src.copy()).to(dev)
+    else:
+        qkv = torch.from_numpy(qkv_bits.reshape(-1).view(np.int16)).to(dev).view(torch.bfloat16)
+    cur = torch.tensor([L], dtype=torch.int32, device=dev)
+    n = 2 * B * NH * maxT * HS
+    if dtype in ("int8", "fp8"):
+        cache = torch.zeros(n, dtype=torch.uint8, device=dev)
+        scale = torch.full((2 * B * NH * maxT,), -1.0, dtype=torch.float32, device=dev)
+    else:
+        cache = torch.zeros(n, dtype=torch.float32 if dtype == "f32" else torch.bfloat16, device=dev)
+        scale = None
+    st = kvattn.lib().kvattn_append(cache.data_ptr(), None if scale is None else scale.data_ptr(), qkv.data_ptr(),
+                                    B, NH, HS, maxT, cur.data_ptr(), kvattn.kv_dtype_code(dtype),
+                                    torch.cuda.current_stream().cuda_stream)
+    assert st == 0, kvattn.strerror(st)
+    torch.cuda.synchronize()
+    if dtype in ("int8", "fp8"):
+        fmt = oracle.W8_INT8 if dtype == "int8" else oracle.W8_FP8_E4M3
+        ref_codes = np.zeros(n, dtype=np.uint8)
+        ref_scales = np.full(2 * B * NH * maxT, -1.0, dtype=np.float32)
+        oracle.cache_write_w8(ref_codes, ref_scales, src, [L] * B, B, NH, HS, maxT, fmt)
+        assert np.array_equal(cache.cpu().numpy(), ref_codes)
+        assert np.array_equal(scale.cpu().numpy().view(np.uint32), ref_scales.view(np.uint32))
+    else:
+        if dtype == "f32":
+            ref = np.zeros(n, dtype=np.float32)
+            oracle.cache_write(ref, src, [L] * B, B, NH, HS, maxT)
+            got = cache.cpu().numpy()
+        else:
+            ref = np.zeros(n, dtype=np.uint16)
+            oracle.cache_write(ref, qkv_bits.reshape(-1), [L] * B, B, NH, HS, maxT)
+            got = cache.view(torch.int16).cpu().numpy().view(np.uint16)
+        assert np.array_equal(got.view(np.uint8), ref.view(np.uint8))
+
+
 @pytest.mark.parametrize("dtype", ["int8", "fp8"])
 def test_append_w8_codes_bitexact(dev, dtype):
     """Fill a whole 8-bit cache by one append per position; codes and scales bit-exact.
