@@ -1654,6 +1654,10 @@ int launch_graph_pair(const SplitArgs& a, int kv_dtype, bool lat, hipStream_t st
 //   part_max, part_lse [B*NH*S] f32, part_out [B*NH*S*64] f32   reference-format partials
 //   tag_ml [B*NH*S*2] u64, tag_out [B*NH*S*64] u64   designated merger
 // kvattn_workspace_init zeroes it once; every kernel leaves the counters and tags at 0.
+// The counters and partials are laid out from the front of the buffer and the tags from
+// its end, so that calls planned with different slot counts S on one buffer never put a
+// tag word where another call left a partial: a float pair read as a tagged word would
+// pass for a published partial.
 struct Workspace {
     unsigned* counters;
     float* part_max;
@@ -1664,7 +1668,8 @@ struct Workspace {
     size_t bytes;
 };
 
-Workspace carve(void* base, int B, int NH, int S) {
+// avail: the caller's buffer size (0: the size query, the buffer exactly as large).
+Workspace carve(void* base, int B, int NH, int S, size_t avail = 0) {
     const size_t bh = (size_t)B * NH;
     const size_t nc = align_up(bh * sizeof(unsigned), 256);
     const size_t nm = align_up(bh * S * sizeof(float), 256);
@@ -1677,9 +1682,10 @@ Workspace carve(void* base, int B, int NH, int S) {
     w.part_max = (float*)(p + nc);
     w.part_lse = (float*)(p + nc + nm);
     w.part_out = (float*)(p + nc + 2 * nm);
-    w.tag_ml = (unsigned long long*)(p + nc + 2 * nm + no);
-    w.tag_out = (unsigned long long*)(p + nc + 2 * nm + no + ntm);
     w.bytes = nc + 2 * nm + no + ntm + nto;
+    const size_t end = avail >= w.bytes ? avail / 256 * 256 : w.bytes;   // w.bytes is a multiple of 256
+    w.tag_out = (unsigned long long*)(p + end - nto);
+    w.tag_ml = (unsigned long long*)(p + end - nto - ntm);
     return w;
 }
 
@@ -1816,7 +1822,7 @@ int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scal
 
     if (!workspace) return KVATTN_ERR_WORKSPACE;
     if (!aligned16(workspace)) return KVATTN_ERR_MISALIGNED;
-    const Workspace w = carve(workspace, B, NH, plan.slots);
+    const Workspace w = carve(workspace, B, NH, plan.slots, workspace_bytes);
     if (w.bytes > workspace_bytes) return KVATTN_ERR_WORKSPACE;
     KV_TRY(resolve_len(d_cur_len));
 

@@ -342,6 +342,85 @@ def test_c5_ragged_64_sequences(dev):
         assert float(d.max()) <= 1e-2, f"C5 {name} disagrees with split_merge ({float(d.max()):.3e})"
 
 
+@pytest.mark.parametrize("dtype", ALL_DT)
+def test_streaming_ragged_every_dtype(dev, dtype):
+    """AUTO on a ragged batch that streams (64 x 2 heads x maxT = 4096, 2^19 rows): the
+    half-grid split kernel with device-planned segments, then the merge kernel, in each
+    cache type.  Every (b,h) against the oracle, for three calls on one workspace with the
+    lengths changed between them.  Lengths include one-segment heads, exact multiples of
+    the planned segment rows and maxT.  The fused append on the same path is bit-identical
+    to append + attention."""
+    import torch
+    kvattn = _kv()
+    B, NH, maxT = 64, 2, 4096
+    assert kvattn.plan(B, NH, HS, maxT, kv_dtype=dtype)[:2] == (kvattn.STRATEGIES["split_merge"], 8)
+    rng = np.random.RandomState(17)
+    lens_a = rng.randint(1, maxT + 1, B).astype(np.int32)
+    lens_a[:8] = [1, 2, 256, 257, 512, 1024, 2048, maxT]
+    lens_b = rng.randint(1, maxT + 1, B).astype(np.int32)
+    lens_b[-4:] = [maxT, 1, 4095, 300]
+    case = make_case(dtype, B, NH, maxT, lens_a - 1, seed=400 + len(dtype))
+    qkv, cache, scale, cur = to_device(case, dev)
+    ws = kvattn.Workspace(B, NH, maxT, 0)
+    for call, lens in enumerate((lens_a, lens_b, lens_a[::-1].copy())):
+        case.cur_lens[:] = lens - 1
+        cur.copy_(torch.from_numpy(case.cur_lens.copy()))
+        out = out_tensor(case, dev)
+        kvattn.decode(out, qkv, cache, B, NH, HS, maxT, kv_dtype=dtype, kv_scale=scale, cur_len=cur,
+                      lens_per_seq=True, **ws.kwargs())
+        torch.cuda.synchronize()
+        assert_close(out.float().cpu().numpy(), case.reference(), dtype, f"streaming {dtype} call {call}")
+    # The fused append through the same launch.
+    c_a, c_b = cache.clone(), cache.clone()
+    s_a = None if scale is None else scale.clone()
+    s_b = None if scale is None else scale.clone()
+    o_a, o_b = out_tensor(case, dev), out_tensor(case, dev)
+    kw = dict(kv_dtype=dtype, cur_len=cur, lens_per_seq=True, **ws.kwargs())
+    kvattn.kv_cache_write(c_a, qkv, B, NH, HS, maxT, kv_dtype=dtype, kv_scale=s_a, cur_len=cur, lens_per_seq=True)
+    kvattn.decode(o_a, qkv, c_a, B, NH, HS, maxT, kv_scale=s_a, **kw)
+    kvattn.append_decode(o_b, qkv, c_b, B, NH, HS, maxT, kv_scale=s_b, **kw)
+    torch.cuda.synchronize()
+    iv = torch.int32 if dtype == "f32" else (torch.int16 if dtype == "bf16" else torch.uint8)
+    assert torch.equal(c_a.view(iv), c_b.view(iv)), f"{dtype}: appended cache"
+    if scale is not None:
+        assert torch.equal(s_a.view(torch.int32), s_b.view(torch.int32)), f"{dtype}: appended scales"
+    ov = torch.int32 if dtype == "f32" else torch.int16
+    assert torch.equal(o_a.view(ov), o_b.view(ov)), f"{dtype}: fused append output"
+
+
+def test_workspace_shared_by_plans_of_different_slot_counts(dev):
+    """One workspace, sized for the largest plan, serves calls whose plans differ in slot
+    count: AUTO's split + merge (8 slots), the last-block merge with 16 and 4 slots, the
+    designated merger with 64 slots, and AUTO again.  Each output against split + merge on a
+    workspace of its own.  The partials of one plan must never land where another plan keeps
+    its tagged words (a float pair can read as a published partial)."""
+    import torch
+    kvattn = _kv()
+    B, NH, maxT = 64, 2, 4096
+    rng = np.random.RandomState(23)
+    lens = rng.randint(1, maxT + 1, B).astype(np.int32)
+    case = make_case("bf16", B, NH, maxT, lens - 1, seed=431)
+    qkv, cache, _, cur = to_device(case, dev)
+    nbytes = max(kvattn.workspace_bytes(B, NH, HS, maxT, S) for S in (0, 16, 4, -64))
+    buf = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+    kw = dict(workspace=buf, workspace_nbytes=nbytes)
+    ref = out_tensor(case, dev)
+    own = kvattn.Workspace(B, NH, maxT, 0)
+    kvattn.decode(ref, qkv, cache, B, NH, HS, maxT, kv_dtype="bf16", cur_len=cur, lens_per_seq=True,
+                  strategy="split_merge", **own.kwargs())
+    torch.cuda.synchronize()
+    ref_h = ref.float().cpu().numpy()
+    assert_close(ref_h, case.reference(), "bf16", "split + merge")
+    for i, (strategy, S) in enumerate([("auto", 0), ("lastblock", 16), ("designated", -64), ("lastblock", 4),
+                                       ("designated", -64), ("auto", 0), ("auto", 0)]):
+        out = out_tensor(case, dev)
+        kvattn.decode(out, qkv, cache, B, NH, HS, maxT, kv_dtype="bf16", cur_len=cur, lens_per_seq=True, S=S,
+                      strategy=strategy, **kw)
+        torch.cuda.synchronize()
+        d = np.abs(out.float().cpu().numpy() - ref_h).max()
+        assert d <= 2e-2, f"call {i} {strategy} S={S}: max |diff| {d:.3e} against split + merge"
+
+
 @pytest.mark.parametrize("B", [130, 300])
 def test_ragged_many_sequences_strided_grid(dev, B):
     """Ragged lengths with more sequences than one wave counts at once: B = 130 takes the
