@@ -131,8 +131,23 @@ __device__ __forceinline__ size_t cache_row(const GemvArgs& a, int b, int part, 
     return row;
 }
 
+// The weights, x, scales, bias, shape and output also come as leading scalar parameters
+// (14 dwords, preloaded into SGPRs at wave launch: the library is built with kernel-argument
+// preloading), so the weight and x loads issue without a scalar load of the argument block.
 template <int WT, int kC>
-__global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(GemvArgs a) {
+__global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(const uint8_t* pk_W, const uint8_t* pk_x,
+                                                                  const float* pk_w_scale, const void* pk_bias,
+                                                                  int pk_B, int pk_M, int pk_K, void* pk_out,
+                                                                  int pk_gelu, GemvArgs a) {
+    a.W = pk_W;
+    a.x = pk_x;
+    a.w_scale = pk_w_scale;
+    a.bias = pk_bias;
+    a.B = pk_B;
+    a.M = pk_M;
+    a.K = pk_K;
+    a.out = pk_out;
+    a.gelu = pk_gelu;
     using F = WFmt<WT>;
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int m = blockIdx.x * kGemvWaves + wave;
@@ -270,7 +285,7 @@ int launch_gemv(GemvArgs a, int w_dtype, void* stream) {
         case KVATTN_KV_INT8: fn = gemv_ptr<KVATTN_KV_INT8>(per_lane); break;
         default: fn = gemv_ptr<KVATTN_KV_FP8_E4M3>(per_lane); break;
     }
-    void* params[] = {&a};
+    void* params[] = {&a.W, &a.x, &a.w_scale, &a.bias, &a.B, &a.M, &a.K, &a.out, &a.gelu, &a};
     const hipError_t e = hipLaunchKernel(fn, dim3((unsigned)((M + kGemvWaves - 1) / kGemvWaves)),
                                          dim3(kGemvWaves * kWave), params, 0, (hipStream_t)stream);
     if (e != hipSuccess) {

@@ -572,10 +572,12 @@ __device__ __forceinline__ void weight_tile(const Slot& sl, int r, int total, in
 // kFresh: append and attend in one launch; kv_out / kv_scale_out receive the current
 // token's row (they alias kv / kv_scale, whose row cur_len is then never used).
 template <int DT, int kThreads, int kU, bool kFresh>
+// Parameters in the order the first loads need them: the leading 14 dwords are preloaded
+// into SGPRs at wave launch (the library is built with kernel-argument preloading).
 __global__ __launch_bounds__(kThreads) void fused_single_kernel(
-    void* __restrict__ out, const void* __restrict__ qkv, const uint8_t* kv,
-    const float* kv_scale, uint8_t* kv_out, float* kv_scale_out, const int* __restrict__ cur_len,
-    int lens_per_seq, int B, int NH, int maxT, int spec_rows, float qscale) {
+    const void* __restrict__ qkv, const uint8_t* kv, const int* __restrict__ cur_len, int lens_per_seq, int B,
+    int NH, int maxT, int spec_rows, float qscale, const float* kv_scale, void* __restrict__ out, uint8_t* kv_out,
+    float* kv_scale_out) {
     using R = Row<DT>;
     constexpr int kW = kThreads / kWave;
     constexpr int kRPL = kRowsPerLoad<DT>;
@@ -730,6 +732,13 @@ struct SplitArgs {
     int spec_rows;  // the host's view of the attended length (0: unknown); see split_kernel
     float qscale;   // scale * log2(e)
 };
+
+// Kernel parameter arrays of split_kernel and merge_kernel (their leading scalars, then the
+// struct), for launches through hipLaunchKernel, cooperative launches and graph nodes.
+#define SPLIT_PARAMS(x) {&(x).kv, &(x).qkv, &(x).cur_len, &(x).B, &(x).NH, &(x).maxT, &(x).S, &(x).seg_rows, \
+                         &(x).spec_rows, &(x).lens_per_seq, &(x).qscale, &(x)}
+#define MERGE_PARAMS(x) {&(x).part_max, &(x).part_lse, &(x).part_out, &(x).cur_len, &(x).B, &(x).NH, &(x).maxT, \
+                         &(x).S, &(x).seg_rows, &(x).lens_per_seq, &(x)}
 
 struct Item {
     int b, h, s, total, n_seg, rows;
@@ -910,7 +919,24 @@ __device__ __forceinline__ void merge_partials(void* out, const float* part_out,
 // cur_len takes that row from qkv and writes it to the cache).  kPaged: the cache is a page
 // pool addressed through a block table (segments then start at multiples of the tile).
 template <int DT, int kMode, int kW, int kU, bool kFresh, bool kPaged>
-__global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS : 1) void split_kernel(SplitArgs a) {
+__global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS : 1) void split_kernel(const uint8_t* pk_kv, const void* pk_qkv, const int* pk_len, int pk_B, int pk_NH,
+                                         int pk_maxT, int pk_S, int pk_seg_rows, int pk_spec_rows, int pk_lens,
+                                         float pk_qscale, SplitArgs a) {
+    // The fields that the first loads depend on also come as leading scalar parameters: the
+    // library is built with kernel-argument preloading (14 dwords), so the hardware hands
+    // them over in SGPRs at wave launch and the first K/V, q and length requests do not wait
+    // for a scalar load of the argument block.  The struct keeps the rest.
+    a.kv = pk_kv;
+    a.qkv = pk_qkv;
+    a.cur_len = pk_len;
+    a.B = pk_B;
+    a.NH = pk_NH;
+    a.maxT = pk_maxT;
+    a.S = pk_S;
+    a.seg_rows = pk_seg_rows;
+    a.spec_rows = pk_spec_rows;
+    a.lens_per_seq = pk_lens;
+    a.qscale = pk_qscale;
     using R = Row<DT>;
     __shared__ float s_m[kW];
     __shared__ float s_l[kW];
@@ -1253,7 +1279,21 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
 
 // Stand-alone merge: one wave per (b,h).
 template <int DT>
-__global__ __launch_bounds__(kWave) void merge_kernel(SplitArgs a) {
+// The partial pointers, the length and the shape also come as leading scalars (preloaded
+// into SGPRs, as for split_kernel), so the partial loads issue without a scalar wait.
+__global__ __launch_bounds__(kWave) void merge_kernel(const float* pk_max, const float* pk_lse, const float* pk_out,
+                                                      const int* pk_len, int pk_B, int pk_NH, int pk_maxT, int pk_S,
+                                                      int pk_seg_rows, int pk_lens, SplitArgs a) {
+    a.part_max = const_cast<float*>(pk_max);
+    a.part_lse = const_cast<float*>(pk_lse);
+    a.part_out = const_cast<float*>(pk_out);
+    a.cur_len = pk_len;
+    a.B = pk_B;
+    a.NH = pk_NH;
+    a.maxT = pk_maxT;
+    a.S = pk_S;
+    a.seg_rows = pk_seg_rows;
+    a.lens_per_seq = pk_lens;
     const int bh = blockIdx.x;
     const int b = bh / a.NH;
     const int c = threadIdx.x;
@@ -1454,13 +1494,12 @@ int launch_fused_single(void* out, const void* qkv, const void* kv, const float*
         constexpr int kThreads = kWavesLat * kWave;
         if (kv_out)
             hipLaunchKernelGGL((fused_single_kernel<DT, kThreads, kUnrollLat<DT>, true>), dim3(B * NH),
-                               dim3(kThreads), lds, stream, out, qkv, (const uint8_t*)kv, kv_scale,
-                               (uint8_t*)kv_out, kv_scale_out, cur_len, lens_per_seq, B, NH, maxT, spec_rows, qs);
+                               dim3(kThreads), lds, stream, qkv, (const uint8_t*)kv, cur_len, lens_per_seq, B, NH,
+                               maxT, spec_rows, qs, kv_scale, out, (uint8_t*)kv_out, kv_scale_out);
         else
             hipLaunchKernelGGL((fused_single_kernel<DT, kThreads, kUnrollLat<DT>, false>), dim3(B * NH),
-                               dim3(kThreads), lds, stream, out, qkv, (const uint8_t*)kv, kv_scale,
-                               (uint8_t*)nullptr, (float*)nullptr, cur_len, lens_per_seq, B, NH, maxT, spec_rows,
-                               qs);
+                               dim3(kThreads), lds, stream, qkv, (const uint8_t*)kv, cur_len, lens_per_seq, B, NH,
+                               maxT, spec_rows, qs, kv_scale, out, (uint8_t*)nullptr, (float*)nullptr);
         KV_HIP(hipGetLastError());
         return KVATTN_OK;
     });
@@ -1523,7 +1562,7 @@ int launch_split(const SplitArgs& a, int kv_dtype, int mode, bool lat, hipStream
         if (!fn) return KVATTN_ERR_DTYPE;
         grid = (grid + kStridedFactor - 1) / kStridedFactor;
     }
-    void* params[] = {&args};
+    void* params[] = SPLIT_PARAMS(args);
     KV_HIP(hipLaunchKernel(fn, dim3((unsigned)grid), dim3(threads), params, 0, stream));
     return KVATTN_OK;
 }
@@ -1531,7 +1570,8 @@ int launch_split(const SplitArgs& a, int kv_dtype, int mode, bool lat, hipStream
 int launch_merge(const SplitArgs& a, int kv_dtype, hipStream_t stream) {
     return dispatch_dtype(kv_dtype, [&](auto dtc) -> int {
         constexpr int DT = decltype(dtc)::value;
-        hipLaunchKernelGGL((merge_kernel<DT>), dim3(a.B * a.NH), dim3(kWave), 0, stream, a);
+        hipLaunchKernelGGL((merge_kernel<DT>), dim3(a.B * a.NH), dim3(kWave), 0, stream, a.part_max, a.part_lse,
+                           a.part_out, a.cur_len, a.B, a.NH, a.maxT, a.S, a.seg_rows, a.lens_per_seq, a);
         KV_HIP(hipGetLastError());
         return KVATTN_OK;
     });
@@ -1566,7 +1606,7 @@ int launch_coop(const SplitArgs& a, int kv_dtype, bool lat, hipStream_t stream) 
         KV_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, 0));
         if (blocks > (long long)per_cu * cus) continue;
         SplitArgs args = a;
-        void* params[] = {&args};
+        void* params[] = SPLIT_PARAMS(args);
         KV_HIP(hipLaunchCooperativeKernel(fn, dim3((unsigned)blocks), dim3(threads), params, 0, stream));
         return KVATTN_OK;
     }
@@ -1617,7 +1657,8 @@ int launch_graph_pair(const SplitArgs& a, int kv_dtype, bool lat, hipStream_t st
             return KVATTN_OK;
         });
         SplitArgs args = a;
-        void* params[] = {&args};
+        void* params[] = SPLIT_PARAMS(args);
+        void* mparams[] = MERGE_PARAMS(args);
         hipGraph_t g = nullptr;
         KV_HIP(hipGraphCreate(&g, 0));
         hipKernelNodeParams ps{};
@@ -1632,6 +1673,7 @@ int launch_graph_pair(const SplitArgs& a, int kv_dtype, bool lat, hipStream_t st
         if (e == hipSuccess) {
             hipKernelNodeParams pm = ps;
             pm.func = fmerge;
+            pm.kernelParams = mparams;
             pm.gridDim = dim3((unsigned)a.B * a.NH);
             pm.blockDim = dim3(kWave);
             e = hipGraphAddKernelNode(&nmerge, g, &nsplit, 1, &pm);
