@@ -178,3 +178,51 @@ def test_gemv_qkv_append_equals_gemv_then_append(dev, dtype, kv, lens):
         off = 2 * B * NH * HS * 4
         arrivals = ws[off:off + 2 * B * NH * 256].view(torch.int32)
         assert int(arrivals.abs().sum()) == 0, f"{dtype} {kv} {lens}: arrival words left armed"
+
+
+@pytest.mark.parametrize("kv", ["int8", "fp8"])
+def test_gemv_qkv_append_8bit_graph_replays(dev, kv):
+    """The 8-bit QKV epilogue captured in a graph: its arrival words are re-armed by the
+    kernel itself (no memset node), so every replay must quantise afresh.  Three replays
+    with new inputs and eager work in between, each against kvattn_gemv +
+    kvattn_cache_write on a copy of the cache: qkv, codes and row scales bit for bit."""
+    import torch
+    kvattn = _kv()
+    NH, HS, K, maxT, B = 12, 64, 768, 64, 2
+    M = 3 * NH * HS
+    d, _ = _make("int8", B, M, K, seed=91)
+    W, scale = d["W"].to(dev), d["scale"].to(dev)
+    bias = None if d["bias"] is None else d["bias"].to(dev)
+    x = d["x"].to(dev).contiguous()
+    cache = torch.zeros(2 * B * NH * maxT * HS, dtype=torch.uint8, device=dev)
+    kscale = torch.zeros(2 * B * NH * maxT, device=dev)
+    cur = torch.tensor([5, 40], dtype=torch.int32, device=dev)
+    ws_bytes = kvattn.gemv_qkv_append_workspace_bytes(B, NH)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    kvattn.workspace_init(ws, ws_bytes)
+    qkv = torch.empty(B * M, dtype=torch.bfloat16, device=dev)
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            kvattn.gemv_qkv_append(qkv, W, x, B, NH, HS, K, cache, maxT, w_dtype="int8", kv_dtype=kv, w_scale=scale,
+                                   bias=bias, kv_scale=kscale, cur_len=cur, lens_per_seq=True, workspace=ws,
+                                   workspace_nbytes=ws_bytes)
+    torch.cuda.synchronize()
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(92)
+    for rep in range(3):
+        x.copy_(torch.randn(x.numel(), generator=gen, device=dev).to(x.dtype).view_as(x))
+        cur.copy_(torch.tensor([5 + rep, 40 + 7 * rep], dtype=torch.int32, device=dev))
+        c_ref, s_ref = cache.clone(), kscale.clone()
+        q_ref = torch.empty_like(qkv)
+        kvattn.gemv(q_ref, W, x, B, M, K, w_dtype="int8", w_scale=scale, bias=bias)
+        kvattn.kv_cache_write(c_ref, q_ref, B, NH, HS, maxT, kv_dtype=kv, kv_scale=s_ref, cur_len=cur,
+                              lens_per_seq=True)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(qkv.view(torch.int16), q_ref.view(torch.int16)), f"{kv} replay {rep}: qkv"
+        assert torch.equal(cache, c_ref), f"{kv} replay {rep}: codes"
+        assert torch.equal(kscale.view(torch.int32), s_ref.view(torch.int32)), f"{kv} replay {rep}: row scales"
