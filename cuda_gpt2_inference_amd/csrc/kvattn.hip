@@ -466,13 +466,24 @@ __device__ __forceinline__ void online_tiles_paged(const PagedView& pv, int b, i
         if (page < 0 || page >= pv.num_pages) continue;
         const int pr0 = r / P * P;
         const Slot sp = page_slot<DT>(pv, page, h, slice);
-        load_tile<DT, kU, true>(t, sp, r - pr0, j1 - pr0, slot_row);
-        if (kFresh && cur >= r && cur < min(r + kTile, j1)) {
-            const size_t rk = ((size_t)page * 2 * pv.NH + h) * P + (cur - pr0);
-            const FreshDst fd{kv_out, kv_scale_out, rk, rk + (size_t)pv.NH * P, slice};
-            patch_tile<DT, kU>(t, fr, fd, r - pr0, slot_row, cur - pr0);
+        auto fresh = [&]() {
+            if (kFresh && cur >= r && cur < min(r + kTile, j1)) {
+                const size_t rk = ((size_t)page * 2 * pv.NH + h) * P + (cur - pr0);
+                const FreshDst fd{kv_out, kv_scale_out, rk, rk + (size_t)pv.NH * P, slice};
+                patch_tile<DT, kU>(t, fr, fd, r - pr0, slot_row, cur - pr0);
+            }
+        };
+        // Full tiles take the unchecked loads and scores (no per-row conditions around the
+        // loads), as the contiguous walk does; only a segment's last tile is checked.
+        if (r + kTile <= j1) {
+            load_tile<DT, kU, false>(t, sp, r - pr0, j1 - pr0, slot_row);
+            fresh();
+            consume_tile<DT, kU, false>(t, r - pr0, j1 - pr0, slot_row, q, m, l, acc);
+        } else {
+            load_tile<DT, kU, true>(t, sp, r - pr0, j1 - pr0, slot_row);
+            fresh();
+            consume_tile<DT, kU, true>(t, r - pr0, j1 - pr0, slot_row, q, m, l, acc);
         }
-        consume_tile<DT, kU, true>(t, r - pr0, j1 - pr0, slot_row, q, m, l, acc);
     }
 }
 
