@@ -62,19 +62,34 @@ struct GemvArgs {
     unsigned* arrivals;
 };
 
+// The x values one 16-byte weight chunk multiplies: 16 bytes (4 floats or 8 bf16), or 32
+// bytes (16 bf16) for 8-bit weights.
+template <int WT>
+struct XRaw {
+    uint4 v[WFmt<WT>::kXBytes / 16];
+};
+
+template <int WT>
+__device__ __forceinline__ XRaw<WT> load_x(const uint8_t* xp) {
+    XRaw<WT> r;
+#pragma unroll
+    for (int h = 0; h < WFmt<WT>::kXBytes / 16; ++h) r.v[h] = reinterpret_cast<const uint4*>(xp)[h];
+    return r;
+}
+
 // Dot product of one 16-byte weight chunk with the x values it multiplies.
 template <int WT>
-__device__ __forceinline__ float chunk_dot(const uint4& w, const uint8_t* xp) {
+__device__ __forceinline__ float chunk_dot(const uint4& w, const XRaw<WT>& xr) {
     using F = WFmt<WT>;
     float wf[F::kElems], xf[F::kElems];
     if constexpr (WT == KVATTN_KV_F32) {
-        const uint4 xv = *reinterpret_cast<const uint4*>(xp);
+        const uint4 xv = xr.v[0];
         wf[0] = __uint_as_float(w.x); wf[1] = __uint_as_float(w.y);
         wf[2] = __uint_as_float(w.z); wf[3] = __uint_as_float(w.w);
         xf[0] = __uint_as_float(xv.x); xf[1] = __uint_as_float(xv.y);
         xf[2] = __uint_as_float(xv.z); xf[3] = __uint_as_float(xv.w);
     } else if constexpr (WT == KVATTN_KV_BF16) {
-        const uint4 xv = *reinterpret_cast<const uint4*>(xp);
+        const uint4 xv = xr.v[0];
         const uint32_t ww[4] = {w.x, w.y, w.z, w.w}, xw[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -85,7 +100,7 @@ __device__ __forceinline__ float chunk_dot(const uint4& w, const uint8_t* xp) {
         decode_codes<WT == KVATTN_KV_FP8_E4M3>(w, wf);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const uint4 xv = reinterpret_cast<const uint4*>(xp)[h];
+            const uint4 xv = xr.v[h];
             const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -123,8 +138,9 @@ constexpr int kArrivalStride = 64;   // u32 words between two rows' arrival word
 
 // Cache row (in units of kHd elements) of part 1 (K) or 2 (V), head h, sequence b at the
 // position being appended: column cur_len, clamped to [0, maxT - 1] as the append does.
-__device__ __forceinline__ size_t cache_row(const GemvArgs& a, int b, int part, int h) {
-    int cl = a.cur_len[a.lens_per_seq ? b : 0];
+// len0: cur_len[0], loaded ahead with the weights.
+__device__ __forceinline__ size_t cache_row(const GemvArgs& a, int b, int part, int h, int len0) {
+    int cl = a.lens_per_seq && b > 0 ? a.cur_len[b] : len0;
     cl = cl < 0 ? 0 : (cl > a.maxT - 1 ? a.maxT - 1 : cl);
     size_t row = ((size_t)b * a.NH + h) * a.maxT + cl;
     if (part == 2) row += (size_t)a.B * a.NH * a.maxT;
@@ -154,22 +170,36 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(const uint8_t*
     if (m >= a.M) return;   // whole wave; the one barrier (8-bit QKV epilogue) has M % kGemvWaves == 0
     const int nch = a.K * F::kWBytes / 16;
     const uint8_t* wrow = a.W + (size_t)m * a.K * F::kWBytes;
+    // Every load is unconditional, so that all of them issue before the first wait: a lane's
+    // chunks beyond the row (c >= nch) read chunk nch - 1 again and their products are
+    // dropped by a select.  (Loads behind branches make the code generator wait for each
+    // one before the next: one memory round trip per chunk.)
     uint4 w[kC];
 #pragma unroll
-    for (int i = 0; i < kC; ++i) {
-        const int c = lane + i * kWave;
-        w[i] = c < nch ? *reinterpret_cast<const uint4*>(wrow + (size_t)c * 16) : make_uint4(0u, 0u, 0u, 0u);
-    }
-    const float ws = F::k8bit ? a.w_scale[m] : 1.0f;
-    const float bias = a.bias ? load_act<WT>(a.bias, m) : 0.0f;
+    for (int i = 0; i < kC; ++i)
+        w[i] = *reinterpret_cast<const uint4*>(wrow + (size_t)min(lane + i * kWave, nch - 1) * 16);
     constexpr int kActBytes = F::kActF32 ? 4 : 2;
-    for (int b = 0; b < a.B; ++b) {
+    // x of the first vector and the bias are requested right behind the weights, before
+    // anything waits (the weights' unpacking, which the code generator hoists out of the
+    // vector loop, waits for the weights only).
+    XRaw<WT> xr[kC];
+    auto load_xs = [&](int b) {
         const uint8_t* xb = a.x + (size_t)b * a.K * kActBytes;
+#pragma unroll
+        for (int i = 0; i < kC; ++i) xr[i] = load_x<WT>(xb + (size_t)min(lane + i * kWave, nch - 1) * F::kXBytes);
+    };
+    load_xs(0);
+    const float braw = load_act<WT>(a.bias ? a.bias : (const void*)a.x, a.bias ? m : 0);
+    const float bias = a.bias ? braw : 0.0f;
+    const int len0 = (a.kv ? a.cur_len : reinterpret_cast<const int*>(a.x))[0];   // the QKV epilogue's column
+    const float ws = F::k8bit ? a.w_scale[m] : 1.0f;
+    for (int b = 0; b < a.B; ++b) {
+        if (b > 0) load_xs(b);
         float acc = 0.0f;
 #pragma unroll
         for (int i = 0; i < kC; ++i) {
-            const int c = lane + i * kWave;
-            if (c < nch) acc += chunk_dot<WT>(w[i], xb + (size_t)c * F::kXBytes);
+            const float d = acc + chunk_dot<WT>(w[i], xr[i]);
+            acc = lane + i * kWave < nch ? d : acc;
         }
         acc = wave_sum(acc);
         if (lane == 0) {
@@ -184,7 +214,7 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(const uint8_t*
                 const int part = m / (a.NH * kHd);
                 if (part > 0) {
                     const int h = (m - part * a.NH * kHd) / kHd, c = m - part * a.NH * kHd - h * kHd;
-                    store_act<WT>(a.kv, cache_row(a, b, part, h) * kHd + c, pre);
+                    store_act<WT>(a.kv, cache_row(a, b, part, h, len0) * kHd + c, pre);
                 }
             }
         }
@@ -222,7 +252,7 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(const uint8_t*
                         const float x = __hip_atomic_load(a.stage + rid * kHd + lane, __ATOMIC_RELAXED,
                                                           __HIP_MEMORY_SCOPE_AGENT);
                         const float amax = wave_max(fabsf(x));
-                        const size_t row = cache_row(a, b, part, h);
+                        const size_t row = cache_row(a, b, part, h, len0);
                         if (a.kv_dtype == KVATTN_KV_FP8_E4M3) {
                             const float scale = amax / kW8Limit<KVATTN_KV_FP8_E4M3>;
                             a.kv[row * kHd + lane] = w8_code<KVATTN_KV_FP8_E4M3>(x, scale);
