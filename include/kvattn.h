@@ -190,6 +190,9 @@ int kvattn_plan(int B, int NH, int hs, int maxT, int len_hint, int S, int strate
  *   workspace  device memory of kvattn_workspace_bytes(B, NH, hs, maxT, S) bytes,
  *              initialised once with kvattn_workspace_init; may be NULL for
  *              FUSED_SINGLE.  Calls sharing a workspace must be ordered (one stream).
+ *   workspace_bytes  the buffer's actual size.  One buffer, sized for the largest plan,
+ *              may serve calls planned with different S: the partials are laid out
+ *              from its start and the designated merger's tagged words from its end.
  */
 int kvattn_decode(void* out, const void* qkv, const void* kv_cache, const float* kv_scale,
                   int B, int NH, int hs, int maxT,
