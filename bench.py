@@ -595,13 +595,16 @@ def gemv_cpu_baseline(seconds=3.0):
             "kind": "port", "sample": f"oracle_gemv FP32 768x768, B=1, median of {reps} calls"}
 
 
-def kernel_key(plan, B, NH, append=False, paged=False, ragged=False):
+def kernel_key(plan, B, NH, total, append=False, paged=False, ragged=False):
     """(name prefix, grid suffix) of the BF16 split kernel a plan launches, as keyed in the
-    rocprof summaries: `split_kernel<1, MODE, WAVES, TILE, APPEND, PAGED> grid=WORKITEMS`
-    (4 waves and 8-row-chunk tiles for BF16 in both shapes of this build).  Modes: 0 partials,
-    1 last-block, 2 cooperative, 3 designated, 4 designated planned on the device, 5 partials
-    of ragged lengths on half the grid (two packed segments per workgroup)."""
+    rocprof summaries: `split_kernel<1, MODE, WAVES, TILE, APPEND, PAGED> grid=WORKITEMS`.
+    4 waves in both shapes of this build; TILE (8-row chunks per lane) is 4 in the latency
+    shape (B*NH*total below 2^19 rows, `total` the planned attended length) and 8 in the
+    streaming shape and in the device-planned designated kernel (mode 4).  Modes: 0 partials, 1 last-block, 2 cooperative, 3 designated, 4
+    designated planned on the device, 5 partials of ragged lengths on half the grid (two
+    packed segments per workgroup)."""
     st, slots, rows = plan
+    tile = 4 if B * NH * total < (1 << 19) else 8
     mode = {2: 0, 4: 0, 5: 1, 3: 2, 6: 3}.get(st)
     if mode is None:
         return None
@@ -610,8 +613,10 @@ def kernel_key(plan, B, NH, append=False, paged=False, ragged=False):
         mode = 4
     elif mode == 0 and ragged and rows != 0 and B <= 256:
         mode, blocks = 5, (blocks + 1) // 2
+    if mode == 4:
+        tile = 8
     flags = f"{'true' if append else 'false'}, {'true' if paged else 'false'}"
-    return f"split_kernel<1, {mode}, 4, 8, {flags}>", f"grid={blocks * 256}"
+    return f"split_kernel<1, {mode}, 4, {tile}, {flags}>", f"grid={blocks * 256}"
 
 
 def lookup(traffic, key):
@@ -827,20 +832,20 @@ def main():
     us_call = graph_ms * 1000.0 / c2.L
     nbytes = bytes_per_call([c2.T], c2.NH, 2, 2, c2.B)
     achieved = nbytes / (us_call * 1e-6) / 1e9
-    key2, traffic2 = lookup(traffic, kernel_key(c2.plan, c2.B, c2.NH))
+    key2, traffic2 = lookup(traffic, kernel_key(c2.plan, c2.B, c2.NH, c2.T))
 
     c5 = None
     if not args.no_c5:
         c5o = C5(args, torch, kvattn, dev)
         c5 = c5o.measure()
-        k5, t5 = lookup(traffic, kernel_key(c5o.plan, c5o.B, c5o.NH, ragged=True))
+        k5, t5 = lookup(traffic, kernel_key(c5o.plan, c5o.B, c5o.NH, c5o.maxT, ragged=True))
         c5["kernel"] = k5
         c5["traffic_bytes_split_kernel"] = t5
         del c5o
         c5["paged"] = C5Paged(args, torch, kvattn, dev).measure()
         c5["paged"]["kernel"], c5["paged"]["traffic_bytes_split_kernel"] = lookup(
             traffic, kernel_key(kvattn.plan(C5Paged.B, C5Paged.NH, HD, C5Paged.maxT, kv_dtype="bf16"), C5Paged.B,
-                                C5Paged.NH, paged=True, ragged=True))
+                                C5Paged.NH, C5Paged.maxT, paged=True, ragged=True))
     configs = None if args.no_configs else other_configs(torch, kvattn, dev)
     gemv = None if args.no_configs else gemv_configs(torch, kvattn, dev)
     qkv_append = None if args.no_configs else qkv_append_configs(torch, kvattn, dev)

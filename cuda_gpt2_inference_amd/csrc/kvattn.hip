@@ -100,6 +100,16 @@ template <int DT> constexpr int kUnroll = Row<DT>::k8bit ? KVATTN_UNROLL_BYTE : 
 #endif
 template <int DT> constexpr int kUnrollLat = KVATTN_LAT_ROWS / kRowsPerLoad<DT> > 0 ? KVATTN_LAT_ROWS / kRowsPerLoad<DT> : 1;
 constexpr int kWavesLat = KVATTN_LAT_WAVES;
+// The split kernels' latency shape takes KVATTN_SPLIT_LAT_ROWS rows per wave per tile: a
+// 128-row designated segment is then one full tile per wave of a 4-wave workgroup.  Each
+// tile's arithmetic runs over all its row slots, valid or masked, and at GPT-2's sizes it is
+// on the call's critical path: 64-row tiles, half of them masked, cost C2 0.24 µs per call.
+// (The device-planned designated instance keeps KVATTN_LAT_ROWS: see split_ptr.)
+#ifndef KVATTN_SPLIT_LAT_ROWS
+#define KVATTN_SPLIT_LAT_ROWS 32
+#endif
+template <int DT> constexpr int kUnrollSplitLat =
+    KVATTN_SPLIT_LAT_ROWS / kRowsPerLoad<DT> > 0 ? KVATTN_SPLIT_LAT_ROWS / kRowsPerLoad<DT> : 1;
 
 // Decode one lane's 16-byte chunk of a row into kElems floats.
 template <int DT>
@@ -1542,7 +1552,12 @@ const void* split_ptr_shape(int mode, bool fresh, bool paged) {
 
 template <int DT>
 const void* split_ptr(int mode, bool lat, bool fresh, bool paged) {
-    if (lat) return split_ptr_shape<DT, kWavesLat, kUnrollLat<DT>>(mode, fresh, paged);
+    if (lat) {
+        // The device-planned designated instance keeps the 64-row tiles: its segment 0 splits
+        // up to kFusedMaxRows rows over its waves from the first request on (one tile each).
+        if (mode == kDesignatedDev) return split_ptr_shape<DT, kWavesLat, kUnrollLat<DT>>(mode, fresh, paged);
+        return split_ptr_shape<DT, kWavesLat, kUnrollSplitLat<DT>>(mode, fresh, paged);
+    }
     return split_ptr_shape<DT, kWaves, kUnroll<DT>>(mode, fresh, paged);
 }
 
