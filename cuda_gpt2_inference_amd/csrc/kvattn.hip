@@ -100,6 +100,14 @@ template <int DT> constexpr int kUnroll = Row<DT>::k8bit ? KVATTN_UNROLL_BYTE : 
 #endif
 template <int DT> constexpr int kUnrollLat = KVATTN_LAT_ROWS / kRowsPerLoad<DT> > 0 ? KVATTN_LAT_ROWS / kRowsPerLoad<DT> : 1;
 constexpr int kWavesLat = KVATTN_LAT_WAVES;
+// fused_single: a head of up to kFusedMaxRows positions is one tile per wave.  FP32 rows are
+// the widest (four lanes' arithmetic per row of bf16), so FP32 takes 8 waves of 32-row tiles
+// and the others 4 waves of KVATTN_LAT_ROWS-row tiles.  Measured (12-layer graphs, A/B both
+// orders): FP32 at 256 positions −0.15 µs with 8 × 32; BF16 within ±0.04; INT8 +0.23.
+template <int DT> constexpr int kFusedWaves = DT == KVATTN_KV_F32 ? 8 : KVATTN_LAT_WAVES;
+template <int DT> constexpr int kFusedRows = DT == KVATTN_KV_F32 ? 32 : KVATTN_LAT_ROWS;
+template <int DT> constexpr int kUnrollFused =
+    kFusedRows<DT> / kRowsPerLoad<DT> > 0 ? kFusedRows<DT> / kRowsPerLoad<DT> : 1;
 // The split kernels' latency shape takes KVATTN_SPLIT_LAT_ROWS rows per wave per tile: a
 // 128-row designated segment is then one full tile per wave of a 4-wave workgroup.  Each
 // tile's arithmetic runs over all its row slots, valid or masked, and at GPT-2's sizes it is
@@ -1512,13 +1520,13 @@ int launch_fused_single(void* out, const void* qkv, const void* kv, const float*
     const float qs = qscale_for(kHeadDim);
     return dispatch_dtype(kv_dtype, [&](auto dtc) -> int {
         constexpr int DT = decltype(dtc)::value;
-        constexpr int kThreads = kWavesLat * kWave;
+        constexpr int kThreads = kFusedWaves<DT> * kWave;
         if (kv_out)
-            hipLaunchKernelGGL((fused_single_kernel<DT, kThreads, kUnrollLat<DT>, true>), dim3(B * NH),
+            hipLaunchKernelGGL((fused_single_kernel<DT, kThreads, kUnrollFused<DT>, true>), dim3(B * NH),
                                dim3(kThreads), lds, stream, qkv, (const uint8_t*)kv, cur_len, lens_per_seq, B, NH,
                                maxT, spec_rows, qs, kv_scale, out, (uint8_t*)kv_out, kv_scale_out);
         else
-            hipLaunchKernelGGL((fused_single_kernel<DT, kThreads, kUnrollLat<DT>, false>), dim3(B * NH),
+            hipLaunchKernelGGL((fused_single_kernel<DT, kThreads, kUnrollFused<DT>, false>), dim3(B * NH),
                                dim3(kThreads), lds, stream, qkv, (const uint8_t*)kv, cur_len, lens_per_seq, B, NH,
                                maxT, spec_rows, qs, kv_scale, out, (uint8_t*)nullptr, (float*)nullptr);
         KV_HIP(hipGetLastError());
