@@ -34,6 +34,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <tuple>
@@ -41,12 +42,17 @@
 #include "kvattn.h"
 #include "lanes.hpp"
 
+// The 64-bit dispatch id of the running kernel dispatch (LLVM's llvm.amdgcn.dispatch.id; it
+// has no clang builtin).  Kernels that call it receive it in two user SGPRs at wave launch.
+extern "C" __device__ unsigned long long kvattn_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
+
 namespace {
 
 constexpr int kHeadDim = 64;
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / kWave;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kQScale = 0.125f * kLog2e;   // 1/sqrt(hs) * log2(e) for hs = 64 (exact: 0.125 = 2^-3)
 constexpr float kLn2 = 0.69314718055994531f;
 constexpr float kEmptyMax = -FLT_MAX;   // max of an empty segment (reference sentinel)
 constexpr float kStartMax = -1.0e30f;   // finite start value of every running max
@@ -60,6 +66,9 @@ constexpr int kMaxSegments = 1 << 16;   // upper bound on segments per (b,h)
 constexpr int kMaxT = 1 << 23;          // keeps per-slot byte offsets inside 32 bits
 constexpr size_t kFusedMaxLds = 64 * 1024;  // dynamic LDS of fused_single (scores)
 constexpr int kMaxDesignatedSegments = 64;  // the designated merger follows one segment per lane
+// Workspace status words (the first 256 bytes of a kvattn_decode workspace).
+constexpr int kWsStatusMergeTimeouts = 0;   // designated merges that stopped waiting (a sticky count)
+constexpr size_t kWsStatusBytes = 256;
 
 // ------------------------------------------------------------------------------------
 // Per-dtype row geometry.
@@ -369,6 +378,24 @@ __device__ __forceinline__ void patch_tile(Tile<DT, U>& t, const FreshRaw<DT>& f
     }
 }
 
+// Rows at or beyond r1 of a tile may hold anything: a speculative first tile is requested
+// before the length is known, and a cache is never cleared past its length (NaN or Inf
+// bits, FP8 NaN codes 0x7F/0xFF, garbage 8-bit scales).  Their scores are replaced by
+// -inf, which makes p = 0, but 0 * NaN is NaN: so their V chunks and V scales are replaced
+// by zeros as well (a select on the loaded bits), and a masked row contributes exactly
+// nothing to l and acc.
+template <int DT, int U>
+__device__ __forceinline__ void mask_tile_v(Tile<DT, U>& t, int r, int r1, int slot_row) {
+    constexpr int kRPL = kRowsPerLoad<DT>;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        if (r + u * kRPL + slot_row >= r1) {
+            t.v[u] = make_uint4(0u, 0u, 0u, 0u);
+            if constexpr (Row<DT>::k8bit) t.vs[u] = 0.0f;
+        }
+    }
+}
+
 template <int DT, int U, bool kChecked>
 __device__ __forceinline__ void consume_tile(const Tile<DT, U>& t, int r, int r1, int slot_row,
                                              const float (&q)[Row<DT>::kElems], float& m, float& l,
@@ -392,9 +419,11 @@ __device__ __forceinline__ void consume_tile(const Tile<DT, U>& t, int r, int r1
     for (int u = 0; u < U; ++u) {
         const float p = exp2_fast(s[u] - mt);
         l += p;
-        const float pv = R::k8bit ? p * t.vs[u] : p;
+        const bool live = !kChecked || r + u * kRPL + slot_row < r1;
+        const uint4 vd = live ? t.v[u] : make_uint4(0u, 0u, 0u, 0u);
+        const float pv = R::k8bit ? p * (live ? t.vs[u] : 0.0f) : p;
         float x[R::kElems];
-        decode<DT>(t.v[u], x);
+        decode<DT>(vd, x);
 #pragma unroll
         for (int e = 0; e < R::kElems; ++e) acc[e] = fmaf(pv, x[e], acc[e]);
     }
@@ -653,6 +682,8 @@ __global__ __launch_bounds__(kThreads) void fused_single_kernel(
         }
         convert_q<DT>(qr, qscale, q);
         if (kFresh && cur >= r && cur < r + kTile) patch_tile<DT, kU>(t, fr, fd, r, slot_row, cur);
+        // A tile requested for a longer hinted length holds rows at or beyond `total`.
+        mask_tile_v<DT, kU>(t, r, total, slot_row);
         float s[kU];
         float mloc = kStartMax;
 #pragma unroll
@@ -760,12 +791,18 @@ struct SplitArgs {
                     // kDevicePlan: planned_rows(total) of the device length
     int spec_rows;  // the host's view of the attended length (0: unknown); see split_kernel
     float qscale;   // scale * log2(e)
+    // Designated merger: workspace status words (see kWsStatus*) and the poll bound.
+    unsigned* status;
+    int merge_polls;
 };
 
 // Kernel parameter arrays of split_kernel and merge_kernel (their leading scalars, then the
 // struct), for launches through hipLaunchKernel, cooperative launches and graph nodes.
+// split_spec(x) is the packed length hint pk_spec of split_kernel; SPLIT_PARAMS needs an
+// int lvalue `spec` holding it.
+inline int split_spec(const SplitArgs& a) { return a.lens_per_seq ? -1 : (a.spec_rows > 0 ? a.spec_rows : 0); }
 #define SPLIT_PARAMS(x) {&(x).kv, &(x).qkv, &(x).cur_len, &(x).B, &(x).NH, &(x).maxT, &(x).S, &(x).seg_rows, \
-                         &(x).spec_rows, &(x).lens_per_seq, &(x).qscale, &(x)}
+                         &spec, &(x)}
 #define MERGE_PARAMS(x) {&(x).part_max, &(x).part_lse, &(x).part_out, &(x).cur_len, &(x).B, &(x).NH, &(x).maxT, \
                          &(x).S, &(x).seg_rows, &(x).lens_per_seq, &(x)}
 
@@ -888,17 +925,24 @@ __device__ __forceinline__ float get(const float* p) {
 }
 
 // Tagged partial words of the designated merger (agent-scope relaxed atomics, emitted as
-// coherent sc1 stores and loads on gfx950).
-constexpr unsigned long long kWordValid = 1ull << 32;
-constexpr int kMergePolls = 1 << 22;  // bound on the designated merger's polls (seconds)
+// coherent sc1 stores and loads on gfx950): the value in the low half, the call's tag in the
+// high half.  The tag is the launch's dispatch id (one per kernel dispatch, increasing along
+// the queue; every replay of a captured graph dispatches anew) with the top bit set, so a
+// word counts only for the dispatch that wrote it: words left by an earlier call (a merge
+// that stopped waiting, or a plan with other slots on the same workspace) are never taken
+// for this call's, the slots need no clearing, and a zeroed workspace holds no valid word.
+constexpr int kDefaultMergePolls = 1 << 22;  // bound on the designated merger's polls (seconds)
+__device__ __forceinline__ uint32_t call_tag() { return (uint32_t)kvattn_dispatch_id() | 0x80000000u; }
 __device__ __forceinline__ void put_word(unsigned long long* p, unsigned long long w) {
     __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ unsigned long long get_word(const unsigned long long* p) {
     return __hip_atomic_load(const_cast<unsigned long long*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ unsigned long long valid_word(float v) { return kWordValid | __float_as_uint(v); }
-__device__ __forceinline__ bool word_valid(unsigned long long w) { return (w >> 32) == 1u; }
+__device__ __forceinline__ unsigned long long tagged_word(float v, uint32_t tag) {
+    return ((unsigned long long)tag << 32) | __float_as_uint(v);
+}
+__device__ __forceinline__ bool word_is(unsigned long long w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
 __device__ __forceinline__ float word_value(unsigned long long w) { return __uint_as_float((uint32_t)w); }
 
 
@@ -949,12 +993,14 @@ __device__ __forceinline__ void merge_partials(void* out, const float* part_out,
 // pool addressed through a block table (segments then start at multiples of the tile).
 template <int DT, int kMode, int kW, int kU, bool kFresh, bool kPaged>
 __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS : 1) void split_kernel(const uint8_t* pk_kv, const void* pk_qkv, const int* pk_len, int pk_B, int pk_NH,
-                                         int pk_maxT, int pk_S, int pk_seg_rows, int pk_spec_rows, int pk_lens,
-                                         float pk_qscale, SplitArgs a) {
+                                         int pk_maxT, int pk_S, int pk_seg_rows, int pk_spec, SplitArgs a) {
     // The fields that the first loads depend on also come as leading scalar parameters: the
-    // library is built with kernel-argument preloading (14 dwords), so the hardware hands
-    // them over in SGPRs at wave launch and the first K/V, q and length requests do not wait
-    // for a scalar load of the argument block.  The struct keeps the rest.
+    // library is built with kernel-argument preloading, so the hardware hands them over in
+    // SGPRs at wave launch and the first K/V, q and length requests do not wait for a scalar
+    // load of the argument block.  They fit in 12 dwords, all that is left of the 16 user
+    // SGPRs once the designated instances also take the dispatch id: pk_spec is the length
+    // hint, or -1 for per-sequence lengths (the hint is not used then), and the q scale is
+    // the constant of hs = 64.  The struct keeps the rest.
     a.kv = pk_kv;
     a.qkv = pk_qkv;
     a.cur_len = pk_len;
@@ -963,9 +1009,9 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
     a.maxT = pk_maxT;
     a.S = pk_S;
     a.seg_rows = pk_seg_rows;
-    a.spec_rows = pk_spec_rows;
-    a.lens_per_seq = pk_lens;
-    a.qscale = pk_qscale;
+    a.lens_per_seq = pk_spec < 0 ? 1 : 0;
+    a.spec_rows = pk_spec < 0 ? 0 : pk_spec;
+    a.qscale = kQScale;
     using R = Row<DT>;
     __shared__ float s_m[kW];
     __shared__ float s_l[kW];
@@ -1116,19 +1162,23 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                         // The only segment of its (b,h): the result needs no merge.
                         store_out<DT>(a.out, (size_t)bh * kHeadDim + lane, A / L);
                     } else if constexpr (kDes) {
+                        const uint32_t tag = call_tag();
                         if (it.s != 0) {
                             // Producer: publish the tagged partial and finish; nothing waits.
-                            put_word(a.tag_out + pidx * kHeadDim + lane, valid_word(A));
+                            put_word(a.tag_out + pidx * kHeadDim + lane, tagged_word(A, tag));
                             if (lane == 0) {
-                                put_word(a.tag_ml + 2 * pidx, valid_word(Mb * kLn2));
-                                put_word(a.tag_ml + 2 * pidx + 1, valid_word(L));
+                                put_word(a.tag_ml + 2 * pidx, tagged_word(Mb * kLn2, tag));
+                                put_word(a.tag_ml + 2 * pidx + 1, tagged_word(L, tag));
                             }
                         } else {
                             // Designated merger (segment 0): lane u follows segment u.  A head's
                             // segments have consecutive workgroup ids with segment 0 first, and
                             // workgroups are dispatched in id order, so the producers waited for are
                             // already resident or next in line behind workgroups that do not wait:
-                            // the polls end.  The bound only guards against that order failing.
+                            // the polls end.  The host also keeps every designated grid within what
+                            // the GPU holds at once.  The bound (a.merge_polls rounds) only guards
+                            // against that order failing; a merge that reaches it writes NaN and
+                            // counts itself in the workspace's status words for the host to read.
                             const int n = it.n_seg;
                             const size_t p0 = (size_t)bh * a.S;
                             bool lost = n > kMaxDesignatedSegments;
@@ -1136,6 +1186,7 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                             if (lane < n) seg_range(lane, uj0, uj1);
                             const bool need = lane >= 1 && lane < n && uj1 > uj0 && !lost;
                             const unsigned long long prod = __ballot(need);   // segments a producer publishes
+                            const unsigned long long kHave = (unsigned long long)tag << 32;  // a slot not waited for
                             // Channel words of up to 16 segments per batch; the first batch is
                             // requested together with the maxima and exp-sums, so up to 17
                             // segments merge after one memory round trip.
@@ -1145,36 +1196,23 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                                 for (int u = 0; u < kBatch; ++u)
                                     w[u] = k + u < n && ((prod >> (k + u)) & 1ull)
                                                ? get_word(a.tag_out + (p0 + k + u) * kHeadDim + lane)
-                                               : kWordValid;
+                                               : kHave;
                             };
-                            auto batch_valid = [&](const unsigned long long (&w)[kBatch]) {
+                            auto batch_ok = [&](const unsigned long long (&w)[kBatch]) {
                                 bool ok = true;
 #pragma unroll
-                                for (int u = 0; u < kBatch; ++u) ok = ok && word_valid(w[u]);
+                                for (int u = 0; u < kBatch; ++u) ok = ok && word_is(w[u], tag);
                                 return ok;
                             };
-                            auto clear_batch = [&](int k) {
-#pragma unroll
-                                for (int u = 0; u < kBatch; ++u)
-                                    if (k + u < n && ((prod >> (k + u)) & 1ull))
-                                        put_word(a.tag_out + (p0 + k + u) * kHeadDim + lane, 0ull);
-                            };
-                            unsigned long long wm = kWordValid, wl = kWordValid, w[kBatch];
-                            for (int r = 0;; ++r) {
+                            unsigned long long wm = kHave, wl = kHave, w[kBatch];
+                            for (int r = 0; !lost; ++r) {
+                                if (r >= a.merge_polls) { lost = true; break; }
                                 if (need) {
                                     wm = get_word(a.tag_ml + 2 * (p0 + lane));
                                     wl = get_word(a.tag_ml + 2 * (p0 + lane) + 1);
                                 }
                                 load_batch(1, w);
-                                if (__all(word_valid(wm) && word_valid(wl) && batch_valid(w))) break;
-                                if (r >= kMergePolls) { lost = true; break; }
-                            }
-                            // The words just read are not needed again: empty their slots for the next
-                            // call now, so that these stores complete while the merge runs.
-                            clear_batch(1);
-                            if (need) {
-                                put_word(a.tag_ml + 2 * (p0 + lane), 0ull);
-                                put_word(a.tag_ml + 2 * (p0 + lane) + 1, 0ull);
+                                if (__all(word_is(wm, tag) && word_is(wl, tag) && batch_ok(w))) break;
                             }
                             // Merge this wave's partial (segment 0) and the producers' partials, in
                             // segment order, with merge_partials' arithmetic.
@@ -1187,11 +1225,11 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                             for (int k = 1; k < n && !lost; k += kBatch) {
                                 if (k > 1) {
                                     for (int r = 0;; ++r) {
+                                        if (r >= a.merge_polls) { lost = true; break; }
                                         load_batch(k, w);
-                                        if (__all(batch_valid(w))) break;
-                                        if (r >= kMergePolls) { lost = true; break; }
+                                        if (__all(batch_ok(w))) break;
                                     }
-                                    clear_batch(k);
+                                    if (lost) break;
                                 }
 #pragma unroll
                                 for (int u = 0; u < kBatch; ++u)
@@ -1200,13 +1238,9 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                                                  word_value(w[u]), O);
                             }
                             store_out<DT>(a.out, (size_t)bh * kHeadDim + lane, lost ? __builtin_nanf("") : O / LL);
-                            if (lost) {
-                                // A merge that ran out of polls empties every slot of its head.
-                                for (unsigned long long clr = prod; clr; clr &= clr - 1) {
-                                    const int u = __ffsll((long long)clr) - 1;
-                                    put_word(a.tag_out + (p0 + u) * kHeadDim + lane, 0ull);
-                                }
-                            }
+                            if (lost && lane == 0)
+                                __hip_atomic_fetch_add(a.status + kWsStatusMergeTimeouts, 1u, __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT);
                         }
                     } else {
                         put<kCoh>(a.part_out + pidx * kHeadDim + lane, A);
@@ -1447,6 +1481,9 @@ __global__ __launch_bounds__(kWave) void set_len_kernel(int* __restrict__ p, int
 // ------------------------------------------------------------------------------------
 thread_local int t_last_hip_error = 0;
 
+// Bound on the designated merger's polls for launches from now on (kvattn_set_merge_poll_limit).
+std::atomic<int> g_merge_polls{kDefaultMergePolls};
+
 #define KV_HIP(expr)                                            \
     do {                                                        \
         hipError_t e_ = (expr);                                 \
@@ -1596,6 +1633,7 @@ int launch_split(const SplitArgs& a, int kv_dtype, int mode, bool lat, hipStream
         if (!fn) return KVATTN_ERR_DTYPE;
         grid = (grid + kStridedFactor - 1) / kStridedFactor;
     }
+    int spec = split_spec(args);
     void* params[] = SPLIT_PARAMS(args);
     KV_HIP(hipLaunchKernel(fn, dim3((unsigned)grid), dim3(threads), params, 0, stream));
     return KVATTN_OK;
@@ -1618,15 +1656,34 @@ int stream_capturing(hipStream_t stream, bool& capturing) {
     return KVATTN_OK;
 }
 
+// Workgroups of kernel `fn` (with `threads` threads) that the current device holds at once
+// (occupancy per CU x CUs), and whether the device launches cooperatively; queried once per
+// (device, kernel) and cached: the occupancy and attribute queries cost host time that an
+// eager call should not pay every time.
+int resident_capacity(const void* fn, int threads, long long& cap, bool* coop_out = nullptr) {
+    int dev = 0;
+    KV_HIP(hipGetDevice(&dev));
+    static std::mutex mu;
+    static std::map<std::tuple<int, const void*, int>, std::pair<long long, bool>> cache;
+    std::lock_guard<std::mutex> lock(mu);
+    const auto key = std::make_tuple(dev, fn, threads);
+    auto itc = cache.find(key);
+    if (itc == cache.end()) {
+        int cus = 0, coop = 0, per_cu = 0;
+        KV_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        KV_HIP(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev));
+        KV_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, 0));
+        itc = cache.emplace(key, std::make_pair((long long)per_cu * cus, coop != 0)).first;
+    }
+    cap = itc->second.first;
+    if (coop_out) *coop_out = itc->second.second;
+    return KVATTN_OK;
+}
+
 int launch_coop(const SplitArgs& a, int kv_dtype, bool lat, hipStream_t stream) {
     bool capturing = false;
     KV_TRY(stream_capturing(stream, capturing));
     if (capturing) return KVATTN_ERR_CAPTURE;
-    int dev = 0, cus = 0, coop = 0;
-    KV_HIP(hipGetDevice(&dev));
-    KV_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    KV_HIP(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev));
-    if (!coop) return KVATTN_ERR_COOP_TOO_LARGE;
     const long long blocks = (long long)a.B * a.NH * a.S;
     // Every workgroup must be resident at once: take the latency shape if the grid fits
     // with it, else the 4-wave shape, else refuse.
@@ -1636,10 +1693,13 @@ int launch_coop(const SplitArgs& a, int kv_dtype, bool lat, hipStream_t stream) 
         const void* fn = split_ptr_for(a, kv_dtype, kCoopMerge, use_lat);
         if (!fn) return KVATTN_ERR_DTYPE;
         const int threads = split_threads(use_lat);
-        int per_cu = 0;
-        KV_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, 0));
-        if (blocks > (long long)per_cu * cus) continue;
+        long long cap = 0;
+        bool coop = false;
+        KV_TRY(resident_capacity(fn, threads, cap, &coop));
+        if (!coop) return KVATTN_ERR_COOP_TOO_LARGE;
+        if (blocks > cap) continue;
         SplitArgs args = a;
+        int spec = split_spec(args);
         void* params[] = SPLIT_PARAMS(args);
         KV_HIP(hipLaunchCooperativeKernel(fn, dim3((unsigned)blocks), dim3(threads), params, 0, stream));
         return KVATTN_OK;
@@ -1648,16 +1708,18 @@ int launch_coop(const SplitArgs& a, int kv_dtype, bool lat, hipStream_t stream) 
 }
 
 // hipGraph holding the split and merge kernel nodes, built once per argument set.
+// Every kernel argument of the two nodes is part of the key (the length hint spec_rows
+// decides which rows the split kernel requests before it reads the device length).
 struct GraphKey {
     int dev, dt, lat;
-    const void *out, *qkv, *kv, *ks, *kv_out, *table, *len, *po, *pl, *pm;
-    int lens_per_seq, B, NH, maxT, S, seg_rows, max_pages, page_rows, num_pages;
+    const void *out, *qkv, *kv, *ks, *kv_out, *ks_out, *table, *len, *po, *pl, *pm;
+    int lens_per_seq, B, NH, maxT, S, seg_rows, spec_rows, max_pages, page_rows, num_pages;
     bool operator<(const GraphKey& o) const {
-        return std::tie(dev, dt, lat, out, qkv, kv, ks, kv_out, table, len, po, pl, pm, lens_per_seq, B, NH, maxT,
-                        S, seg_rows, max_pages, page_rows, num_pages) <
-               std::tie(o.dev, o.dt, o.lat, o.out, o.qkv, o.kv, o.ks, o.kv_out, o.table, o.len, o.po, o.pl, o.pm,
-                        o.lens_per_seq, o.B, o.NH, o.maxT, o.S, o.seg_rows, o.max_pages, o.page_rows,
-                        o.num_pages);
+        return std::tie(dev, dt, lat, out, qkv, kv, ks, kv_out, ks_out, table, len, po, pl, pm, lens_per_seq, B,
+                        NH, maxT, S, seg_rows, spec_rows, max_pages, page_rows, num_pages) <
+               std::tie(o.dev, o.dt, o.lat, o.out, o.qkv, o.kv, o.ks, o.kv_out, o.ks_out, o.table, o.len, o.po,
+                        o.pl, o.pm, o.lens_per_seq, o.B, o.NH, o.maxT, o.S, o.seg_rows, o.spec_rows,
+                        o.max_pages, o.page_rows, o.num_pages);
     }
 };
 
@@ -1671,10 +1733,10 @@ int launch_graph_pair(const SplitArgs& a, int kv_dtype, bool lat, hipStream_t st
     }
     int dev = 0;
     KV_HIP(hipGetDevice(&dev));
-    GraphKey key{dev,        kv_dtype,   lat ? 1 : 0, a.out,          a.qkv,      a.kv,
-                 a.kv_scale, a.kv_out,   a.table,     a.cur_len,      a.part_out, a.part_lse,
-                 a.part_max, a.lens_per_seq, a.B,     a.NH,           a.maxT,     a.S,
-                 a.seg_rows, a.max_pages, a.page_rows, a.num_pages};
+    GraphKey key{dev,        kv_dtype,   lat ? 1 : 0, a.out,      a.qkv,          a.kv,       a.kv_scale,
+                 a.kv_out,   a.kv_scale_out, a.table, a.cur_len,  a.part_out,     a.part_lse, a.part_max,
+                 a.lens_per_seq, a.B,    a.NH,        a.maxT,     a.S,            a.seg_rows, a.spec_rows,
+                 a.max_pages, a.page_rows, a.num_pages};
     static std::mutex mu;
     static std::map<GraphKey, hipGraphExec_t> cache;
     std::lock_guard<std::mutex> lock(mu);
@@ -1691,6 +1753,7 @@ int launch_graph_pair(const SplitArgs& a, int kv_dtype, bool lat, hipStream_t st
             return KVATTN_OK;
         });
         SplitArgs args = a;
+        int spec = split_spec(args);
         void* params[] = SPLIT_PARAMS(args);
         void* mparams[] = MERGE_PARAMS(args);
         hipGraph_t g = nullptr;
@@ -1726,15 +1789,18 @@ int launch_graph_pair(const SplitArgs& a, int kv_dtype, bool lat, hipStream_t st
 }
 
 // Workspace, every region 256-byte aligned:
+//   status [64] u32                           sticky status words (kWsStatus*)
 //   counters [B*NH] u32                       last-block merge
 //   part_max, part_lse [B*NH*S] f32, part_out [B*NH*S*64] f32   reference-format partials
 //   tag_ml [B*NH*S*2] u64, tag_out [B*NH*S*64] u64   designated merger
-// kvattn_workspace_init zeroes it once; every kernel leaves the counters and tags at 0.
+// kvattn_workspace_init zeroes it once; the last-block kernels leave the counters at 0, and
+// the designated merger's words carry the dispatch that wrote them, so they need no clearing.
 // The counters and partials are laid out from the front of the buffer and the tags from
 // its end, so that calls planned with different slot counts S on one buffer never put a
 // tag word where another call left a partial: a float pair read as a tagged word would
 // pass for a published partial.
 struct Workspace {
+    unsigned* status;
     unsigned* counters;
     float* part_max;
     float* part_lse;
@@ -1754,12 +1820,16 @@ Workspace carve(void* base, int B, int NH, int S, size_t avail = 0) {
     const size_t nto = align_up(bh * S * kHeadDim * sizeof(unsigned long long), 256);
     Workspace w;
     uint8_t* p = (uint8_t*)base;
+    w.status = (unsigned*)p;
+    p += kWsStatusBytes;
     w.counters = (unsigned*)p;
     w.part_max = (float*)(p + nc);
     w.part_lse = (float*)(p + nc + nm);
     w.part_out = (float*)(p + nc + 2 * nm);
-    w.bytes = nc + 2 * nm + no + ntm + nto;
-    const size_t end = avail >= w.bytes ? avail / 256 * 256 : w.bytes;   // w.bytes is a multiple of 256
+    w.bytes = kWsStatusBytes + nc + 2 * nm + no + ntm + nto;
+    avail = avail >= kWsStatusBytes ? avail - kWsStatusBytes : 0;
+    const size_t body = w.bytes - kWsStatusBytes;
+    const size_t end = avail >= body ? avail / 256 * 256 : body;   // body is a multiple of 256
     w.tag_out = (unsigned long long*)(p + end - nto);
     w.tag_ml = (unsigned long long*)(p + end - nto - ntm);
     return w;
@@ -1910,6 +1980,8 @@ int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scal
     a.counters = w.counters;
     a.tag_ml = w.tag_ml;
     a.tag_out = w.tag_out;
+    a.status = w.status;
+    a.merge_polls = g_merge_polls.load(std::memory_order_relaxed);
     a.qkv = qkv;
     a.kv = (const uint8_t*)kv;
     a.kv_scale = kv_scale;
@@ -1936,9 +2008,20 @@ int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scal
             KV_TRY(launch_split(a, kv_dtype, kPartialsOnly, plan.lat, stream));
             return launch_merge(a, kv_dtype, stream);
         case KVATTN_SPLIT_LASTBLOCK: return launch_split(a, kv_dtype, kLastBlockMerge, plan.lat, stream);
-        case KVATTN_SPLIT_DESIGNATED:
-            return launch_split(a, kv_dtype, plan.seg_rows == kDevicePlanDes && !pm ? kDesignatedDev : kDesignated,
-                                plan.lat, stream);
+        case KVATTN_SPLIT_DESIGNATED: {
+            const int mode = plan.seg_rows == kDevicePlanDes && !pm ? kDesignatedDev : kDesignated;
+            // The mergers wait for their producers, so the whole grid must fit on the GPU at once
+            // (AUTO plans at most kDesignatedMaxGrid workgroups, one per CU).
+            const long long grid = (long long)B * NH * plan.slots;
+            if (grid > kDesignatedMaxGrid) {
+                const void* fn = split_ptr_for(a, kv_dtype, mode, plan.lat);
+                if (!fn) return KVATTN_ERR_DTYPE;
+                long long cap = 0;
+                KV_TRY(resident_capacity(fn, split_threads(plan.lat), cap));
+                if (grid > cap) return KVATTN_ERR_GRID_TOO_LARGE;
+            }
+            return launch_split(a, kv_dtype, mode, plan.lat, stream);
+        }
         case KVATTN_SINGLE_LAUNCH_COOP: return launch_coop(a, kv_dtype, plan.lat, stream);
         case KVATTN_SINGLE_LAUNCH_GRAPH: return launch_graph_pair(a, kv_dtype, plan.lat, stream);
         default: return KVATTN_ERR_STRATEGY;
@@ -2035,6 +2118,8 @@ const char* kvattn_strerror(int status) {
         case KVATTN_ERR_CAPTURE: return "cooperative launch is not allowed inside stream capture";
         case KVATTN_ERR_LENGTH: return "length hint outside [-1, maxT-1]";
         case KVATTN_ERR_HIP: return "HIP runtime error";
+        case KVATTN_ERR_GRID_TOO_LARGE: return "designated-merger grid exceeds what the GPU holds at once";
+        case KVATTN_ERR_MERGE_TIMEOUT: return "a designated merge stopped waiting for its producers (output NaN)";
         default: return "unknown status";
     }
 }
@@ -2172,6 +2257,30 @@ int kvattn_workspace_init(void* workspace, size_t workspace_bytes, void* stream)
                        (uint32_t*)workspace, words);
     KV_HIP(hipGetLastError());
     return KVATTN_OK;
+}
+
+int kvattn_workspace_status(void* workspace, size_t workspace_bytes, int clear, void* stream_v,
+                            int* merge_timeouts) {
+    if (!workspace) return KVATTN_ERR_NULL_POINTER;
+    if (!aligned16(workspace)) return KVATTN_ERR_MISALIGNED;
+    if (workspace_bytes < kWsStatusBytes) return KVATTN_ERR_WORKSPACE;
+    hipStream_t stream = (hipStream_t)stream_v;
+    unsigned* st = (unsigned*)workspace;
+    unsigned n = 0;
+    KV_HIP(hipMemcpyAsync(&n, st + kWsStatusMergeTimeouts, sizeof(n), hipMemcpyDeviceToHost, stream));
+    KV_HIP(hipStreamSynchronize(stream));
+    if (clear && n != 0) {
+        hipLaunchKernelGGL(zero_words_kernel, dim3(1), dim3(kBlock), 0, stream, (uint32_t*)st,
+                           kWsStatusBytes / sizeof(uint32_t));
+        KV_HIP(hipGetLastError());
+        KV_HIP(hipStreamSynchronize(stream));
+    }
+    if (merge_timeouts) *merge_timeouts = (int)n;
+    return n ? KVATTN_ERR_MERGE_TIMEOUT : KVATTN_OK;
+}
+
+int kvattn_set_merge_poll_limit(int polls) {
+    return g_merge_polls.exchange(polls < 0 ? kDefaultMergePolls : polls);
 }
 
 int kvattn_plan(int B, int NH, int hs, int maxT, int len_hint, int S, int strategy, int kv_dtype,

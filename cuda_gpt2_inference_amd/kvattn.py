@@ -38,6 +38,8 @@ ERR_LDS = 10
 ERR_CAPTURE = 11
 ERR_LENGTH = 12
 ERR_HIP = 13
+ERR_GRID_TOO_LARGE = 14
+ERR_MERGE_TIMEOUT = 15
 
 # kvattn_dtype
 KV_F32 = 0
@@ -85,6 +87,8 @@ SIGNATURES = {
     "kvattn_merge": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "kvattn_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
     "kvattn_workspace_init": (_i, [_vp, _sz, _vp]),
+    "kvattn_workspace_status": (_i, [_vp, _sz, _i, _vp, ctypes.POINTER(_i)]),
+    "kvattn_set_merge_poll_limit": (_i, [_i]),
     "kvattn_plan": (_i, [_i, _i, _i, _i, _i, _i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i),
                          ctypes.POINTER(_i)]),
     "kvattn_decode": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp, _sz, _i, _i, _i, _vp]),
@@ -232,6 +236,24 @@ def workspace_init(workspace, nbytes, stream=None) -> None:
     _check(lib().kvattn_workspace_init(_ptr(workspace), nbytes, _stream(stream)), "kvattn_workspace_init")
 
 
+def workspace_status(workspace, nbytes, clear=False, stream=None) -> int:
+    """Designated merges that stopped waiting for their producers (and wrote NaN) since the
+    workspace was initialised or last cleared (kvattn_workspace_status; synchronises the
+    stream).  Returns the count; it is not an error to find one here."""
+    n = _i()
+    st = lib().kvattn_workspace_status(_ptr(workspace), int(nbytes), int(bool(clear)), _stream(stream),
+                                       ctypes.byref(n))
+    if st not in (OK, ERR_MERGE_TIMEOUT):
+        _check(st, "kvattn_workspace_status")
+    return n.value
+
+
+def set_merge_poll_limit(polls: int) -> int:
+    """Bound on the designated merger's polls for later launches (0: give up at once, a
+    fault-injection setting; < 0: the default).  Returns the previous bound."""
+    return int(lib().kvattn_set_merge_poll_limit(int(polls)))
+
+
 def plan(B, NH, hs, maxT, *, kv_dtype, len_hint=-1, S=0, strategy="auto"):
     """(strategy code, segment slots per (b,h), rows per segment) kvattn_decode would use."""
     st, seg, rows = _i(), _i(), _i()
@@ -341,3 +363,7 @@ class Workspace:
 
     def kwargs(self):
         return {"workspace": self.buf, "workspace_nbytes": self.nbytes}
+
+    def status(self, clear=False, stream=None) -> int:
+        """Designated merges on this workspace that stopped waiting (see workspace_status)."""
+        return workspace_status(self.buf, self.nbytes, clear=clear, stream=stream)

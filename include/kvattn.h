@@ -51,7 +51,11 @@ typedef enum kvattn_status {
     KVATTN_ERR_LDS = 10,            /* fused_single scores for maxT do not fit in LDS */
     KVATTN_ERR_CAPTURE = 11,        /* cooperative launch requested inside stream capture */
     KVATTN_ERR_LENGTH = 12,         /* host length hint outside [0, maxT-1] */
-    KVATTN_ERR_HIP = 13             /* a HIP runtime call failed; see kvattn_last_hip_error */
+    KVATTN_ERR_HIP = 13,            /* a HIP runtime call failed; see kvattn_last_hip_error */
+    KVATTN_ERR_GRID_TOO_LARGE = 14, /* explicit SPLIT_DESIGNATED grid exceeds what the GPU holds
+                                       at once (its mergers wait for their producers) */
+    KVATTN_ERR_MERGE_TIMEOUT = 15   /* kvattn_workspace_status: a designated merge stopped
+                                       waiting for its producers and wrote NaN */
 } kvattn_status;
 
 typedef enum kvattn_dtype {
@@ -159,10 +163,31 @@ int kvattn_merge(void* out, const float* part_out, const float* part_lse,
  * exactly S segments per (b,h); S == 0 sizes for every automatic choice. */
 size_t kvattn_workspace_bytes(int B, int NH, int hs, int maxT, int S);
 
-/* Zero the workspace's merge counters.  Call once after allocating a workspace and
- * before the first kvattn_decode on it; the kernels leave the counters at zero after
- * every call.  Enqueues one fill kernel (no hipMemsetAsync), so it may also be captured. */
+/* Zero the workspace (merge counters, status words).  Call once after allocating a
+ * workspace and before the first kvattn_decode on it; the kernels leave the counters at
+ * zero after every call, and the designated merger's partial words carry the dispatch that
+ * wrote them, so they never need clearing.  Enqueues one fill kernel (no hipMemsetAsync),
+ * so it may also be captured. */
 int kvattn_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
+
+/* The workspace's sticky status: waits for `stream`, then reads the number of designated
+ * merges (SPLIT_DESIGNATED, AUTO's latency-bound choice) that stopped waiting for their
+ * producers since the workspace was initialised or last cleared; each such merge wrote NaN
+ * for its (b,h).  *merge_timeouts (may be NULL) receives that number; clear != 0 resets it.
+ * Returns KVATTN_ERR_MERGE_TIMEOUT when it is non-zero, else KVATTN_OK.  Partials left by
+ * such a call are never taken for a later call's (each partial word carries the dispatch
+ * that wrote it), so the workspace stays usable without re-initialising.
+ * No reference counterpart: the reference has no in-kernel wait that can give up, and
+ * reports errors by exiting (common.h:123-130). */
+int kvattn_workspace_status(void* workspace, size_t workspace_bytes, int clear, void* stream,
+                            int* merge_timeouts);
+
+/* Bound on the designated merger's polls for its producers' partials, for launches (and
+ * captures) from this call on, process-wide: polls > 0 sets it, polls == 0 makes every
+ * merge of a multi-segment (b,h) give up at once (a fault-injection setting, for testing
+ * the reporting above), polls < 0 restores the default (2^22 polls, seconds).  Returns
+ * the previous bound.  No reference counterpart (testing and fault-injection hook). */
+int kvattn_set_merge_poll_limit(int polls);
 
 /* The launch plan kvattn_decode would use for these arguments, without launching:
  * *strategy_out = the resolved kvattn_strategy (AUTO resolved), *segments_out = segment

@@ -41,22 +41,22 @@ def test_symbols_are_c_linkage():
 def test_strerror_covers_every_status():
     kvattn = _kv()
     seen = set()
-    for st in range(0, 14):
+    for st in range(0, 16):
         msg = kvattn.strerror(st)
         assert msg and msg != "unknown status"
         seen.add(msg)
-    assert len(seen) == 14
+    assert len(seen) == 16
     assert kvattn.strerror(99) == "unknown status"
 
 
 def test_workspace_bytes():
     kvattn = _kv()
-    # counters (B*NH u32), part_max, part_lse (B*NH*S f32), part_out (B*NH*S*64 f32), the
-    # designated merger's tagged words (B*NH*S*2 and B*NH*S*64 u64), every region rounded up
-    # to 256 bytes.
+    # 256 bytes of status words, counters (B*NH u32), part_max, part_lse (B*NH*S f32),
+    # part_out (B*NH*S*64 f32), the designated merger's tagged words (B*NH*S*2 and
+    # B*NH*S*64 u64), every region rounded up to 256 bytes.
     def expect(B, NH, S):
         up = lambda x: (x + 255) // 256 * 256  # noqa: E731
-        return (up(B * NH * 4) + 2 * up(B * NH * S * 4) + up(B * NH * S * 64 * 4)
+        return (256 + up(B * NH * 4) + 2 * up(B * NH * S * 4) + up(B * NH * S * 64 * 4)
                 + up(B * NH * S * 2 * 8) + up(B * NH * S * 64 * 8))
     assert kvattn.workspace_bytes(1, 12, 64, 1024, 8) == expect(1, 12, 8)
     assert kvattn.workspace_bytes(64, 12, 64, 8192, 0) == expect(64, 12, 8192 // 64)
@@ -149,3 +149,22 @@ def test_paged_decode_argument_errors(kw, status):
         st = kvattn.lib().kvattn_paged_cache_write(ALIGNED, None, a["table"], a["max_pages"], a["page_rows"],
                                                    a["num_pages"], ALIGNED, 1, 12, 64, None, 0, 1, None)
         assert st == status, kvattn.strerror(st)
+
+
+def test_set_merge_poll_limit_round_trip():
+    """The designated merger's poll bound is host state only (no GPU call)."""
+    kvattn = _kv()
+    prev = kvattn.set_merge_poll_limit(5)
+    try:
+        assert kvattn.set_merge_poll_limit(-1) == 5
+        assert kvattn.set_merge_poll_limit(-1) == 1 << 22
+    finally:
+        kvattn.set_merge_poll_limit(prev)
+
+
+def test_workspace_status_rejects_bad_arguments():
+    kvattn = _kv()
+    n = ctypes.c_int(-1)
+    assert kvattn.lib().kvattn_workspace_status(None, 4096, 0, None, ctypes.byref(n)) == kvattn.ERR_NULL_POINTER
+    assert kvattn.lib().kvattn_workspace_status(ALIGNED + 4, 4096, 0, None, ctypes.byref(n)) == kvattn.ERR_MISALIGNED
+    assert kvattn.lib().kvattn_workspace_status(ALIGNED, 100, 0, None, ctypes.byref(n)) == kvattn.ERR_WORKSPACE

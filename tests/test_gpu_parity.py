@@ -293,7 +293,9 @@ def test_c5_ragged_64_sequences(dev):
     """64 sequences x NH=12, BF16, maxT=8192, lengths ~ U[1,8192] from a seed (~1.6 GB
     cache).  Inputs come from torch's seeded generator on the device; 24 (b,h) slots are
     copied back and checked against the oracle; every slot is checked for the
-    size-independent bound min_j V <= out <= max_j V and all strategies must agree."""
+    size-independent bound min_j V <= out <= max_j V and all strategies must agree.  The
+    designated merger's grid for this shape (32 slots per head) exceeds what the GPU holds
+    at once, so an explicit designated plan is refused."""
     import torch
     kvattn = _kv()
     B, NH, maxT = 64, 12, 8192
@@ -304,9 +306,14 @@ def test_c5_ragged_64_sequences(dev):
     cache = torch.randn(2 * B * NH * maxT * HS, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
     qkv = torch.randn(B * 3 * NH * HS, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
     outs = {}
-    for strategy in ("auto", "split_merge", "lastblock", "designated"):
+    ws = kvattn.Workspace(B, NH, maxT, 0)
+    out = torch.empty(B * NH * HS, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(kvattn.KvAttnError) as err:
+        kvattn.decode(out, qkv, cache, B, NH, HS, maxT, kv_dtype="bf16", cur_len=cur, lens_per_seq=True,
+                      strategy="designated", **ws.kwargs())
+    assert err.value.status == kvattn.ERR_GRID_TOO_LARGE
+    for strategy in ("auto", "split_merge", "lastblock"):
         out = torch.empty(B * NH * HS, dtype=torch.bfloat16, device=dev)
-        ws = kvattn.Workspace(B, NH, maxT, 0)
         kvattn.decode(out, qkv, cache, B, NH, HS, maxT, kv_dtype="bf16", cur_len=cur, lens_per_seq=True,
                       strategy=strategy, **ws.kwargs())
         torch.cuda.synchronize()
@@ -391,7 +398,8 @@ def test_streaming_ragged_every_dtype(dev, dtype):
 def test_workspace_shared_by_plans_of_different_slot_counts(dev):
     """One workspace, sized for the largest plan, serves calls whose plans differ in slot
     count: AUTO's split + merge (8 slots), the last-block merge with 16 and 4 slots, the
-    designated merger with 64 slots, and AUTO again.  Each output against split + merge on a
+    designated merger with 4 slots of 1024 rows (a grid the GPU holds at once), and AUTO
+    again.  Each output against split + merge on a
     workspace of its own.  The partials of one plan must never land where another plan keeps
     its tagged words (a float pair can read as a published partial)."""
     import torch
@@ -401,7 +409,7 @@ def test_workspace_shared_by_plans_of_different_slot_counts(dev):
     lens = rng.randint(1, maxT + 1, B).astype(np.int32)
     case = make_case("bf16", B, NH, maxT, lens - 1, seed=431)
     qkv, cache, _, cur = to_device(case, dev)
-    nbytes = max(kvattn.workspace_bytes(B, NH, HS, maxT, S) for S in (0, 16, 4, -64))
+    nbytes = max(kvattn.workspace_bytes(B, NH, HS, maxT, S) for S in (0, 16, 4, -1024))
     buf = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
     kw = dict(workspace=buf, workspace_nbytes=nbytes)
     ref = out_tensor(case, dev)
@@ -411,8 +419,8 @@ def test_workspace_shared_by_plans_of_different_slot_counts(dev):
     torch.cuda.synchronize()
     ref_h = ref.float().cpu().numpy()
     assert_close(ref_h, case.reference(), "bf16", "split + merge")
-    for i, (strategy, S) in enumerate([("auto", 0), ("lastblock", 16), ("designated", -64), ("lastblock", 4),
-                                       ("designated", -64), ("auto", 0), ("auto", 0)]):
+    for i, (strategy, S) in enumerate([("auto", 0), ("lastblock", 16), ("designated", -1024), ("lastblock", 4),
+                                       ("designated", -1024), ("auto", 0), ("auto", 0)]):
         out = out_tensor(case, dev)
         kvattn.decode(out, qkv, cache, B, NH, HS, maxT, kv_dtype="bf16", cur_len=cur, lens_per_seq=True, S=S,
                       strategy=strategy, **kw)
@@ -519,9 +527,9 @@ def test_graph_capture_replay_tracks_device_length(dev):
 
 
 def test_designated_merger_workspace_reuse(dev):
-    """The designated merger leaves its tagged slots empty after every call: one workspace
+    """The designated merger's slots carry the dispatch that wrote them: one workspace
     serves calls that alternate strategy, segment count and inputs, each checked against
-    the oracle (a stale slot would hand a later call an old partial)."""
+    the oracle (a stale slot taken for fresh would hand a later call an old partial)."""
     import torch
     kvattn = _kv()
     B, NH, maxT = 2, 3, 700
@@ -540,21 +548,33 @@ def test_designated_merger_workspace_reuse(dev):
 
 
 def test_designated_merger_grid_beyond_residency(dev):
-    """12,288 workgroups, far more than the GPU holds at once: segment 0 of each (b,h) waits
-    for segments dispatched after it, which relies on in-order dispatch of workgroups.
-    Repeated calls, every output finite, a subset of sequences against the oracle."""
+    """An explicit designated plan whose grid exceeds what the GPU holds at once (12,288
+    workgroups) is refused: its mergers wait for producers that would have to be dispatched
+    behind them.  Halving the batch until the grid fits, the accepted call runs repeatedly
+    with every output finite and a subset of sequences against the oracle."""
     import torch
     kvattn = _kv()
-    B, NH, maxT = 64, 12, 1024
-    lens = np.full(B, maxT, np.int32)
-    lens[::5] = np.arange(1, B + 1, 5, dtype=np.int32) * 15
-    case = make_case("bf16", B, NH, maxT, lens - 1, seed=97)
-    qkv, cache, _, cur = to_device(case, dev)
-    out = out_tensor(case, dev)
-    S = -64
-    assert kvattn.plan(B, NH, HS, maxT, kv_dtype="bf16", S=S, strategy="designated") == \
+    NH, maxT, S = 12, 1024, -64
+    big = 64
+    lens_big = np.full(big, maxT, np.int32)
+    lens_big[::5] = np.arange(1, big + 1, 5, dtype=np.int32) * 15
+    assert kvattn.plan(big, NH, HS, maxT, kv_dtype="bf16", S=S, strategy="designated") == \
         (kvattn.SPLIT_DESIGNATED, 16, 64)
-    ws = kvattn.Workspace(B, NH, maxT, S)
+    B = big
+    while True:
+        case = make_case("bf16", B, NH, maxT, lens_big[:B] - 1, seed=97)
+        qkv, cache, _, cur = to_device(case, dev)
+        out = out_tensor(case, dev)
+        ws = kvattn.Workspace(B, NH, maxT, S)
+        try:
+            kvattn.decode(out, qkv, cache, B, NH, HS, maxT, kv_dtype="bf16", cur_len=cur, lens_per_seq=True, S=S,
+                          strategy="designated", **ws.kwargs())
+            break
+        except kvattn.KvAttnError as e:
+            assert e.status == kvattn.ERR_GRID_TOO_LARGE, str(e)
+            assert B > 1, "a 16-workgroup designated grid was refused"
+            B //= 2
+    assert B < big, "a 12,288-workgroup designated grid was accepted"
     for _ in range(3):
         out.fill_(float("nan"))
         kvattn.decode(out, qkv, cache, B, NH, HS, maxT, kv_dtype="bf16", cur_len=cur, lens_per_seq=True, S=S,
@@ -562,11 +582,12 @@ def test_designated_merger_grid_beyond_residency(dev):
         torch.cuda.synchronize()
         got = out.float().cpu().numpy().reshape(B, NH, HS)
         assert np.isfinite(got).all()
-    sub = [0, 1, 5, 10, 63]
+    assert ws.status() == 0
+    sub = [i for i in (0, 1, 5, 10, 63) if i < B]
     q = np.ascontiguousarray(case.qkv_host.reshape(B, 3, NH, HS)[sub]).reshape(-1)
     c = np.ascontiguousarray(case.cache_host.reshape(2, B, NH, maxT, HS)[:, sub]).reshape(-1)
-    ref = oracle.attention_f32(q, c, lens[sub], len(sub), NH, HS, maxT)
-    assert_close(got[sub].reshape(-1), ref, "bf16", "designated, grid beyond residency")
+    ref = oracle.attention_f32(q, c, case.totals[sub], len(sub), NH, HS, maxT)
+    assert_close(got[sub].reshape(-1), ref, "bf16", f"designated, largest accepted grid (B={B})")
 
 
 def test_workspace_init_zeroes_eager_and_in_graph(dev):

@@ -1,0 +1,180 @@
+"""Robustness of the HIP decode attention on an MI355X (runs on the GPU box).
+
+* Cache rows at and past a sequence's length hold garbage, as in the reference engine,
+  which allocates its cache with cudaMalloc and never clears it
+  (inference_gpt2_opt.cu:692-699): NaN and Inf bits (f32 / bf16), FP8 NaN codes 0x7F/0xFF
+  and NaN / Inf row scales (8-bit).  Kernels that request rows before they know the length
+  (a stale host hint, the device-planned first tile) must not let them into the result.
+* The designated merger's bounded wait: a merge that gives up (forced from the host with a
+  poll bound of 0, so every kernel still exits normally) writes NaN, is counted in the
+  workspace's status, and the partials its producers publish afterwards are never taken
+  for a later call's.
+
+Bars as in kvcases.TOL (FP32 1e-5, BF16 1e-2, 8-bit 2e-2 against the oracle on the
+dequantised cache).
+"""
+import numpy as np
+import pytest
+
+from kvcases import FMT, HS, assert_close, make_case, out_tensor, to_device
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+ALL_DT = ["f32", "bf16", "int8", "fp8"]
+
+
+def _kv():
+    from cuda_gpt2_inference_amd import kvattn
+    return kvattn
+
+
+def poison_past_length(case):
+    """Overwrite every cache row at or beyond each sequence's attended length, in place:
+    even rows NaN, odd rows +Inf (K) / -Inf (V); 8-bit caches get FP8 NaN codes and NaN /
+    Inf row scales.  The oracle never reads those rows."""
+    B, NH, maxT = case.B, case.NH, case.maxT
+    raw = case.cache_raw.reshape(2, B, NH, maxT, HS)
+    sc = None if case.scale_raw is None else case.scale_raw.reshape(2, B, NH, maxT)
+    for b, t in enumerate(case.totals):
+        rows = np.arange(t, maxT)
+        even, odd = rows[rows % 2 == 0], rows[rows % 2 == 1]
+        if case.dtype == "f32":
+            raw[:, b, :, even, :] = np.nan
+            raw[0, b, :, odd, :] = np.inf
+            raw[1, b, :, odd, :] = -np.inf
+        elif case.dtype == "bf16":
+            raw[:, b, :, even, :] = 0x7FC0
+            raw[0, b, :, odd, :] = 0x7F80
+            raw[1, b, :, odd, :] = 0xFF80
+        else:
+            raw[:, b, :, even, :] = 0x7F
+            raw[:, b, :, odd, :] = 0xFF
+            sc[:, b, :, even] = np.nan
+            sc[:, b, :, odd] = np.inf
+    return case
+
+
+def _uniform(dtype, NH, maxT, total, seed):
+    return poison_past_length(make_case(dtype, 1, NH, maxT, [total - 1], seed=seed))
+
+
+def _decode(case, dev, strategy, len_hint, S=0, append=False):
+    """One call with a single device length for the batch (lens_per_seq = 0), so that the
+    host's hint may steer the first requests."""
+    import torch
+    kvattn = _kv()
+    qkv, cache, scale, _ = to_device(case, dev)
+    cur = torch.tensor([int(case.cur_lens[0])], dtype=torch.int32, device=dev)
+    out = out_tensor(case, dev)
+    ws = kvattn.Workspace(case.B, case.NH, case.maxT, S)
+    fn = kvattn.append_decode if append else kvattn.decode
+    fn(out, qkv, cache, case.B, case.NH, HS, case.maxT, kv_dtype=case.dtype, kv_scale=scale, cur_len=cur,
+       len_hint=len_hint, S=S, strategy=strategy, **ws.kwargs())
+    torch.cuda.synchronize()
+    assert ws.status() == 0
+    return out.float().cpu().numpy(), cache, scale
+
+
+@pytest.mark.parametrize("dtype", ALL_DT)
+def test_fused_single_stale_hint_ignores_rows_past_length(dev, dtype):
+    """fused_single requests its one tile per wave for the hinted 256 positions before it
+    reads the device length (100 or 201 positions)."""
+    for total in (100, 201):
+        case = _uniform(dtype, 12, 256, total, seed=300 + total)
+        got, _, _ = _decode(case, dev, "fused_single", len_hint=255)
+        assert_close(got, case.reference(), dtype, f"fused_single stale hint T={total}")
+
+
+@pytest.mark.parametrize("dtype", ALL_DT)
+def test_device_planned_designated_ignores_rows_past_length(dev, dtype):
+    """AUTO without a hint plans on the device; the designated instance requests its
+    nominal first tile (segment 0: up to 256 rows) before the length: T below and above 256."""
+    kvattn = _kv()
+    assert kvattn.plan(1, 12, HS, 1024, kv_dtype=dtype, len_hint=-1)[0] == kvattn.SPLIT_DESIGNATED
+    for total in (70, 200, 300, 700):
+        case = _uniform(dtype, 12, 1024, total, seed=320 + total)
+        got, _, _ = _decode(case, dev, "auto", len_hint=-1)
+        assert_close(got, case.reference(), dtype, f"device-planned designated T={total}")
+
+
+@pytest.mark.parametrize("dtype", ALL_DT)
+@pytest.mark.parametrize("strategy", ["designated", "lastblock", "split_merge", "graph", "coop"])
+def test_hinted_split_ignores_rows_past_length(dev, dtype, strategy):
+    """A host hint of 1024 positions (segments of fixed rows, first tiles requested before
+    the length) while the device length is 600 or 130."""
+    for total in (600, 130):
+        case = _uniform(dtype, 12, 1024, total, seed=340 + total)
+        got, _, _ = _decode(case, dev, strategy, len_hint=1023)
+        assert_close(got, case.reference(), dtype, f"{strategy} hint 1024, T={total}")
+
+
+@pytest.mark.parametrize("dtype", ALL_DT)
+def test_append_decode_ignores_rows_past_length(dev, dtype):
+    """Append and attend in one launch over a poisoned cache: the fresh row replaces the
+    garbage at position cur_len, every row after it stays out of the result."""
+    for strategy, len_hint, total, maxT in (("auto", -1, 500, 1024), ("auto", 1023, 500, 1024),
+                                            ("fused_single", 255, 150, 256)):
+        case = _uniform(dtype, 12, maxT, total, seed=360 + total)
+        got, cache, scale = _decode(case, dev, strategy, len_hint=len_hint, append=True)
+        # The reference: the oracle's append into the host copy, then attention over it.
+        B, NH = case.B, case.NH
+        if dtype in ("int8", "fp8"):
+            codes, scales = case.cache_raw.copy(), case.scale_raw.copy()
+            oracle.cache_write_w8(codes, scales, case.qkv_host, case.cur_lens, B, NH, HS, maxT, FMT[dtype])
+            assert np.array_equal(cache.cpu().numpy(), codes)
+            assert np.array_equal(scale.cpu().numpy().view(np.uint32), scales.view(np.uint32))
+            host = oracle.dequant_w8(codes, scales, B, NH, HS, maxT, FMT[dtype])
+        elif dtype == "bf16":
+            import torch
+            bits = case.cache_raw.copy()
+            oracle.cache_write(bits, case.qkv_raw, case.cur_lens, B, NH, HS, maxT)
+            assert np.array_equal(cache.view(torch.int16).cpu().numpy().view(np.uint16), bits)
+            host = oracle.bf16_decode(bits)
+        else:
+            host = case.cache_raw.copy()
+            oracle.cache_write(host, case.qkv_raw, case.cur_lens, B, NH, HS, maxT)
+            assert np.array_equal(cache.cpu().numpy().view(np.uint32), host.view(np.uint32))
+        ref = oracle.attention_f32(case.qkv_host, host, case.totals, B, NH, HS, maxT)
+        assert_close(got, ref, dtype, f"append_decode {strategy} hint {len_hint} T={total}")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp8"])
+def test_designated_give_up_is_reported_and_workspace_stays_usable(dev, dtype):
+    """Poll bound 0: every multi-segment merge gives up at once (NaN output, counted in the
+    workspace status) while its producers publish afterwards.  The next call on the same
+    workspace, with different q, K and V, must not take those late partials for its own
+    and matches the oracle; the count stays until cleared."""
+    import torch
+    kvattn = _kv()
+    B, NH, maxT, total = 1, 12, 1024, 1024
+    first = make_case(dtype, B, NH, maxT, [total - 1], seed=401)
+    second = make_case(dtype, B, NH, maxT, [total - 1], seed=402)
+    ws = kvattn.Workspace(B, NH, maxT, 8)
+    assert ws.status() == 0
+    for strategy, S in (("designated", 8), ("auto", 0)):
+        # Call 1 gives up; call 2 (defaults restored) must ignore call 1's late partials.
+        qkv, cache, scale, cur = to_device(first, dev)
+        out = out_tensor(first, dev)
+        prev = kvattn.set_merge_poll_limit(0)
+        try:
+            kvattn.decode(out, qkv, cache, B, NH, HS, maxT, kv_dtype=dtype, kv_scale=scale, cur_len=cur,
+                          len_hint=total - 1, S=S, strategy=strategy, **ws.kwargs())
+            torch.cuda.synchronize()
+        finally:
+            kvattn.set_merge_poll_limit(prev)
+        got = out.float().cpu().numpy().reshape(B * NH, HS)
+        assert np.isnan(got).all(), f"{strategy}: a merge that gave up wrote a number"
+        assert ws.status() == B * NH
+        qkv2, cache2, scale2, cur2 = to_device(second, dev)
+        out2 = out_tensor(second, dev)
+        for rep in range(3):
+            kvattn.decode(out2, qkv2, cache2, B, NH, HS, maxT, kv_dtype=dtype, kv_scale=scale2, cur_len=cur2,
+                          len_hint=total - 1, S=S, strategy=strategy, **ws.kwargs())
+            torch.cuda.synchronize()
+            assert_close(out2.float().cpu().numpy(), second.reference(), dtype,
+                         f"{strategy}: call {rep + 1} after the give-up")
+        assert ws.status() == B * NH, "the give-up count is sticky until cleared"
+        assert ws.status(clear=True) == B * NH
+        assert ws.status() == 0
+
