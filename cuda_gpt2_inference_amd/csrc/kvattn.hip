@@ -27,7 +27,6 @@
 // Workgroup size and tile depth are template parameters (the "latency" and "streaming"
 // shapes picked per call by the host plan; both are 4 waves in this build).
 #include <hip/hip_runtime.h>
-#include <hip/hip_cooperative_groups.h>
 
 #include <float.h>
 #include <stdint.h>
@@ -67,7 +66,8 @@ constexpr int kMaxT = 1 << 23;          // keeps per-slot byte offsets inside 32
 constexpr size_t kFusedMaxLds = 64 * 1024;  // dynamic LDS of fused_single (scores)
 constexpr int kMaxDesignatedSegments = 64;  // the designated merger follows one segment per lane
 // Workspace status words (the first 256 bytes of a kvattn_decode workspace).
-constexpr int kWsStatusMergeTimeouts = 0;   // designated merges that stopped waiting (a sticky count)
+constexpr int kWsStatusMergeTimeouts = 0;   // merges that stopped waiting (a sticky count)
+constexpr int kWsStatusBarrier = 2;         // u64 {generation, count} of the cooperative grid barrier
 constexpr size_t kWsStatusBytes = 256;
 
 // ------------------------------------------------------------------------------------
@@ -791,8 +791,10 @@ struct SplitArgs {
                     // kDevicePlan: planned_rows(total) of the device length
     int spec_rows;  // the host's view of the attended length (0: unknown); see split_kernel
     float qscale;   // scale * log2(e)
-    // Designated merger: workspace status words (see kWsStatus*) and the poll bound.
+    // Designated merger and cooperative barrier: workspace status words (see kWsStatus*), the
+    // cooperative launch's barrier word {generation, count}, and the bound on their waits.
     unsigned* status;
+    unsigned long long* barrier;
     int merge_polls;
 };
 
@@ -1077,7 +1079,7 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                        const int spec_end) {
         const int bh = it.b * a.NH + it.h;
         const size_t pidx = (size_t)bh * a.S + it.s;
-        constexpr bool kCoh = kMode == kLastBlockMerge;
+        constexpr bool kCoh = kMode == kLastBlockMerge || kMode == kCoopMerge;
         constexpr bool kDes = kMode == kDesignated || kDev;
 
         // Rows [sj0, sj1) of segment s of this (b,h).
@@ -1158,7 +1160,7 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                         L = fmaf(g, s_l[w], L);
                         A = fmaf(g, s_acc[w][lane], A);
                     }
-                    if ((kMode == kLastBlockMerge || kDes) && it.n_seg == 1) {
+                    if ((kMode == kLastBlockMerge || kMode == kCoopMerge || kDes) && it.n_seg == 1) {
                         // The only segment of its (b,h): the result needs no merge.
                         store_out<DT>(a.out, (size_t)bh * kHeadDim + lane, A / L);
                     } else if constexpr (kDes) {
@@ -1270,9 +1272,40 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                 }
             }
         } else if constexpr (kMode == kCoopMerge) {
-            cooperative_groups::this_grid().sync();
-            if (active && it.s == 0 && wave == 0)
-                merge_partials<DT, false>(a.out, a.part_out, a.part_lse, a.part_max, a.S, it.n_seg, bh, lane);
+            // Grid barrier, for the mergers only.  Wave 0 of every workgroup (with a segment or
+            // not) waits until its coherent partial stores are acknowledged and arrives on the
+            // barrier word {generation, count}; the last of the gridDim.x arrivals re-arms it
+            // as {generation + 1, 0}.  Segment 0 of each (b,h) waits for the generation to move
+            // on, then merges; every other wave has nothing left to do and finishes.  The
+            // cooperative launch keeps the whole grid resident, so the wait ends (bounded by
+            // a.merge_polls like the designated merger's).
+            if (wave == 0) {
+                wait_vm_stores();
+                unsigned long long prev = 0;
+                if (lane == 0) prev = __hip_atomic_fetch_add(a.barrier, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const uint32_t gen = (uint32_t)__builtin_amdgcn_readfirstlane((int)(prev >> 32));
+                const uint32_t cnt = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)prev);
+                const bool last = cnt == gridDim.x - 1;
+                if (last && lane == 0)
+                    __hip_atomic_store(a.barrier, (unsigned long long)(gen + 1u) << 32, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                if (active && it.s == 0 && it.n_seg > 1) {
+                    bool lost = false;
+                    for (int r = 0; !last; ++r) {
+                        if (r >= a.merge_polls) { lost = true; break; }
+                        if ((uint32_t)(get_word(a.barrier) >> 32) != gen) break;
+                        __builtin_amdgcn_s_sleep(1);
+                    }
+                    if (lost) {
+                        store_out<DT>(a.out, (size_t)bh * kHeadDim + lane, __builtin_nanf(""));
+                        if (lane == 0)
+                            __hip_atomic_fetch_add(a.status + kWsStatusMergeTimeouts, 1u, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+                    } else {
+                        merge_partials<DT, true>(a.out, a.part_out, a.part_lse, a.part_max, a.S, it.n_seg, bh, lane);
+                    }
+                }
+            }
         }
     };
 
@@ -1981,6 +2014,7 @@ int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scal
     a.tag_ml = w.tag_ml;
     a.tag_out = w.tag_out;
     a.status = w.status;
+    a.barrier = reinterpret_cast<unsigned long long*>(w.status + kWsStatusBarrier);
     a.merge_polls = g_merge_polls.load(std::memory_order_relaxed);
     a.qkv = qkv;
     a.kv = (const uint8_t*)kv;
@@ -2026,6 +2060,34 @@ int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scal
         case KVATTN_SINGLE_LAUNCH_GRAPH: return launch_graph_pair(a, kv_dtype, plan.lat, stream);
         default: return KVATTN_ERR_STRATEGY;
     }
+}
+
+// A workspace the library owns for kvattn_forward_large's single launch, one per (device,
+// stream) so that calls on different streams never share one; allocated (and zeroed on the
+// stream) at the first call that needs it, grown when a later call needs more, and kept
+// until the process ends.  Calls on one stream are ordered, so they may share theirs.
+int stream_workspace(hipStream_t stream, size_t need, void*& base) {
+    int dev = 0;
+    KV_HIP(hipGetDevice(&dev));
+    static std::mutex mu;
+    static std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> owned;
+    std::lock_guard<std::mutex> lock(mu);
+    auto& w = owned[std::make_pair(dev, stream)];
+    if (w.second < need) {
+        if (w.first) {
+            KV_HIP(hipStreamSynchronize(stream));
+            KV_HIP(hipFree(w.first));
+            w = {nullptr, 0};
+        }
+        KV_HIP(hipMalloc(&w.first, need));
+        w.second = need;
+        const size_t words = need / 4;
+        hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)std::min<size_t>((words + kBlock - 1) / kBlock, 4096)),
+                           dim3(kBlock), 0, stream, (uint32_t*)w.first, words);
+        KV_HIP(hipGetLastError());
+    }
+    base = w.first;
+    return KVATTN_OK;
 }
 
 SplitArgs caller_partials(void* out, const void* qkv, const void* kv, const float* kv_scale, int B, int NH,
@@ -2202,15 +2264,34 @@ int kvattn_forward_large(void* out, const void* qkv, const void* kv_cache, const
     KV_TRY(check_partials(part_out, part_lse, part_max, S));
     KV_TRY(resolve_len(d_cur_len));
     hipStream_t stream = (hipStream_t)stream_v;
-    const SplitArgs a = caller_partials(out, qkv, kv_cache, kv_scale, B, NH, maxT, d_cur_len, lens_per_seq,
-                                        part_out, part_lse, part_max, S);
+    SplitArgs a = caller_partials(out, qkv, kv_cache, kv_scale, B, NH, maxT, d_cur_len, lens_per_seq, part_out,
+                                  part_lse, part_max, S);
+    const bool lat = latency_bound(B, NH, maxT);
     bool capturing = false;
     KV_TRY(stream_capturing(stream, capturing));
-    if (B == 1 && !capturing) {
-        const int st = launch_coop(a, kv_dtype, latency_bound(B, NH, maxT), stream);
-        if (st != KVATTN_ERR_COOP_TOO_LARGE) return st;
+    if (B == 1 && !capturing && S <= kMaxDesignatedSegments) {
+        // The reference saves the merge launch for B == 1 with a cooperative launch.  On this
+        // stack a cooperative dispatch costs ~20 us of GPU time even for an empty kernel
+        // (2.4 us for an ordinary one), so the single launch here is the designated merger,
+        // over the reference partition, with a workspace the library keeps per stream.
+        const void* fn = split_ptr_for(a, kv_dtype, kDesignated, lat);
+        long long cap = 0;
+        if (!fn) return KVATTN_ERR_DTYPE;
+        KV_TRY(resident_capacity(fn, split_threads(lat), cap));
+        if ((long long)B * NH * S <= cap) {
+            const size_t need = carve(nullptr, B, NH, S).bytes;
+            void* base = nullptr;
+            KV_TRY(stream_workspace(stream, need, base));
+            const Workspace w = carve(base, B, NH, S, need);
+            a.tag_ml = w.tag_ml;
+            a.tag_out = w.tag_out;
+            a.status = w.status;
+            a.barrier = reinterpret_cast<unsigned long long*>(w.status + kWsStatusBarrier);
+            a.merge_polls = g_merge_polls.load(std::memory_order_relaxed);
+            return launch_split(a, kv_dtype, kDesignated, lat, stream);
+        }
     }
-    KV_TRY(launch_split(a, kv_dtype, kPartialsOnly, latency_bound(B, NH, maxT), stream));
+    KV_TRY(launch_split(a, kv_dtype, kPartialsOnly, lat, stream));
     return launch_merge(a, kv_dtype, stream);
 }
 

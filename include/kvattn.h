@@ -130,7 +130,12 @@ int kvattn_forward_small(void* out, const void* qkv, const void* kv_cache,
                          int kv_dtype, void* stream);
 
 /* Long-context path with caller-owned partials of S segments per (b,h).  As in the
- * reference, B == 1 uses the cooperative single launch and B > 1 the split + merge pair.
+ * reference, B == 1 takes a single launch and B > 1 (or a capture) the split + merge pair
+ * over the caller's partials.  The single launch is the designated merger (SPLIT_DESIGNATED
+ * over the reference partition), not a cooperative launch: on this stack a cooperative
+ * dispatch alone costs ~20 us of GPU time.  Its tagged partials live in a workspace the
+ * library allocates per (device, stream) at the first such call and keeps; S > 64, or a grid
+ * the GPU cannot hold at once, takes the split + merge pair instead.
  * Replaces attention_forward_kv_large (Inference_gpt2/attention_kvcache.cuh:464-487) and
  * attention_forward_kv_large_w8 (Inference_gpt2/attention_kvcache_w8.cuh:541-566). */
 int kvattn_forward_large(void* out, const void* qkv, const void* kv_cache,

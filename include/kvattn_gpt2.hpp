@@ -77,7 +77,8 @@ inline void attention_forward_kv_small_w8(void* out, const void* qkv, uint8_t* k
 }
 
 // attention_forward_kv_large (Inference_gpt2/attention_kvcache.cuh:464-487): B == 1 ->
-// cooperative single launch, B > 1 -> split + merge, caller-owned partials of S segments.
+// single launch (the designated merger; the reference launches cooperatively), B > 1 ->
+// split + merge, caller-owned partials of S segments.
 inline void attention_forward_kv_large(void* out, const void* qkv, void* kv_cache, int B, int NH, int hs,
                                        int maxT, hipStream_t stream, float* part_out, float* part_lse,
                                        float* part_max, int S, int kv_dtype = KVATTN_KV_BF16,

@@ -178,3 +178,36 @@ def test_designated_give_up_is_reported_and_workspace_stays_usable(dev, dtype):
         assert ws.status(clear=True) == B * NH
         assert ws.status() == 0
 
+
+
+def test_cooperative_barrier_give_up_is_reported(dev):
+    """The cooperative strategy's grid barrier is bounded like the designated merger's wait:
+    with a poll bound of 0 every merger that is not the last to arrive gives up (NaN,
+    counted); with the bound restored the next calls on the same workspace, with other
+    inputs and another segment count, match the oracle."""
+    import torch
+    kvattn = _kv()
+    B, NH, maxT, total = 1, 12, 1024, 1024
+    first = make_case("bf16", B, NH, maxT, [total - 1], seed=411)
+    second = make_case("bf16", B, NH, maxT, [total - 1], seed=412)
+    ws = kvattn.Workspace(B, NH, maxT, 16)
+    qkv, cache, _, cur = to_device(first, dev)
+    out = out_tensor(first, dev)
+    prev = kvattn.set_merge_poll_limit(0)
+    try:
+        kvattn.decode(out, qkv, cache, B, NH, HS, maxT, kv_dtype="bf16", cur_len=cur, len_hint=total - 1, S=8,
+                      strategy="coop", **ws.kwargs())
+        torch.cuda.synchronize()
+    finally:
+        kvattn.set_merge_poll_limit(prev)
+    got = out.float().cpu().numpy().reshape(B * NH, HS)
+    gave_up = int(np.isnan(got).all(axis=1).sum())
+    assert gave_up >= B * NH - 1 and ws.status(clear=True) == gave_up
+    qkv2, cache2, _, cur2 = to_device(second, dev)
+    for S in (8, 16, 5):
+        out2 = out_tensor(second, dev)
+        kvattn.decode(out2, qkv2, cache2, B, NH, HS, maxT, kv_dtype="bf16", cur_len=cur2, len_hint=total - 1, S=S,
+                      strategy="coop", **ws.kwargs())
+        torch.cuda.synchronize()
+        assert_close(out2.float().cpu().numpy(), second.reference(), "bf16", f"coop S={S} after the give-up")
+    assert ws.status() == 0
