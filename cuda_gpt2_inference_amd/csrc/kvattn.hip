@@ -1843,28 +1843,40 @@ struct Workspace {
     size_t bytes;
 };
 
+// Bytes of each region for B*NH heads of S slots, every one rounded up to 256.
+struct RegionSizes {
+    size_t nc, nm, no, ntm, nto;
+    size_t body() const { return 2 * nm + no + ntm + nto; }   // partials and tagged words
+};
+RegionSizes region_sizes(int B, int NH, int S) {
+    const size_t bh = (size_t)B * NH;
+    return {align_up(bh * sizeof(unsigned), 256), align_up(bh * S * sizeof(float), 256),
+            align_up(bh * S * kHeadDim * sizeof(float), 256),
+            align_up(bh * S * 2 * sizeof(unsigned long long), 256),
+            align_up(bh * S * kHeadDim * sizeof(unsigned long long), 256)};
+}
+
+// The partials from `body` on and the tagged words at the end of the `avail` bytes there
+// (avail below what they need: right after the partials).
+void carve_body(Workspace& w, uint8_t* body, const RegionSizes& z, size_t avail) {
+    w.part_max = (float*)body;
+    w.part_lse = (float*)(body + z.nm);
+    w.part_out = (float*)(body + 2 * z.nm);
+    const size_t end = avail >= z.body() ? avail / 256 * 256 : z.body();   // z.body() is a multiple of 256
+    w.tag_out = (unsigned long long*)(body + end - z.nto);
+    w.tag_ml = (unsigned long long*)(body + end - z.nto - z.ntm);
+}
+
 // avail: the caller's buffer size (0: the size query, the buffer exactly as large).
 Workspace carve(void* base, int B, int NH, int S, size_t avail = 0) {
-    const size_t bh = (size_t)B * NH;
-    const size_t nc = align_up(bh * sizeof(unsigned), 256);
-    const size_t nm = align_up(bh * S * sizeof(float), 256);
-    const size_t no = align_up(bh * S * kHeadDim * sizeof(float), 256);
-    const size_t ntm = align_up(bh * S * 2 * sizeof(unsigned long long), 256);
-    const size_t nto = align_up(bh * S * kHeadDim * sizeof(unsigned long long), 256);
+    const RegionSizes z = region_sizes(B, NH, S);
     Workspace w;
     uint8_t* p = (uint8_t*)base;
     w.status = (unsigned*)p;
-    p += kWsStatusBytes;
-    w.counters = (unsigned*)p;
-    w.part_max = (float*)(p + nc);
-    w.part_lse = (float*)(p + nc + nm);
-    w.part_out = (float*)(p + nc + 2 * nm);
-    w.bytes = kWsStatusBytes + nc + 2 * nm + no + ntm + nto;
-    avail = avail >= kWsStatusBytes ? avail - kWsStatusBytes : 0;
-    const size_t body = w.bytes - kWsStatusBytes;
-    const size_t end = avail >= body ? avail / 256 * 256 : body;   // body is a multiple of 256
-    w.tag_out = (unsigned long long*)(p + end - nto);
-    w.tag_ml = (unsigned long long*)(p + end - nto - ntm);
+    w.counters = (unsigned*)(p + kWsStatusBytes);
+    w.bytes = kWsStatusBytes + z.nc + z.body();
+    const size_t head = kWsStatusBytes + z.nc;
+    carve_body(w, p + head, z, avail >= head ? avail - head : 0);
     return w;
 }
 
@@ -1980,10 +1992,14 @@ int make_plan(int B, int NH, int maxT, int len_hint, int S, int strategy, Plan& 
 
 // append == true: the launch also writes the current token's K/V row (kvattn_append_decode).
 // pm != nullptr: kv / kv_scale are page pools addressed through pm's block table.
+// use_scratch: the workspace is the library's static device array (kvattn_decode_static).
+int scratch_base(hipStream_t stream, uint8_t*& base);
+bool carve_scratch(uint8_t* base, int B, int NH, int S, Workspace& w);
+
 int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scale, int B, int NH, int hs,
                 int maxT, const int* d_cur_len, int lens_per_seq, int len_hint, void* workspace,
                 size_t workspace_bytes, int S, int strategy, int kv_dtype, void* stream_v, bool append,
-                const CacheMap* pm = nullptr) {
+                const CacheMap* pm = nullptr, bool use_scratch = false) {
     KV_TRY(check_common(qkv, kv, kv_scale, B, NH, hs, maxT, kv_dtype));
     if (!out) return KVATTN_ERR_NULL_POINTER;
     if (!aligned16(out)) return KVATTN_ERR_MISALIGNED;
@@ -1999,10 +2015,21 @@ int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scal
                                    stream);
     }
 
-    if (!workspace) return KVATTN_ERR_WORKSPACE;
-    if (!aligned16(workspace)) return KVATTN_ERR_MISALIGNED;
-    const Workspace w = carve(workspace, B, NH, plan.slots, workspace_bytes);
-    if (w.bytes > workspace_bytes) return KVATTN_ERR_WORKSPACE;
+    Workspace w{};
+    if (use_scratch) {
+        // The cooperative launch and the library's own graph pair are not offered here: the
+        // runtime may allocate device memory for them.
+        if (plan.strategy == KVATTN_SINGLE_LAUNCH_COOP || plan.strategy == KVATTN_SINGLE_LAUNCH_GRAPH)
+            return KVATTN_ERR_STRATEGY;
+        uint8_t* base = nullptr;
+        KV_TRY(scratch_base(stream, base));
+        if (!carve_scratch(base, B, NH, plan.slots, w)) return KVATTN_ERR_WORKSPACE;
+    } else {
+        if (!workspace) return KVATTN_ERR_WORKSPACE;
+        if (!aligned16(workspace)) return KVATTN_ERR_MISALIGNED;
+        w = carve(workspace, B, NH, plan.slots, workspace_bytes);
+        if (w.bytes > workspace_bytes) return KVATTN_ERR_WORKSPACE;
+    }
     KV_TRY(resolve_len(d_cur_len));
 
     SplitArgs a{};
@@ -2088,6 +2115,55 @@ int stream_workspace(hipStream_t stream, size_t need, void*& base) {
     }
     base = w.first;
     return KVATTN_OK;
+}
+
+// ------------------------------------------------------------------------------------
+// kvattn_decode_static: the workspace in a static device array.
+// ------------------------------------------------------------------------------------
+// Layout: the status words, a fixed region of merge counters for up to kScratchMaxHeads
+// (b,h) (so that calls of different B*NH never find another plan's partials where their
+// counters sit; the last-block kernels leave the counters at zero after every call), then
+// the partials and tagged words of the current plan (carved as in a caller's workspace).
+constexpr size_t kScratchBytes = 8u << 20;
+constexpr int kScratchMaxHeads = 16384;
+constexpr size_t kScratchCounterBytes = kScratchMaxHeads * sizeof(unsigned);
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+// Device address of this device's `scratch`, found once per device with hipGetSymbolAddress
+// (the host-side name of the array is a stand-in, not a device address); on that first call
+// its status words and counters are cleared with a fill kernel on `stream`.
+int scratch_base(hipStream_t stream, uint8_t*& base) {
+    int dev = 0;
+    KV_HIP(hipGetDevice(&dev));
+    static std::mutex mu;
+    static std::map<int, uint8_t*> bases;
+    std::lock_guard<std::mutex> lock(mu);
+    auto itb = bases.find(dev);
+    if (itb == bases.end()) {
+        uint8_t* ptr = nullptr;
+        KV_HIP(hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch)));
+        if (!ptr) return KVATTN_ERR_HIP;
+        const size_t words = (kWsStatusBytes + kScratchCounterBytes) / sizeof(uint32_t);
+        hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((words + kBlock - 1) / kBlock)), dim3(kBlock), 0,
+                           stream, (uint32_t*)ptr, words);
+        KV_HIP(hipGetLastError());
+        itb = bases.emplace(dev, ptr).first;
+    }
+    base = itb->second;
+    return KVATTN_OK;
+}
+
+// The plan's workspace regions inside the scratch array; false when they do not fit.
+bool carve_scratch(uint8_t* base, int B, int NH, int S, Workspace& w) {
+    if ((long long)B * NH > kScratchMaxHeads) return false;
+    const RegionSizes z = region_sizes(B, NH, S);
+    const size_t head = kWsStatusBytes + kScratchCounterBytes;
+    if (z.body() > kScratchBytes - head) return false;
+    w.status = (unsigned*)base;
+    w.counters = (unsigned*)(base + kWsStatusBytes);
+    w.bytes = head + z.body();
+    carve_body(w, base + head, z, kScratchBytes - head);
+    return true;
 }
 
 SplitArgs caller_partials(void* out, const void* qkv, const void* kv, const float* kv_scale, int B, int NH,
@@ -2383,6 +2459,13 @@ int kvattn_decode(void* out, const void* qkv, const void* kv_cache, const float*
                   size_t workspace_bytes, int S, int strategy, int kv_dtype, void* stream) {
     return decode_impl(out, qkv, kv_cache, kv_scale, B, NH, hs, maxT, d_cur_len, lens_per_seq, len_hint,
                        workspace, workspace_bytes, S, strategy, kv_dtype, stream, false);
+}
+
+int kvattn_decode_static(void* out, const void* qkv, const void* kv_cache, const float* kv_scale, int B, int NH,
+                         int hs, int maxT, const int* d_cur_len, int lens_per_seq, int len_hint, int S, int strategy,
+                         int kv_dtype, void* stream) {
+    return decode_impl(out, qkv, kv_cache, kv_scale, B, NH, hs, maxT, d_cur_len, lens_per_seq, len_hint, nullptr, 0,
+                       S, strategy, kv_dtype, stream, false, nullptr, true);
 }
 
 int kvattn_append_decode(void* out, const void* qkv, void* kv_cache, float* kv_scale, int B, int NH, int hs,

@@ -93,6 +93,7 @@ SIGNATURES = {
                          ctypes.POINTER(_i)]),
     "kvattn_decode": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp, _sz, _i, _i, _i, _vp]),
     "kvattn_append_decode": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp, _sz, _i, _i, _i, _vp]),
+    "kvattn_decode_static": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _i, _i, _i, _i, _vp]),
     "kvattn_gemv": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "kvattn_gemv_qkv_append": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _i, _vp, _i, _i, _i, _vp,
                                     _sz, _vp]),
@@ -274,6 +275,16 @@ def decode(out, qkv, kv_cache, B, NH, hs, maxT, *, kv_dtype, kv_scale=None, cur_
                                _ptr(cur_len), int(bool(lens_per_seq)), int(len_hint), _ptr(workspace),
                                int(workspace_nbytes), int(S), strategy_code(strategy),
                                kv_dtype_code(kv_dtype), _stream(stream)), "kvattn_decode")
+
+
+def decode_static(out, qkv, kv_cache, B, NH, hs, maxT, *, kv_dtype, kv_scale=None, cur_len=None,
+                  lens_per_seq=False, len_hint=-1, S=0, strategy="auto", stream=None) -> None:
+    """decode with the library's static device scratch as workspace (kvattn_decode_static):
+    allocates nothing; calls that overlap in time on one GPU race."""
+    _check(lib().kvattn_decode_static(_ptr(out), _ptr(qkv), _ptr(kv_cache), _ptr(kv_scale), B, NH, hs, maxT,
+                                      _ptr(cur_len), int(bool(lens_per_seq)), int(len_hint), int(S),
+                                      strategy_code(strategy), kv_dtype_code(kv_dtype), _stream(stream)),
+           "kvattn_decode_static")
 
 
 def append_decode(out, qkv, kv_cache, B, NH, hs, maxT, *, kv_dtype, kv_scale=None, cur_len=None,

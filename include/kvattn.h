@@ -230,6 +230,24 @@ int kvattn_decode(void* out, const void* qkv, const void* kv_cache, const float*
                   void* workspace, size_t workspace_bytes,
                   int S, int strategy, int kv_dtype, void* stream);
 
+/* kvattn_decode without a workspace argument: the partials, merge counters and tagged words
+ * live in `scratch`, a static device array of 8 MiB that the library holds on each GPU it
+ * runs on until the process ends, so the call allocates nothing (no hipMalloc, no hipFree;
+ * a fill kernel clears the array's counters on its first call on a device).
+ * No reference counterpart: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Limits: B*NH <= 16384, and the plan's partials and tagged words (kvattn_workspace_bytes
+ * less its status words and counters) within 8 MiB - 64.25 KiB, else KVATTN_ERR_WORKSPACE;
+ * strategies AUTO, FUSED_SINGLE, SPLIT_MERGE, SPLIT_LASTBLOCK, SPLIT_DESIGNATED (the
+ * cooperative launch and the library's graph pair return KVATTN_ERR_STRATEGY: the runtime may
+ * allocate for them).  Every call on one GPU shares that GPU's array, which keeps the last
+ * call's contents: calls that overlap in time on one GPU (unordered streams, concurrent host
+ * threads) race; calls ordered on one stream do not. */
+int kvattn_decode_static(void* out, const void* qkv, const void* kv_cache, const float* kv_scale,
+                         int B, int NH, int hs, int maxT,
+                         const int* d_cur_len, int lens_per_seq, int len_hint,
+                         int S, int strategy, int kv_dtype, void* stream);
+
 /* kvattn_cache_write followed by kvattn_decode with the same arguments, in one launch
  * (two for SPLIT_MERGE): the current token's K and V rows are taken from qkv in registers
  * (8-bit: quantised exactly as kvattn_cache_write does), written into column cur_len, and
