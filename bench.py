@@ -85,9 +85,10 @@ def bytes_per_call(lengths, NH, kv_bytes, act_bytes, B):
 @contextlib.contextmanager
 def phase(name: str):
     """Marks a timed region in the source.  Regions are attributed in profiles by running one
-    workload per rocprofv3 process (--only), not by marker ranges: every --marker-trace run
-    on this stack ended in a segmentation fault in exit-time handlers after the profiler's
-    own finalisation, while plain --kernel-trace runs exit cleanly."""
+    workload per rocprofv3 process (--only), not by marker ranges.  (A rocprofv3 run of a
+    process that made a cooperative launch ends in a segmentation fault in exit-time
+    handlers after the profiler's own finalisation, with or without marker ranges, its
+    result files complete; runs without a cooperative launch exit cleanly.)"""
     yield
 
 
@@ -562,10 +563,34 @@ def small_config(torch, kvattn, dev, dtype, NH, maxT, T, strategy, S, reps=200, 
     return res
 
 
-def other_configs(torch, kvattn, dev, cpu_seconds=2.0):
+COOP_ROWS = (("c4_fp8_T512_coop_S8", 512), ("c4_fp8_T1024_coop_S8", 1024))
+
+
+def coop_configs(torch, kvattn, dev, cpu_seconds=2.0):
+    """C4's cooperative single launch (FP8, S = 8, T = 512 and 1024), measured before the
+    process captures any graph.  On this stack, when a process makes its first cooperative
+    launch after it has captured three or more HIP graphs (freed or not), every cooperative
+    dispatch of that process costs about four times as much: ~96 us per call instead of
+    ~24 us, the kernel itself running ~29 us instead of ~6 us.  A first cooperative launch
+    made earlier keeps them at ~24 us, later captures notwithstanding.  The reference engine
+    makes its cooperative launches in eager runs, which capture no graph, so these rows are
+    measured first; other_configs() times the same call again late in the run
+    (`us_per_call_eager_after_graph_captures`)."""
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    res = {name: small_config(torch, kvattn, dev, "fp8", 12, 1024, T, "coop", 8, reps=50, flush=flush,
+                              cpu_seconds=cpu_seconds)
+           for name, T in COOP_ROWS}
+    del flush
+    return res
+
+
+def other_configs(torch, kvattn, dev, cpu_seconds=2.0, coop=None):
     """The remaining GPT-2-shaped configurations, single layer: warm cache (graph replay),
     cold cache (single eager calls after a 512 MiB flush), and the CPU attention on the same
-    inputs for the first entry of each configuration."""
+    inputs for the first entry of each configuration.  `coop`: the cooperative rows as
+    coop_configs() measured them before any graph capture (measured here first if None)."""
+    if coop is None:
+        coop = coop_configs(torch, kvattn, dev, cpu_seconds)
     flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
     cfg = lambda *a, **k: small_config(torch, kvattn, dev, *a, flush=flush, **k)  # noqa: E731
     cs = cpu_seconds
@@ -576,9 +601,9 @@ def other_configs(torch, kvattn, dev, cpu_seconds=2.0):
         "c3_int8_T1024_lastblock_S8": cfg("int8", 12, 1024, 1024, "lastblock", 8, outliers=0.01),
         "c3_int8_T1024_designated_S8": cfg("int8", 12, 1024, 1024, "designated", 8, outliers=0.01),
         "c3_int8_T1024_auto": cfg("int8", 12, 1024, 1024, "auto", 0, outliers=0.01),
-        "c4_fp8_T512_coop_S8": cfg("fp8", 12, 1024, 512, "coop", 8, reps=50, cpu_seconds=cs),
+        "c4_fp8_T512_coop_S8": dict(coop["c4_fp8_T512_coop_S8"]),
         "c4_fp8_T512_graph_S8": cfg("fp8", 12, 1024, 512, "graph", 8),
-        "c4_fp8_T1024_coop_S8": cfg("fp8", 12, 1024, 1024, "coop", 8, reps=50, cpu_seconds=cs),
+        "c4_fp8_T1024_coop_S8": dict(coop["c4_fp8_T1024_coop_S8"]),
         "c4_fp8_T1024_graph_S8": cfg("fp8", 12, 1024, 1024, "graph", 8),
         "c4_fp8_T1024_forward_large_S8": cfg("fp8", 12, 1024, 1024, "forward_large", 8),
         "c4_fp8_T1024_lastblock_S8": cfg("fp8", 12, 1024, 1024, "lastblock", 8),
@@ -586,6 +611,9 @@ def other_configs(torch, kvattn, dev, cpu_seconds=2.0):
         "c4_fp8_T1024_designated_S8": cfg("fp8", 12, 1024, 1024, "designated", 8),
         "c4_fp8_T1024_auto": cfg("fp8", 12, 1024, 1024, "auto", 0),
     }
+    for name, T in COOP_ROWS:
+        late = small_config(torch, kvattn, dev, "fp8", 12, 1024, T, "coop", 8, reps=50)
+        res[name]["us_per_call_eager_after_graph_captures"] = late["us_per_call_eager"]
     del flush
     return res
 
@@ -961,6 +989,9 @@ def main():
         print(json.dumps({"only": args.only, "result": part, "gpu": torch.cuda.get_device_name(dev)}))
         return
 
+    # The cooperative rows first: graph captures earlier in the process slow every later
+    # cooperative dispatch (coop_configs).
+    coop = None if args.no_configs else coop_configs(torch, kvattn, dev, cpu_seconds=cpu_s)
     c2 = C2(args, torch, kvattn, dev)
     graph_ms, eager_ms = c2.measure()
     rel = c2.check()
@@ -987,7 +1018,7 @@ def main():
         c5["paged"]["kernel"], c5["paged"]["traffic_bytes_split_kernel"] = lookup(
             traffic, kernel_key(kvattn.plan(C5Paged.B, C5Paged.NH, HD, C5Paged.maxT, kv_dtype="bf16"), C5Paged.B,
                                 C5Paged.NH, C5Paged.maxT, paged=True, ragged=True))
-    configs = None if args.no_configs else other_configs(torch, kvattn, dev, cpu_seconds=cpu_s)
+    configs = None if args.no_configs else other_configs(torch, kvattn, dev, cpu_seconds=cpu_s, coop=coop)
     gemv = None if args.no_configs else gemv_configs(torch, kvattn, dev)
     qkv_append = None if args.no_configs else qkv_append_configs(torch, kvattn, dev)
     gemv_cpu = None if (args.no_configs or args.no_cpu) else gemv_cpu_baseline()

@@ -341,22 +341,22 @@ struct Tile {
     float ks[U], vs[U];
 };
 
+// kChecked (a wave's first and last tile, which may reach past the rows it owns): every row
+// slot is loaded unconditionally, rows at or beyond r1 clamped to r1 - 1 (r1 is at most the
+// slot's maxT, and at least 1), so no load sits behind a branch and all of them issue back
+// to back.  Those rows hold another row's data: consume_tile<kChecked>, and fused_single's
+// one-tile path, mask them by selection (score -inf, V chunk and V scale zero).
 template <int DT, int U, bool kChecked>
 __device__ __forceinline__ void load_tile(Tile<DT, U>& t, const Slot& sl, int r, int r1, int slot_row) {
     using R = Row<DT>;
     constexpr int kRPL = kRowsPerLoad<DT>;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const int row = r + u * kRPL + slot_row;
-        if (!kChecked || row < r1) {
-            t.k[u] = load16(sl.k + (uint32_t)row * R::kBytes);
-            t.v[u] = load16(sl.v + (uint32_t)row * R::kBytes);
-            if constexpr (R::k8bit) { t.ks[u] = sl.ks[row]; t.vs[u] = sl.vs[row]; }
-        } else {
-            t.k[u] = make_uint4(0u, 0u, 0u, 0u);
-            t.v[u] = make_uint4(0u, 0u, 0u, 0u);
-            if constexpr (R::k8bit) { t.ks[u] = 0.0f; t.vs[u] = 0.0f; }
-        }
+        int row = r + u * kRPL + slot_row;
+        if (kChecked) row = max(min(row, r1 - 1), 0);
+        t.k[u] = load16(sl.k + (uint32_t)row * R::kBytes);
+        t.v[u] = load16(sl.v + (uint32_t)row * R::kBytes);
+        if constexpr (R::k8bit) { t.ks[u] = sl.ks[row]; t.vs[u] = sl.vs[row]; }
     }
 }
 
