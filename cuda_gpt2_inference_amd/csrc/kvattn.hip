@@ -800,10 +800,12 @@ struct SplitArgs {
 
 // Kernel parameter arrays of split_kernel and merge_kernel (their leading scalars, then the
 // struct), for launches through hipLaunchKernel, cooperative launches and graph nodes.
-// split_spec(x) is the packed length hint pk_spec of split_kernel; SPLIT_PARAMS needs an
-// int lvalue `spec` holding it.
+// split_spec(x) is the packed length hint pk_spec of split_kernel and split_pks(x, mode) its
+// packed slot count pk_S (bit 30: the designated grid's XCD-local layout); SPLIT_PARAMS needs
+// int lvalues `spec` and `pks` holding them.
+constexpr int kXcdLocalBit = 1 << 30;
 inline int split_spec(const SplitArgs& a) { return a.lens_per_seq ? -1 : (a.spec_rows > 0 ? a.spec_rows : 0); }
-#define SPLIT_PARAMS(x) {&(x).kv, &(x).qkv, &(x).cur_len, &(x).B, &(x).NH, &(x).maxT, &(x).S, &(x).seg_rows, \
+#define SPLIT_PARAMS(x) {&(x).kv, &(x).qkv, &(x).cur_len, &(x).B, &(x).NH, &(x).maxT, &pks, &(x).seg_rows, \
                          &spec, &(x)}
 #define MERGE_PARAMS(x) {&(x).part_max, &(x).part_lse, &(x).part_out, &(x).cur_len, &(x).B, &(x).NH, &(x).maxT, \
                          &(x).S, &(x).seg_rows, &(x).lens_per_seq, &(x)}
@@ -862,9 +864,11 @@ __device__ __forceinline__ int seg_count(int seg_rows, int total, int heads, int
 // Map a workgroup index to (b, h, segment).  Uniform lengths (or the reference
 // partition) use the dense grid B*NH*S; ragged lengths with fixed-size segments pack
 // the real segments of all sequences at the front of the grid using a prefix sum over
-// the per-sequence segment counts, computed redundantly by every wave.
-__device__ __forceinline__ bool locate(const SplitArgs& a, int x, Item& it) {
-    if (!a.lens_per_seq || a.seg_rows == 0) {
+// the per-sequence segment counts, computed redundantly by every wave.  `dense`: the dense
+// grid whatever the lengths (designated grids, whose slot order places every segment of a
+// head on one XCD; slots beyond a head's segment count exit).
+__device__ __forceinline__ bool locate(const SplitArgs& a, int x, Item& it, bool dense) {
+    if (dense || !a.lens_per_seq || a.seg_rows == 0) {
         const int bh = x / a.S;
         it.s = x - bh * a.S;
         it.b = bh / a.NH;
@@ -926,17 +930,30 @@ __device__ __forceinline__ float get(const float* p) {
     else return *p;
 }
 
-// Tagged partial words of the designated merger (agent-scope relaxed atomics, emitted as
-// coherent sc1 stores and loads on gfx950): the value in the low half, the call's tag in the
-// high half.  The tag is the launch's dispatch id (one per kernel dispatch, increasing along
-// the queue; every replay of a captured graph dispatches anew) with the top bit set, so a
-// word counts only for the dispatch that wrote it: words left by an earlier call (a merge
-// that stopped waiting, or a plan with other slots on the same workspace) are never taken
-// for this call's, the slots need no clearing, and a zeroed workspace holds no valid word.
-constexpr int kDefaultMergePolls = 1 << 22;  // bound on the designated merger's polls (seconds)
+// Tagged partial words of the designated merger: the value in the low half, the call's tag
+// in the high half.  The tag is the launch's dispatch id (one per kernel dispatch,
+// increasing along the queue; every replay of a captured graph dispatches anew) with the top
+// bit set, so a word counts only for the dispatch that wrote it: words left by an earlier
+// call (a plan with other slots on the same workspace, producers that finished after their
+// merger stopped waiting) are never taken for this call's, the slots need no clearing, and
+// a zeroed workspace holds no valid word.
+//
+// Where the words travel.  The host lays a designated grid out so that every segment of a
+// head runs on one XCD (xcd_slot below).  Producers publish with plain stores, which land in
+// their XCD's L2 and stay there (write-back); the merger polls with agent-scope loads (sc1),
+// which miss the CU's L1 and hit a line of the XCD's L2 that holds written data.  Measured
+// on MI355X (two workgroups handing a flag back and forth, 200 rounds): 460 ns per round
+// trip on one XCD, against 925 ns with write-through (sc1) stores, which an agent-scope load
+// then has to fetch from memory; across XCDs a plain store is never seen, which the merger's
+// bounded wait and fallback cover (split_kernel).  Each slot's words sit in lines of their
+// own (tag_ml: kMlStride words per slot), so a line the merger polls is written by one
+// producer only.
+constexpr int kDefaultMergePolls = 1 << 16;  // the designated merger's polls before it computes missing segments
+constexpr int kMlStride = 16;                // u64 words per slot in tag_ml: {max, exp-sum}, one 128-byte line
 __device__ __forceinline__ uint32_t call_tag() { return (uint32_t)kvattn_dispatch_id() | 0x80000000u; }
-__device__ __forceinline__ void put_word(unsigned long long* p, unsigned long long w) {
-    __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void publish_word(unsigned long long* p, unsigned long long w, bool xcd_local) {
+    if (xcd_local) *p = w;
+    else __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ unsigned long long get_word(const unsigned long long* p) {
     return __hip_atomic_load(const_cast<unsigned long long*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -947,6 +964,25 @@ __device__ __forceinline__ unsigned long long tagged_word(float v, uint32_t tag)
 __device__ __forceinline__ bool word_is(unsigned long long w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
 __device__ __forceinline__ float word_value(unsigned long long w) { return __uint_as_float((uint32_t)w); }
 
+// XCD placement of a designated grid.  The hardware hands consecutive workgroups of a
+// dispatch to the XCDs in turn (workgroup x to XCD (x + c) % 8, c fixed per dispatch), so
+// workgroups x and x + 8 share an XCD.  Workgroup x works on slot xcd_slot(x, S) of the
+// (b,h)-major slot order: segment s of head 8k + r is workgroup 8 (S k + s) + r.  The grid
+// is 8 * ceil(B*NH / 8) * S workgroups; those of heads beyond B*NH exit at once.
+__host__ __device__ __forceinline__ int xcd_slot(int x, int S) {
+    const int r = x & 7, j = x >> 3;
+    const int k = j / S, s = j - k * S;
+    return ((k << 3) + r) * S + s;
+}
+// The layout is used from kXcdLocalHeads heads on: with fewer, whole XCDs would sit idle
+// while the ones holding a head stream all of its bytes; those grids keep the dense slot
+// order, and their producers publish with write-through (sc1) stores, which an agent-scope
+// load sees from any XCD.
+constexpr int kXcdLocalHeads = 8;
+__host__ __device__ __forceinline__ bool xcd_local_layout(int B, int NH) { return B * NH >= kXcdLocalHeads; }
+__host__ __device__ __forceinline__ long long designated_grid(int B, int NH, int S) {
+    return xcd_local_layout(B, NH) ? 8ll * ((B * NH + 7) / 8) * S : (long long)B * NH * S;
+}
 
 // Merge the n_seg partials of (b,h) = bh into out; executed by one full wave, lane c
 // producing channel c.  Lane s holds the max and exp-sum of segment s (64 segments per
@@ -1009,7 +1045,7 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
     a.B = pk_B;
     a.NH = pk_NH;
     a.maxT = pk_maxT;
-    a.S = pk_S;
+    a.S = pk_S & (kXcdLocalBit - 1);
     a.seg_rows = pk_seg_rows;
     a.lens_per_seq = pk_spec < 0 ? 1 : 0;
     a.spec_rows = pk_spec < 0 ? 0 : pk_spec;
@@ -1021,6 +1057,10 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
 
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int slot_row = lane / R::kLanes, slice = lane % R::kLanes;
+    // Designated grids of the XCD-local layout: the slot this workgroup works on (every segment
+    // of a head on one XCD).
+    const bool xl = (kMode == kDesignated || kMode == kDesignatedDev) && (pk_S & kXcdLocalBit) != 0;
+    const int vbx = xl ? xcd_slot(blockIdx.x, a.S) : (int)blockIdx.x;
 
     // Uniform lengths with fixed-size segments: (b, h, s) and the segment's nominal rows
     // [j0, min(j0 + seg_rows, maxT)) follow from blockIdx alone, and the nominal range
@@ -1046,14 +1086,14 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
     int g_w0 = 0, g_w1 = 0, g_j0 = 0, g_end = 0;
     if (!kPaged && kMode != kPartialsStrided && !a.lens_per_seq && (kDev || a.seg_rows > 0)) {
         const int nom = kDev ? designated_base_rows(a.B * a.NH) : a.seg_rows;
-        const int bh0 = blockIdx.x / a.S;
-        const int j0 = (blockIdx.x - bh0 * a.S) * nom;
+        const int bh0 = vbx / a.S;   // beyond B * NH only in a designated grid padded to whole XCD rounds
+        const int j0 = (vbx - bh0 * a.S) * nom;
         const bool first = kDev && j0 == 0 && nom < kFusedMaxRows;
         const int nend = min(j0 + (first ? kFusedMaxRows : nom), a.maxT);
         // 8-bit caches guess only in segment 0's early share: measured, the producers' early
         // tiles cost 8-bit calls more than the length's round trip they hide.
         const bool allowed = !(R::k8bit && kDev && !first);
-        if (allowed && (kDev || j0 < a.spec_rows) && j0 < nend) {
+        if (allowed && bh0 < a.B * a.NH && (kDev || j0 < a.spec_rows) && j0 < nend) {
             const int per = ceil_div_i(nend - j0, kW);
             g_w0 = min(j0 + wave * per, nend);
             g_w1 = min(g_w0 + per, nend);
@@ -1167,20 +1207,21 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                         const uint32_t tag = call_tag();
                         if (it.s != 0) {
                             // Producer: publish the tagged partial and finish; nothing waits.
-                            put_word(a.tag_out + pidx * kHeadDim + lane, tagged_word(A, tag));
+                            publish_word(a.tag_out + pidx * kHeadDim + lane, tagged_word(A, tag), xl);
                             if (lane == 0) {
-                                put_word(a.tag_ml + 2 * pidx, tagged_word(Mb * kLn2, tag));
-                                put_word(a.tag_ml + 2 * pidx + 1, tagged_word(L, tag));
+                                publish_word(a.tag_ml + kMlStride * pidx, tagged_word(Mb * kLn2, tag), xl);
+                                publish_word(a.tag_ml + kMlStride * pidx + 1, tagged_word(L, tag), xl);
                             }
                         } else {
                             // Designated merger (segment 0): lane u follows segment u.  A head's
-                            // segments have consecutive workgroup ids with segment 0 first, and
-                            // workgroups are dispatched in id order, so the producers waited for are
-                            // already resident or next in line behind workgroups that do not wait:
-                            // the polls end.  The host also keeps every designated grid within what
-                            // the GPU holds at once.  The bound (a.merge_polls rounds) only guards
-                            // against that order failing; a merge that reaches it writes NaN and
-                            // counts itself in the workspace's status words for the host to read.
+                            // segments have consecutive slots with segment 0 first, all on this
+                            // XCD, and workgroups are dispatched in id order, so the producers
+                            // waited for are resident or next in line behind workgroups that do
+                            // not wait, and their words land in this XCD's L2.  The wait is bounded
+                            // all the same (a.merge_polls rounds): a merger that reaches the bound
+                            // computes every producer segment itself on this wave (same tile
+                            // code), so the result never depends on where or when the producers
+                            // run, and counts itself in the workspace's status words.
                             const int n = it.n_seg;
                             const size_t p0 = (size_t)bh * a.S;
                             bool lost = n > kMaxDesignatedSegments;
@@ -1210,8 +1251,8 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                             for (int r = 0; !lost; ++r) {
                                 if (r >= a.merge_polls) { lost = true; break; }
                                 if (need) {
-                                    wm = get_word(a.tag_ml + 2 * (p0 + lane));
-                                    wl = get_word(a.tag_ml + 2 * (p0 + lane) + 1);
+                                    wm = get_word(a.tag_ml + kMlStride * (p0 + lane));
+                                    wl = get_word(a.tag_ml + kMlStride * (p0 + lane) + 1);
                                 }
                                 load_batch(1, w);
                                 if (__all(word_is(wm, tag) && word_is(wl, tag) && batch_ok(w))) break;
@@ -1239,7 +1280,53 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                                         O = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), k + u)),
                                                  word_value(w[u]), O);
                             }
-                            store_out<DT>(a.out, (size_t)bh * kHeadDim + lane, lost ? __builtin_nanf("") : O / LL);
+                            float res = O / LL;
+                            if (lost) {
+                                // Fallback: this wave computes segments 1 .. n-1 itself (rows of
+                                // each over all its row slots, the fresh row patched in as the
+                                // producer would) and folds them, in segment order, into this
+                                // segment's partial.
+                                float Mo = Mb * kLn2, Lo = L, Oo = A;
+                                for (int u = 1; u < n; ++u) {
+                                    int sj0 = 0, sj1 = 0;
+                                    seg_range(u, sj0, sj1);
+                                    float mm = kStartMax, ll = 0.0f, ac[R::kElems];
+#pragma unroll
+                                    for (int e2 = 0; e2 < R::kElems; ++e2) ac[e2] = 0.0f;
+                                    if (sj1 > sj0) {
+                                        if constexpr (kPaged) {
+                                            for (int w2 = 0; w2 < kW; ++w2)
+                                                online_tiles_paged<DT, kU, kW, kFresh>(
+                                                    pv, it.b, it.h, sj0, sj1, w2, slot_row, slice, q0, a.qscale, fr,
+                                                    a.kv_out, a.kv_scale_out, cur, mm, ll, ac);
+                                        } else {
+                                            Tile<DT, kU> tf;
+                                            load_tile<DT, kU, true>(tf, sl, sj0, sj1, slot_row);
+                                            online_rows_from<DT, kU, kFresh>(tf, q0, sl, sj0, sj1, slot_row, a.qscale,
+                                                                             fr, fd, cur, mm, ll, ac);
+                                        }
+                                    }
+                                    const float mw2 = slot_reduce<R::kLanes, true>(mm);
+                                    const float f2 = exp2_fast(mm - mw2);
+                                    ll = slot_reduce<R::kLanes, false>(ll * f2);
+                                    // Channel `lane` is element lane % kElems of slice lane / kElems.
+                                    float pa = 0.0f;
+#pragma unroll
+                                    for (int e2 = 0; e2 < R::kElems; ++e2) {
+                                        const float t2 = __shfl(slot_reduce<R::kLanes, false>(ac[e2] * f2),
+                                                                lane / R::kElems);
+                                        pa = lane % R::kElems == e2 ? t2 : pa;
+                                    }
+                                    const float pmu = mw2 * kLn2;
+                                    const float Mn = fmaxf(Mo, pmu);
+                                    const float fo = exp2_fast((Mo - Mn) * kLog2e), fu = exp2_fast((pmu - Mn) * kLog2e);
+                                    Lo = Lo * fo + ll * fu;
+                                    Oo = Oo * fo + pa * fu;
+                                    Mo = Mn;
+                                }
+                                res = Oo / Lo;
+                            }
+                            store_out<DT>(a.out, (size_t)bh * kHeadDim + lane, res);
                             if (lost && lane == 0)
                                 __hip_atomic_fetch_add(a.status + kWsStatusMergeTimeouts, 1u, __ATOMIC_RELAXED,
                                                        __HIP_MEMORY_SCOPE_AGENT);
@@ -1365,7 +1452,7 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
         }
     } else {
         Item it;
-        const bool active = locate(a, blockIdx.x, it);
+        const bool active = locate(a, vbx, it, kMode == kDesignated || kMode == kDesignatedDev);
         if constexpr (kMode != kCoopMerge) {
             if (!active) return;
         }
@@ -1666,7 +1753,10 @@ int launch_split(const SplitArgs& a, int kv_dtype, int mode, bool lat, hipStream
         if (!fn) return KVATTN_ERR_DTYPE;
         grid = (grid + kStridedFactor - 1) / kStridedFactor;
     }
+    const bool des = mode == kDesignated || mode == kDesignatedDev;
+    if (des) grid = designated_grid(a.B, a.NH, a.S);
     int spec = split_spec(args);
+    int pks = a.S | (des && xcd_local_layout(a.B, a.NH) ? kXcdLocalBit : 0);
     void* params[] = SPLIT_PARAMS(args);
     KV_HIP(hipLaunchKernel(fn, dim3((unsigned)grid), dim3(threads), params, 0, stream));
     return KVATTN_OK;
@@ -1733,6 +1823,7 @@ int launch_coop(const SplitArgs& a, int kv_dtype, bool lat, hipStream_t stream) 
         if (blocks > cap) continue;
         SplitArgs args = a;
         int spec = split_spec(args);
+        int pks = args.S;
         void* params[] = SPLIT_PARAMS(args);
         KV_HIP(hipLaunchCooperativeKernel(fn, dim3((unsigned)blocks), dim3(threads), params, 0, stream));
         return KVATTN_OK;
@@ -1787,6 +1878,7 @@ int launch_graph_pair(const SplitArgs& a, int kv_dtype, bool lat, hipStream_t st
         });
         SplitArgs args = a;
         int spec = split_spec(args);
+        int pks = args.S;
         void* params[] = SPLIT_PARAMS(args);
         void* mparams[] = MERGE_PARAMS(args);
         hipGraph_t g = nullptr;
@@ -1852,7 +1944,7 @@ RegionSizes region_sizes(int B, int NH, int S) {
     const size_t bh = (size_t)B * NH;
     return {align_up(bh * sizeof(unsigned), 256), align_up(bh * S * sizeof(float), 256),
             align_up(bh * S * kHeadDim * sizeof(float), 256),
-            align_up(bh * S * 2 * sizeof(unsigned long long), 256),
+            align_up(bh * S * kMlStride * sizeof(unsigned long long), 256),
             align_up(bh * S * kHeadDim * sizeof(unsigned long long), 256)};
 }
 
@@ -2072,7 +2164,8 @@ int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scal
         case KVATTN_SPLIT_DESIGNATED: {
             const int mode = plan.seg_rows == kDevicePlanDes && !pm ? kDesignatedDev : kDesignated;
             // The mergers wait for their producers, so the whole grid must fit on the GPU at once
-            // (AUTO plans at most kDesignatedMaxGrid workgroups, one per CU).
+            // (AUTO plans at most kDesignatedMaxGrid segments, one per CU; the workgroups an
+            // XCD-local grid adds exit at once and do not count).
             const long long grid = (long long)B * NH * plan.slots;
             if (grid > kDesignatedMaxGrid) {
                 const void* fn = split_ptr_for(a, kv_dtype, mode, plan.lat);
@@ -2257,7 +2350,7 @@ const char* kvattn_strerror(int status) {
         case KVATTN_ERR_LENGTH: return "length hint outside [-1, maxT-1]";
         case KVATTN_ERR_HIP: return "HIP runtime error";
         case KVATTN_ERR_GRID_TOO_LARGE: return "designated-merger grid exceeds what the GPU holds at once";
-        case KVATTN_ERR_MERGE_TIMEOUT: return "a designated merge stopped waiting for its producers (output NaN)";
+        case KVATTN_ERR_MERGE_TIMEOUT: return "a merge stopped waiting (designated: computed its producers' segments itself; cooperative: output NaN)";
         default: return "unknown status";
     }
 }

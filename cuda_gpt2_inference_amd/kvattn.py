@@ -238,9 +238,10 @@ def workspace_init(workspace, nbytes, stream=None) -> None:
 
 
 def workspace_status(workspace, nbytes, clear=False, stream=None) -> int:
-    """Designated merges that stopped waiting for their producers (and wrote NaN) since the
-    workspace was initialised or last cleared (kvattn_workspace_status; synchronises the
-    stream).  Returns the count; it is not an error to find one here."""
+    """Merges that stopped waiting since the workspace was initialised or last cleared
+    (kvattn_workspace_status; synchronises the stream): designated mergers that computed
+    their producers' segments themselves, cooperative mergers that wrote NaN.  Returns the
+    count; it is not an error to find one here."""
     n = _i()
     st = lib().kvattn_workspace_status(_ptr(workspace), int(nbytes), int(bool(clear)), _stream(stream),
                                        ctypes.byref(n))
@@ -250,8 +251,8 @@ def workspace_status(workspace, nbytes, clear=False, stream=None) -> int:
 
 
 def set_merge_poll_limit(polls: int) -> int:
-    """Bound on the designated merger's polls for later launches (0: give up at once, a
-    fault-injection setting; < 0: the default).  Returns the previous bound."""
+    """Bound on a merger's polls for later launches (0: stop waiting at once, a
+    fault-injection setting; < 0: the default, 2^16).  Returns the previous bound."""
     return int(lib().kvattn_set_merge_poll_limit(int(polls)))
 
 

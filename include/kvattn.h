@@ -54,8 +54,10 @@ typedef enum kvattn_status {
     KVATTN_ERR_HIP = 13,            /* a HIP runtime call failed; see kvattn_last_hip_error */
     KVATTN_ERR_GRID_TOO_LARGE = 14, /* explicit SPLIT_DESIGNATED grid exceeds what the GPU holds
                                        at once (its mergers wait for their producers) */
-    KVATTN_ERR_MERGE_TIMEOUT = 15   /* kvattn_workspace_status: a designated merge stopped
-                                       waiting for its producers and wrote NaN */
+    KVATTN_ERR_MERGE_TIMEOUT = 15   /* kvattn_workspace_status: a designated merger stopped
+                                       waiting for its producers (and computed their segments
+                                       itself), or a cooperative merger stopped waiting at the
+                                       grid barrier (and wrote NaN) */
 } kvattn_status;
 
 typedef enum kvattn_dtype {
@@ -175,10 +177,12 @@ size_t kvattn_workspace_bytes(int B, int NH, int hs, int maxT, int S);
  * so it may also be captured. */
 int kvattn_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
 
-/* The workspace's sticky status: waits for `stream`, then reads the number of designated
- * merges (SPLIT_DESIGNATED, AUTO's latency-bound choice) that stopped waiting for their
- * producers since the workspace was initialised or last cleared; each such merge wrote NaN
- * for its (b,h).  *merge_timeouts (may be NULL) receives that number; clear != 0 resets it.
+/* The workspace's sticky status: waits for `stream`, then reads the number of merges that
+ * stopped waiting since the workspace was initialised or last cleared.  A designated merger
+ * (SPLIT_DESIGNATED, AUTO's latency-bound choice) that stops waiting for its producers
+ * computes their segments itself, so its output is still the attention (only slower); a
+ * cooperative merger that stops waiting at the grid barrier writes NaN for its (b,h).
+ * *merge_timeouts (may be NULL) receives that number; clear != 0 resets it.
  * Returns KVATTN_ERR_MERGE_TIMEOUT when it is non-zero, else KVATTN_OK.  Partials left by
  * such a call are never taken for a later call's (each partial word carries the dispatch
  * that wrote it), so the workspace stays usable without re-initialising.
@@ -187,11 +191,12 @@ int kvattn_workspace_init(void* workspace, size_t workspace_bytes, void* stream)
 int kvattn_workspace_status(void* workspace, size_t workspace_bytes, int clear, void* stream,
                             int* merge_timeouts);
 
-/* Bound on the designated merger's polls for its producers' partials, for launches (and
- * captures) from this call on, process-wide: polls > 0 sets it, polls == 0 makes every
- * merge of a multi-segment (b,h) give up at once (a fault-injection setting, for testing
- * the reporting above), polls < 0 restores the default (2^22 polls, seconds).  Returns
- * the previous bound.  No reference counterpart (testing and fault-injection hook). */
+/* Bound on the polls of a designated merger waiting for its producers' partials (and of a
+ * cooperative merger at the grid barrier), for launches (and captures) from this call on,
+ * process-wide: polls > 0 sets it, polls == 0 makes every merger of a multi-segment (b,h)
+ * stop waiting at once (a fault-injection setting, for testing the fallback and the
+ * reporting above), polls < 0 restores the default (2^16 polls, tens of milliseconds).
+ * Returns the previous bound.  No reference counterpart (testing and fault-injection hook). */
 int kvattn_set_merge_poll_limit(int polls);
 
 /* The launch plan kvattn_decode would use for these arguments, without launching:

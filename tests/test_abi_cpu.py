@@ -52,12 +52,13 @@ def test_strerror_covers_every_status():
 def test_workspace_bytes():
     kvattn = _kv()
     # 256 bytes of status words, counters (B*NH u32), part_max, part_lse (B*NH*S f32),
-    # part_out (B*NH*S*64 f32), the designated merger's tagged words (B*NH*S*2 and
-    # B*NH*S*64 u64), every region rounded up to 256 bytes.
+    # part_out (B*NH*S*64 f32), the designated merger's tagged words ({max, exp-sum} in a
+    # 128-byte line per slot, B*NH*S*16 u64, and B*NH*S*64 u64 channel words), every region
+    # rounded up to 256 bytes.
     def expect(B, NH, S):
         up = lambda x: (x + 255) // 256 * 256  # noqa: E731
         return (256 + up(B * NH * 4) + 2 * up(B * NH * S * 4) + up(B * NH * S * 64 * 4)
-                + up(B * NH * S * 2 * 8) + up(B * NH * S * 64 * 8))
+                + up(B * NH * S * 16 * 8) + up(B * NH * S * 64 * 8))
     assert kvattn.workspace_bytes(1, 12, 64, 1024, 8) == expect(1, 12, 8)
     assert kvattn.workspace_bytes(64, 12, 64, 8192, 0) == expect(64, 12, 8192 // 64)
     assert kvattn.workspace_bytes(2, 3, 64, 1000, -100) == expect(2, 3, 10)
@@ -157,7 +158,7 @@ def test_set_merge_poll_limit_round_trip():
     prev = kvattn.set_merge_poll_limit(5)
     try:
         assert kvattn.set_merge_poll_limit(-1) == 5
-        assert kvattn.set_merge_poll_limit(-1) == 1 << 22
+        assert kvattn.set_merge_poll_limit(-1) == 1 << 16
     finally:
         kvattn.set_merge_poll_limit(prev)
 

@@ -179,6 +179,47 @@ def test_paged_append_and_fused(dev, dtype):
         assert_close(gb, ref, dtype, what)
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "int8", "fp8"])
+def test_paged_designated_fallback_matches_oracle(dev, dtype):
+    """The designated merger's fallback on a paged cache (poll bound 0: every merger of a
+    multi-segment head computes its producers' segments itself, walking the block table):
+    the output matches the oracle, and with the append fused the pool bytes and the output
+    equal those of the normal path."""
+    import torch
+    kvattn = _kv()
+    B, NH, maxT, P = 3, 4, 1024, 64
+    lens = [1024, 300, 64]
+    case = make_case(dtype, B, NH, maxT, np.array(lens, np.int32) - 1, seed=81)
+    ref = case.reference()
+    cur = torch.from_numpy(case.cur_lens.copy()).to(dev)
+    qkv = torch.from_numpy(case.qkv_raw.view(np.int16 if dtype != "f32" else np.float32)).to(dev)
+    if dtype != "f32":
+        qkv = qkv.view(torch.bfloat16)
+    for S, hint in ((-64, -1), (0, max(lens) - 1)):
+        runs = {}
+        for bound in (None, 0):
+            for append in (False, True):
+                pg = Paged(case, P, dev, seed=3)
+                ws = kvattn.Workspace(B, NH, maxT, S)
+                out = out_tensor(case, dev)
+                prev = kvattn.set_merge_poll_limit(0) if bound == 0 else None
+                try:
+                    kvattn.paged_decode(out, qkv, pg.cache, B, NH, HS, kv_dtype=dtype, cur_len=cur,
+                                        lens_per_seq=True, len_hint=hint, S=S, strategy="designated",
+                                        append=append, **ws.kwargs())
+                    torch.cuda.synchronize()
+                finally:
+                    if prev is not None:
+                        kvattn.set_merge_poll_limit(prev)
+                what = f"paged designated S={S} hint={hint} bound={bound} append={append}"
+                assert (ws.status() > 0) == (bound == 0), what + ": status count"
+                runs[(bound, append)] = (out.float().cpu().numpy(), _dev_bytes(pg.pages).copy())
+                if not append:
+                    assert_close(runs[(bound, append)][0], ref, dtype, what)
+        assert np.array_equal(runs[(0, True)][1], runs[(None, True)][1]), f"S={S}: pool bytes of the fallback"
+        assert_close(runs[(0, True)][0], runs[(None, True)][0], dtype, f"S={S}: fused append, fallback")
+
+
 def test_paged_invalid_table_entries_are_skipped(dev):
     """A table entry outside [0, num_pages) inside a sequence's length: those positions are
     skipped, never read (the result equals attention over the remaining positions)."""
