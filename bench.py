@@ -666,6 +666,50 @@ def gemv_configs(torch, kvattn, dev, layers=12, reps=100):
     return res
 
 
+def gemv_tall_configs(torch, kvattn, dev, reps=40):
+    """The vocabulary projection of the reference engine's decode step, launch_GEMV6_w8x2<float,
+    floatX> over the 8-bit embedding table (inference_gpt2_opt.cu:389-394): Vp = 50304 rows of
+    C = 768, B = 1, float logits (kvattn_gemv_ex), for 8-bit, BF16 and FP32 weights.  A graph
+    of calls over distinct weight copies, together more than the 256 MB Infinity Cache, so
+    every call streams its weights from HBM.  Bytes per call: weights (+ row scales) + x + out."""
+    M, K = 50304, 768
+    g = torch.Generator(device=dev)
+    g.manual_seed(13)
+    res = {}
+    for w_dtype in ("int8", "fp8", "bf16", "f32"):
+        wb = {"int8": 1, "fp8": 1, "bf16": 2, "f32": 4}[w_dtype]
+        copies = max(2, -(-320 * 2 ** 20 // (M * K * wb)))
+        if w_dtype in ("int8", "fp8"):
+            Ws = [torch.randint(0, 126, (M * K,), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
+                  for _ in range(copies)]
+            scale = torch.full((M,), 1e-3, device=dev)
+        else:
+            act = torch.float32 if w_dtype == "f32" else torch.bfloat16
+            Ws = [(torch.randn(M * K, generator=g, device=dev) / K ** 0.5).to(act) for _ in range(copies)]
+            scale = None
+        x = torch.randn(K, generator=g, device=dev).to(torch.float32 if w_dtype == "f32" else torch.bfloat16)
+        out = torch.empty(M, device=dev, dtype=torch.float32)
+
+        def step():
+            for c in range(copies):
+                kvattn.gemv(out, Ws[c], x, 1, M, K, w_dtype=w_dtype, w_scale=scale, out_dtype="f32")
+        s = torch.cuda.Stream()
+        graph = torch.cuda.CUDAGraph()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(graph, stream=s):
+                step()
+        graph.replay()
+        us = timed(torch, graph.replay, reps) * 1000.0 / copies
+        nbytes = M * K * wb + (M * 4 if scale is not None else 0) + K * x.element_size() + M * 4
+        gbs = nbytes / (us * 1e-6) / 1e9
+        res[f"logits_{w_dtype}_{M}x{K}_f32out"] = {
+            "us_per_call": round(us, 3), "bytes_per_call": nbytes, "GBps": round(gbs, 1),
+            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "weight_copies": copies}
+        del Ws, graph
+    return res
+
+
 def qkv_append_configs(torch, kvattn, dev, layers=12, reps=100):
     """The QKV projection followed by the KV append, per layer of a 12-layer graph (B = 1,
     NH = 12, maxT = 1024): two launches (kvattn_gemv then kvattn_cache_write) against one
@@ -984,6 +1028,7 @@ def main():
             part = other_configs(torch, kvattn, dev, cpu_seconds=0.0)
         elif args.only == "gemv":
             part = gemv_configs(torch, kvattn, dev)
+            part["tall"] = gemv_tall_configs(torch, kvattn, dev)
         else:
             part = qkv_append_configs(torch, kvattn, dev)
         print(json.dumps({"only": args.only, "result": part, "gpu": torch.cuda.get_device_name(dev)}))
@@ -1020,6 +1065,7 @@ def main():
                                 C5Paged.NH, C5Paged.maxT, paged=True, ragged=True))
     configs = None if args.no_configs else other_configs(torch, kvattn, dev, cpu_seconds=cpu_s, coop=coop)
     gemv = None if args.no_configs else gemv_configs(torch, kvattn, dev)
+    gemv_tall = None if args.no_configs else gemv_tall_configs(torch, kvattn, dev)
     qkv_append = None if args.no_configs else qkv_append_configs(torch, kvattn, dev)
     gemv_cpu = None if (args.no_configs or args.no_cpu) else gemv_cpu_baseline()
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds, c2)
@@ -1053,7 +1099,8 @@ def main():
                   "cold_us_per_call": round(cold_us, 3),
                   "c2_context_sweep": t_sweep,
                   "c2_token_sweep": tok_sweep,
-                  "gemv": gemv, "gemv_qkv_append": qkv_append, "gemv_cpu_baseline": gemv_cpu,
+                  "gemv": gemv, "gemv_vocabulary": gemv_tall, "gemv_qkv_append": qkv_append,
+                  "gemv_cpu_baseline": gemv_cpu,
                   "rel_err_vs_f64": rel,
                   "gpu_vs_cpu_speedup": (round(cpu["value"] / us_call, 1) if cpu else None),
                   "c5": c5, "configs": configs, "gpu": torch.cuda.get_device_name(dev),

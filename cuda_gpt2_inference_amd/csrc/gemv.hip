@@ -3,12 +3,15 @@
 // tanh GELU, for FP32, BF16 and 8-bit (INT8 / FP8-E4M3 codes with one FP32 scale per row)
 // weights.  The attention output projection consumes the attention output this way.
 //
-// One wave per output row.  A row of K weights is K*wbytes/16 chunks of 16 bytes; lane l
-// holds chunks l, l+64, ... in registers (all requested at once), multiplies them with the
-// matching x chunks of every input vector, and a wave reduction (DPP + permlane) finishes
-// each dot product.  The weights are read once for all B vectors.  At GPT-2 sizes (0.6 to
-// 4.7 MB of weights per layer) a call is bound by launch and memory latency, not by HBM
-// bandwidth; MFMA is not used (B is a handful of decode tokens, 1-2 flops per byte).
+// One wave per kR output rows (kR = 1 for the per-layer shapes, 4 for tall matrices such as
+// the vocabulary projection).  A row of K weights is K*wbytes/16 chunks of 16
+// bytes; lane l holds chunks l, l+64, ... of a block of 64*kC chunks of each of its rows in
+// registers (all requested at once), multiplies them with the matching x chunks of every
+// input vector, and a wave reduction (DPP + permlane) finishes each dot product.  Rows longer
+// than one block loop over blocks.  At GPT-2's per-layer sizes (0.6 to 4.7 MB of weights) a
+// call is bound by launch and memory latency, and one row per wave gives the most waves; a
+// tall matrix (50304 x 768) streams, and 4 rows per wave keep 3-12 KB per wave in flight.
+// MFMA is not used (B is a handful of decode tokens, 1-2 flops per byte).
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -18,8 +21,9 @@
 
 namespace {
 
-constexpr int kGemvWaves = 4;          // rows (waves) per workgroup
-constexpr int kGemvMaxChunks = 16;     // 16-byte weight chunks per lane: K*wbytes <= 16 KB
+constexpr int kGemvWaves = 4;          // waves per workgroup
+constexpr int kGemvMaxChunks = 16;     // 16-byte weight chunks per lane and row in one block
+constexpr int kGemvMaxRowChunks = 16;  // kR * kC: weight registers of a wave (64 VGPRs)
 
 template <int WT> struct WFmt;
 template <> struct WFmt<KVATTN_KV_F32> {   // x, bias, out: float
@@ -127,6 +131,14 @@ __device__ __forceinline__ void store_act(void* p, size_t i, float v) {
     else reinterpret_cast<uint16_t*>(p)[i] = f32_to_bf16(v);
 }
 
+// out / pre_gelu element: float or bf16 (the output type may differ from the activations,
+// as in the reference's float logits over bf16 activations).
+template <bool kOutF32>
+__device__ __forceinline__ void store_res(void* p, size_t i, float v) {
+    if constexpr (kOutF32) reinterpret_cast<float*>(p)[i] = v;
+    else reinterpret_cast<uint16_t*>(p)[i] = f32_to_bf16(v);
+}
+
 // GPT-2's GELU, tanh form: 0.5 v (1 + tanh(sqrt(2/pi) (v + 0.044715 v^3))).
 __device__ __forceinline__ float gelu_tanh(float v) {
     const float cube = 0.044715f * v * v * v;
@@ -150,11 +162,15 @@ __device__ __forceinline__ size_t cache_row(const GemvArgs& a, int b, int part, 
 // The weights, x, scales, bias, shape and output also come as leading scalar parameters
 // (14 dwords, preloaded into SGPRs at wave launch: the library is built with kernel-argument
 // preloading), so the weight and x loads issue without a scalar load of the argument block.
-template <int WT, int kC>
+// kC: 16-byte chunks per lane and row in one block of the row; kR: rows per wave; kOutF32:
+// out and pre_gelu as float (else bf16).  Rows of more than 64*kC chunks take several blocks
+// (the weights are then read again for each input vector).
+template <int WT, int kC, int kR, bool kOutF32>
 __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(const uint8_t* pk_W, const uint8_t* pk_x,
                                                                   const float* pk_w_scale, const void* pk_bias,
                                                                   int pk_B, int pk_M, int pk_K, void* pk_out,
                                                                   int pk_gelu, GemvArgs a) {
+    static_assert(kR * kC <= kGemvMaxRowChunks && (kR == 1 || kR == 4), "weight registers");
     a.W = pk_W;
     a.x = pk_x;
     a.w_scale = pk_w_scale;
@@ -166,59 +182,95 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(const uint8_t*
     a.gelu = pk_gelu;
     using F = WFmt<WT>;
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    const int m = blockIdx.x * kGemvWaves + wave;
-    if (m >= a.M) return;   // whole wave; the one barrier (8-bit QKV epilogue) has M % kGemvWaves == 0
+    const int m0 = (blockIdx.x * kGemvWaves + wave) * kR;
+    if (m0 >= a.M) return;   // whole wave; the one barrier (8-bit QKV epilogue, kR = 1) has M % kGemvWaves == 0
     const int nch = a.K * F::kWBytes / 16;
-    const uint8_t* wrow = a.W + (size_t)m * a.K * F::kWBytes;
+    constexpr int kBlk = kWave * kC;                 // chunks of a row in one block
+    const int nblk = (nch + kBlk - 1) / kBlk;
+    const size_t row_bytes = (size_t)a.K * F::kWBytes;
     // Every load is unconditional, so that all of them issue before the first wait: a lane's
     // chunks beyond the row (c >= nch) read chunk nch - 1 again and their products are
-    // dropped by a select.  (Loads behind branches make the code generator wait for each
-    // one before the next: one memory round trip per chunk.)
-    uint4 w[kC];
+    // dropped by a select, and rows beyond M (the last wave of a kR > 1 grid) read row M - 1
+    // and are not stored.  (Loads behind branches make the code generator wait for each one
+    // before the next: one memory round trip per chunk.)  The weights are read once per
+    // call and marked non-temporal (vocabulary projection, 50304 x 768: -3 % INT8, -6 %
+    // BF16, -9 % FP32 per call; the per-layer shapes within +-0.05 us).
+    uint4 w[kR][kC];
+    auto load_w = [&](int kb) {
 #pragma unroll
-    for (int i = 0; i < kC; ++i)
-        w[i] = *reinterpret_cast<const uint4*>(wrow + (size_t)min(lane + i * kWave, nch - 1) * 16);
+        for (int r = 0; r < kR; ++r) {
+            const uint8_t* wrow = a.W + (size_t)min(m0 + r, a.M - 1) * row_bytes;
+#pragma unroll
+            for (int i = 0; i < kC; ++i)
+                w[r][i] = load16(wrow + (size_t)min(kb * kBlk + lane + i * kWave, nch - 1) * 16);
+        }
+    };
+    load_w(0);
     constexpr int kActBytes = F::kActF32 ? 4 : 2;
     // x of the first vector and the bias are requested right behind the weights, before
     // anything waits (the weights' unpacking, which the code generator hoists out of the
     // vector loop, waits for the weights only).
     XRaw<WT> xr[kC];
-    auto load_xs = [&](int b) {
+    auto load_xs = [&](int b, int kb) {
         const uint8_t* xb = a.x + (size_t)b * a.K * kActBytes;
 #pragma unroll
-        for (int i = 0; i < kC; ++i) xr[i] = load_x<WT>(xb + (size_t)min(lane + i * kWave, nch - 1) * F::kXBytes);
+        for (int i = 0; i < kC; ++i)
+            xr[i] = load_x<WT>(xb + (size_t)min(kb * kBlk + lane + i * kWave, nch - 1) * F::kXBytes);
     };
-    load_xs(0);
-    const float braw = load_act<WT>(a.bias ? a.bias : (const void*)a.x, a.bias ? m : 0);
-    const float bias = a.bias ? braw : 0.0f;
-    const int len0 = (a.kv ? a.cur_len : reinterpret_cast<const int*>(a.x))[0];   // the QKV epilogue's column
-    const float ws = F::k8bit ? a.w_scale[m] : 1.0f;
-    for (int b = 0; b < a.B; ++b) {
-        if (b > 0) load_xs(b);
-        float acc = 0.0f;
+    load_xs(0, 0);
+    float bias[kR], ws[kR];
 #pragma unroll
-        for (int i = 0; i < kC; ++i) {
-            const float d = acc + chunk_dot<WT>(w[i], xr[i]);
-            acc = lane + i * kWave < nch ? d : acc;
-        }
-        acc = wave_sum(acc);
-        if (lane == 0) {
-            float pre = acc * ws + bias;
-            const size_t o = (size_t)b * a.M + m;
-            if (a.pre_gelu) store_act<WT>(a.pre_gelu, o, pre);
-            if (a.gelu) pre = gelu_tanh(pre);
-            store_act<WT>(a.out, o, pre);
-            if (a.kv && a.kv_dtype == (F::kActF32 ? KVATTN_KV_F32 : KVATTN_KV_BF16)) {
-                // Output m is channel c of head h of part q/k/v; K and V also land in the cache
-                // row of position cur_len, as the separate append would copy them.
-                const int part = m / (a.NH * kHd);
-                if (part > 0) {
-                    const int h = (m - part * a.NH * kHd) / kHd, c = m - part * a.NH * kHd - h * kHd;
-                    store_act<WT>(a.kv, cache_row(a, b, part, h, len0) * kHd + c, pre);
+    for (int r = 0; r < kR; ++r) {
+        const int mr = min(m0 + r, a.M - 1);
+        const float braw = load_act<WT>(a.bias ? a.bias : (const void*)a.x, a.bias ? mr : 0);
+        bias[r] = a.bias ? braw : 0.0f;
+        ws[r] = F::k8bit ? a.w_scale[mr] : 1.0f;
+    }
+    const int len0 = (a.kv ? a.cur_len : reinterpret_cast<const int*>(a.x))[0];   // the QKV epilogue's column
+    for (int b = 0; b < a.B; ++b) {
+        float accr[kR];
+#pragma unroll
+        for (int r = 0; r < kR; ++r) accr[r] = 0.0f;
+        for (int kb = 0; kb < nblk; ++kb) {
+            if (kb > 0 || b > 0) {
+                if (nblk > 1) load_w(kb);   // one block: the weights stay in registers for every vector
+                load_xs(b, kb);
+            }
+#pragma unroll
+            for (int r = 0; r < kR; ++r) {
+#pragma unroll
+                for (int i = 0; i < kC; ++i) {
+                    const float d = accr[r] + chunk_dot<WT>(w[r][i], xr[i]);
+                    accr[r] = kb * kBlk + lane + i * kWave < nch ? d : accr[r];
                 }
             }
         }
-        if (a.kv && (a.kv_dtype == KVATTN_KV_INT8 || a.kv_dtype == KVATTN_KV_FP8_E4M3)) {
+#pragma unroll
+        for (int r = 0; r < kR; ++r) accr[r] = wave_sum(accr[r]);
+        if (lane == 0) {
+#pragma unroll
+            for (int r = 0; r < kR; ++r) {
+                const int m = m0 + r;
+                if (m >= a.M) break;
+                float pre = accr[r] * ws[r] + bias[r];
+                const size_t o = (size_t)b * a.M + m;
+                if (a.pre_gelu) store_res<kOutF32>(a.pre_gelu, o, pre);
+                if (a.gelu) pre = gelu_tanh(pre);
+                store_res<kOutF32>(a.out, o, pre);
+                if (kR == 1 && a.kv && a.kv_dtype == (F::kActF32 ? KVATTN_KV_F32 : KVATTN_KV_BF16)) {
+                    // Output m is channel c of head h of part q/k/v; K and V also land in the cache
+                    // row of position cur_len, as the separate append would copy them.
+                    const int part = m / (a.NH * kHd);
+                    if (part > 0) {
+                        const int h = (m - part * a.NH * kHd) / kHd, c = m - part * a.NH * kHd - h * kHd;
+                        store_act<WT>(a.kv, cache_row(a, b, part, h, len0) * kHd + c, pre);
+                    }
+                }
+            }
+        }
+        const int m = m0;
+        const float acc = accr[0];
+        if (kR == 1 && a.kv && (a.kv_dtype == KVATTN_KV_INT8 || a.kv_dtype == KVATTN_KV_FP8_E4M3)) {
             // An 8-bit row's scale needs the amax of the head's 64 channels, which 16
             // workgroups compute (4 channels each; M = 3*NH*64 is a multiple of 4, so every
             // wave of the workgroup is here and part/h are the same for all four).  The four
@@ -234,7 +286,7 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(const uint8_t*
             const int part = m / (a.NH * kHd);
             if (part > 0) {
                 const int h = (m - part * a.NH * kHd) / kHd;
-                if (lane == 0) s_val[b & 1][wave] = bf16_to_f32(f32_to_bf16(acc * ws + bias));
+                if (lane == 0) s_val[b & 1][wave] = bf16_to_f32(f32_to_bf16(acc * ws[0] + bias[0]));
                 __syncthreads();
                 if (wave == 0) {
                     const size_t rid = ((size_t)b * 2 + (part - 1)) * a.NH + h;
@@ -272,13 +324,32 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(const uint8_t*
     }
 }
 
+// Rows per wave: one for the per-layer shapes (latency bound: the most waves), 4 from
+// kGemvTallRows rows on (bandwidth bound: more bytes in flight per wave).  kC: chunks per
+// lane and row in one block, the fewest that hold the row, at most kGemvMaxRowChunks / kR
+// (longer rows loop over blocks).
+#ifndef KVATTN_GEMV_TALL_ROWS
+#define KVATTN_GEMV_TALL_ROWS 8192
+#endif
+constexpr int kGemvTallRows = KVATTN_GEMV_TALL_ROWS;
+
+template <int WT, bool kOut>
+const void* gemv_ptr(int chunks_per_lane, int rows) {
+    if (rows == 4) {
+        if (chunks_per_lane <= 1) return (const void*)&gemv_kernel<WT, 1, 4, kOut>;
+        if (chunks_per_lane <= 2) return (const void*)&gemv_kernel<WT, 2, 4, kOut>;
+        return (const void*)&gemv_kernel<WT, 4, 4, kOut>;
+    }
+    if (chunks_per_lane <= 1) return (const void*)&gemv_kernel<WT, 1, 1, kOut>;
+    if (chunks_per_lane <= 2) return (const void*)&gemv_kernel<WT, 2, 1, kOut>;
+    if (chunks_per_lane <= 4) return (const void*)&gemv_kernel<WT, 4, 1, kOut>;
+    if (chunks_per_lane <= 8) return (const void*)&gemv_kernel<WT, 8, 1, kOut>;
+    return (const void*)&gemv_kernel<WT, kGemvMaxChunks, 1, kOut>;
+}
+
 template <int WT>
-const void* gemv_ptr(int chunks_per_lane) {
-    if (chunks_per_lane <= 1) return (const void*)&gemv_kernel<WT, 1>;
-    if (chunks_per_lane <= 2) return (const void*)&gemv_kernel<WT, 2>;
-    if (chunks_per_lane <= 4) return (const void*)&gemv_kernel<WT, 4>;
-    if (chunks_per_lane <= 8) return (const void*)&gemv_kernel<WT, 8>;
-    return (const void*)&gemv_kernel<WT, kGemvMaxChunks>;
+const void* gemv_ptr_out(int chunks_per_lane, int rows, bool out_f32) {
+    return out_f32 ? gemv_ptr<WT, true>(chunks_per_lane, rows) : gemv_ptr<WT, false>(chunks_per_lane, rows);
 }
 
 }  // namespace
@@ -289,34 +360,42 @@ void set_last_hip_error(int e);   // kvattn.hip: read back by kvattn_last_hip_er
 
 namespace {
 
-// Checks shared by both entry points, then the launch.
-int launch_gemv(GemvArgs a, int w_dtype, void* stream) {
+// Checks shared by the entry points, then the launch.  out_f32: out and pre_gelu as float,
+// else bf16.
+int launch_gemv(GemvArgs a, int w_dtype, bool out_f32, void* stream) {
     if (w_dtype < KVATTN_KV_F32 || w_dtype > KVATTN_KV_FP8_E4M3) return KVATTN_ERR_DTYPE;
     const bool w8 = w_dtype == KVATTN_KV_INT8 || w_dtype == KVATTN_KV_FP8_E4M3;
     const int wbytes = w_dtype == KVATTN_KV_F32 ? 4 : (w_dtype == KVATTN_KV_BF16 ? 2 : 1);
     const size_t act = w_dtype == KVATTN_KV_F32 ? 4 : 2;
+    const size_t osz = out_f32 ? 4 : 2;
     const int B = a.B, M = a.M, K = a.K;
     if (B < 1 || M < 1 || K < 16 || K % 16 != 0) return KVATTN_ERR_SHAPE;
-    if ((long long)K * wbytes > (long long)kGemvMaxChunks * kWave * 16) return KVATTN_ERR_SHAPE;
-    if ((long long)B * M >= (1ll << 31) || (long long)M * K * wbytes >= (1ll << 40)) return KVATTN_ERR_SHAPE;
+    if ((long long)B * M >= (1ll << 31) || (long long)M * K * wbytes >= (1ll << 40) || (long long)B * K >= (1ll << 31))
+        return KVATTN_ERR_SHAPE;
     if (!a.out || !a.W || !a.x) return KVATTN_ERR_NULL_POINTER;
     if (w8 && !a.w_scale) return KVATTN_ERR_DTYPE;
     if (((uintptr_t)a.W & 15u) || ((uintptr_t)a.x & 15u)) return KVATTN_ERR_MISALIGNED;
-    if (((uintptr_t)a.out % act) || ((uintptr_t)a.pre_gelu % act) || ((uintptr_t)a.bias % act) ||
+    if (((uintptr_t)a.out % osz) || ((uintptr_t)a.pre_gelu % osz) || ((uintptr_t)a.bias % act) ||
         ((uintptr_t)a.w_scale & 3u) ||
         (a.kv && a.kv_dtype != KVATTN_KV_INT8 && a.kv_dtype != KVATTN_KV_FP8_E4M3 && ((uintptr_t)a.kv % act)))
         return KVATTN_ERR_MISALIGNED;
     const int nch = K * wbytes / 16;
     const int per_lane = (nch + kWave - 1) / kWave;
+    // The QKV epilogue needs one row per wave (its workgroups meet per four channels).
+    // Measured at 50304 x 768 (per call, graph of calls over weights beyond the Infinity
+    // Cache): 4 rows per wave 9.2 / 13.8 / 24.9 us (INT8 / BF16 / FP32), 8 rows 9.8 / 15.5 /
+    // 24.9, one row 16.8 / 19.0 / 26.6.
+    const int rows = a.kv || M < kGemvTallRows ? 1 : 4;
     const void* fn = nullptr;
     switch (w_dtype) {
-        case KVATTN_KV_F32: fn = gemv_ptr<KVATTN_KV_F32>(per_lane); break;
-        case KVATTN_KV_BF16: fn = gemv_ptr<KVATTN_KV_BF16>(per_lane); break;
-        case KVATTN_KV_INT8: fn = gemv_ptr<KVATTN_KV_INT8>(per_lane); break;
-        default: fn = gemv_ptr<KVATTN_KV_FP8_E4M3>(per_lane); break;
+        case KVATTN_KV_F32: fn = gemv_ptr_out<KVATTN_KV_F32>(per_lane, rows, out_f32); break;
+        case KVATTN_KV_BF16: fn = gemv_ptr_out<KVATTN_KV_BF16>(per_lane, rows, out_f32); break;
+        case KVATTN_KV_INT8: fn = gemv_ptr_out<KVATTN_KV_INT8>(per_lane, rows, out_f32); break;
+        default: fn = gemv_ptr_out<KVATTN_KV_FP8_E4M3>(per_lane, rows, out_f32); break;
     }
+    const long long waves = ((long long)M + rows - 1) / rows;
     void* params[] = {&a.W, &a.x, &a.w_scale, &a.bias, &a.B, &a.M, &a.K, &a.out, &a.gelu, &a};
-    const hipError_t e = hipLaunchKernel(fn, dim3((unsigned)((M + kGemvWaves - 1) / kGemvWaves)),
+    const hipError_t e = hipLaunchKernel(fn, dim3((unsigned)((waves + kGemvWaves - 1) / kGemvWaves)),
                                          dim3(kGemvWaves * kWave), params, 0, (hipStream_t)stream);
     if (e != hipSuccess) {
         kvattn_internal::set_last_hip_error((int)e);
@@ -331,7 +410,16 @@ extern "C" int kvattn_gemv(void* out, void* pre_gelu, const void* W, const float
                            const void* bias, int B, int M, int K, int w_dtype, int gelu, void* stream) {
     GemvArgs a{out, pre_gelu, (const uint8_t*)W, w_scale, (const uint8_t*)x, bias, B, M, K, gelu ? 1 : 0,
                nullptr, nullptr, 0, 0, 0, 0, nullptr, nullptr, nullptr};
-    return launch_gemv(a, w_dtype, stream);
+    return launch_gemv(a, w_dtype, w_dtype == KVATTN_KV_F32, stream);
+}
+
+extern "C" int kvattn_gemv_ex(void* out, void* pre_gelu, const void* W, const float* w_scale, const void* x,
+                              const void* bias, int B, int M, int K, int w_dtype, int out_dtype, int gelu,
+                              void* stream) {
+    if (out_dtype != KVATTN_KV_F32 && out_dtype != KVATTN_KV_BF16) return KVATTN_ERR_DTYPE;
+    GemvArgs a{out, pre_gelu, (const uint8_t*)W, w_scale, (const uint8_t*)x, bias, B, M, K, gelu ? 1 : 0,
+               nullptr, nullptr, 0, 0, 0, 0, nullptr, nullptr, nullptr};
+    return launch_gemv(a, w_dtype, out_dtype == KVATTN_KV_F32, stream);
 }
 
 extern "C" size_t kvattn_gemv_qkv_append_workspace_bytes(int B, int NH) {
@@ -369,5 +457,5 @@ extern "C" int kvattn_gemv_qkv_append(void* qkv, const void* W, const float* w_s
     }
     GemvArgs a{qkv, nullptr, (const uint8_t*)W, w_scale, (const uint8_t*)x, bias, B, 3 * NH * hs, K, 0,
                (uint8_t*)kv_cache, d_cur_len, lens_per_seq ? 1 : 0, NH, maxT, kv_dtype, kv_scale, stage, arrivals};
-    return launch_gemv(a, w_dtype, stream);
+    return launch_gemv(a, w_dtype, w_dtype == KVATTN_KV_F32, stream);
 }

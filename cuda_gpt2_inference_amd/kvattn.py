@@ -95,6 +95,7 @@ SIGNATURES = {
     "kvattn_append_decode": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp, _sz, _i, _i, _i, _vp]),
     "kvattn_decode_static": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _i, _i, _i, _i, _vp]),
     "kvattn_gemv": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
+    "kvattn_gemv_ex": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "kvattn_gemv_qkv_append": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _i, _vp, _i, _i, _i, _vp,
                                     _sz, _vp]),
     "kvattn_gemv_qkv_append_workspace_bytes": (_sz, [_i, _i]),
@@ -298,11 +299,17 @@ def append_decode(out, qkv, kv_cache, B, NH, hs, maxT, *, kv_dtype, kv_scale=Non
                                       kv_dtype_code(kv_dtype), _stream(stream)), "kvattn_append_decode")
 
 
-def gemv(out, W, x, B, M, K, *, w_dtype, w_scale=None, bias=None, pre_gelu=None, gelu=False,
+def gemv(out, W, x, B, M, K, *, w_dtype, w_scale=None, bias=None, pre_gelu=None, gelu=False, out_dtype=None,
          stream=None) -> None:
-    """Decode-step fully connected layer out = [GELU](W x [* w_scale] + bias) (kvattn_gemv)."""
-    _check(lib().kvattn_gemv(_ptr(out), _ptr(pre_gelu), _ptr(W), _ptr(w_scale), _ptr(x), _ptr(bias), B, M, K,
-                             kv_dtype_code(w_dtype), int(bool(gelu)), _stream(stream)), "kvattn_gemv")
+    """Decode-step fully connected layer out = [GELU](W x [* w_scale] + bias) (kvattn_gemv;
+    kvattn_gemv_ex when out_dtype, "f32" or "bf16", is given)."""
+    if out_dtype is None:
+        _check(lib().kvattn_gemv(_ptr(out), _ptr(pre_gelu), _ptr(W), _ptr(w_scale), _ptr(x), _ptr(bias), B, M, K,
+                                 kv_dtype_code(w_dtype), int(bool(gelu)), _stream(stream)), "kvattn_gemv")
+        return
+    _check(lib().kvattn_gemv_ex(_ptr(out), _ptr(pre_gelu), _ptr(W), _ptr(w_scale), _ptr(x), _ptr(bias), B, M, K,
+                                kv_dtype_code(w_dtype), kv_dtype_code(out_dtype), int(bool(gelu)),
+                                _stream(stream)), "kvattn_gemv_ex")
 
 
 def gemv_qkv_append(qkv, W, x, B, NH, hs, K, kv_cache, maxT, *, w_dtype, kv_dtype=None, w_scale=None, bias=None,

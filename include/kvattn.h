@@ -307,14 +307,26 @@ int kvattn_paged_decode(void* out, const void* qkv, void* pages, float* page_sca
  *   BF16       W, x, bias, out, pre_gelu bf16
  *   INT8, FP8  W one code per weight ([M][K] bytes) with one FP32 scale per row; x, bias,
  *              out, pre_gelu bf16
- * W is row-major [M][K]; x [B][K]; out [B][M].  Requires K % 16 == 0, K * weight bytes <=
- * 16 KB, 16-byte aligned W and x.  bias may be NULL.
+ * W is row-major [M][K]; x [B][K]; out [B][M].  Requires K % 16 == 0 (any length: rows
+ * beyond 64 * 16 chunks of 16 bytes are walked in blocks, as the reference's tail loops walk
+ * any K), 16-byte aligned W and x.  bias may be NULL.  From 8192 rows on (a vocabulary
+ * projection), each wave takes 4 rows so that more weight bytes are in flight.
  * Replaces launch_GEMV6_fused (Inference_gpt2/GEMV.cuh:132-206) and launch_GEMV6_w8x2
  * (Inference_gpt2/GEMV_w8.cuh:64-184), which matmul_forward[_w8] calls for one decode token
  * (inference_gpt2_opt.cu:106-132); the attention output projection is at :349-355.  B > 1
- * reads the weights once for all B vectors (the reference takes cuBLASLt there). */
+ * reads the weights once for all B vectors when a row fits in one block (the reference
+ * takes cuBLASLt there). */
 int kvattn_gemv(void* out, void* pre_gelu, const void* W, const float* w_scale, const void* x,
                 const void* bias, int B, int M, int K, int w_dtype, int gelu, void* stream);
+
+/* kvattn_gemv with the output type given: out and pre_gelu are float (out_dtype
+ * KVATTN_KV_F32) or bf16 (KVATTN_KV_BF16), whatever the weights; x and bias keep the
+ * activation type of w_dtype.  Replaces the reference's instantiations with an output type
+ * other than the activations', such as the vocabulary projection over the 8-bit embedding
+ * table, launch_GEMV6_w8x2<float, floatX>(logits, NULL, w8_wte, lnf, w8_wte_s, NULL, Vp, C,
+ * false, stream) (inference_gpt2_opt.cu:389-394). */
+int kvattn_gemv_ex(void* out, void* pre_gelu, const void* W, const float* w_scale, const void* x,
+                   const void* bias, int B, int M, int K, int w_dtype, int out_dtype, int gelu, void* stream);
 
 /* The QKV projection with the KV append in its epilogue: kvattn_gemv with M = 3 * NH * hs
  * (no GELU) into qkv [B][3][NH][hs], whose K and V rows also go to column cur_len of

@@ -129,18 +129,31 @@ inline void kv_append_attention(void* out, const void* qkv, void* kv_cache, floa
 // launch_GEMV6_fused<floatX>(out, pre_gelu, W, x, bias, M, K, do_gelu, stream)
 // (Inference_gpt2/GEMV.cuh:204-208), as matmul_forward calls it for one decode token
 // (inference_gpt2_opt.cu:106-116).  w_dtype: KVATTN_KV_BF16 (floatX = bf16) or KVATTN_KV_F32.
+// out_dtype: the reference's OT when it differs from the activations (KVATTN_KV_F32 or
+// KVATTN_KV_BF16); -1 keeps the activation type.
 inline void launch_GEMV6_fused(void* out, void* pre_gelu, const void* W, const void* x, const void* bias, int M,
-                               int K, bool do_gelu, hipStream_t stream, int w_dtype = KVATTN_KV_BF16) {
-    kvattnCheck(kvattn_gemv(out, pre_gelu, W, nullptr, x, bias, 1, M, K, w_dtype, do_gelu ? 1 : 0, stream));
+                               int K, bool do_gelu, hipStream_t stream, int w_dtype = KVATTN_KV_BF16,
+                               int out_dtype = -1) {
+    if (out_dtype < 0)
+        kvattnCheck(kvattn_gemv(out, pre_gelu, W, nullptr, x, bias, 1, M, K, w_dtype, do_gelu ? 1 : 0, stream));
+    else
+        kvattnCheck(kvattn_gemv_ex(out, pre_gelu, W, nullptr, x, bias, 1, M, K, w_dtype, out_dtype,
+                                   do_gelu ? 1 : 0, stream));
 }
 
 // launch_GEMV6_w8x2(out, pre_gelu, W, x, scale, bias, M, K, do_gelu, stream)
 // (Inference_gpt2/GEMV_w8.cuh:162-184), as matmul_forward_w8 calls it (inference_gpt2_opt.cu:
 // 121-132).  w_dtype: KVATTN_KV_INT8 or KVATTN_KV_FP8_E4M3 (the reference's USE_INT8 / USE_FP8).
+// out_dtype KVATTN_KV_F32 is the reference's launch_GEMV6_w8x2<float, floatX>, the vocabulary
+// projection into float logits (inference_gpt2_opt.cu:389-394); -1 keeps bf16.
 inline void launch_GEMV6_w8x2(void* out, void* pre_gelu, const uint8_t* W, const void* x, const float* scale,
                               const void* bias, int M, int K, bool do_gelu, hipStream_t stream,
-                              int w_dtype = KVATTN_KV_INT8) {
-    kvattnCheck(kvattn_gemv(out, pre_gelu, W, scale, x, bias, 1, M, K, w_dtype, do_gelu ? 1 : 0, stream));
+                              int w_dtype = KVATTN_KV_INT8, int out_dtype = -1) {
+    if (out_dtype < 0)
+        kvattnCheck(kvattn_gemv(out, pre_gelu, W, scale, x, bias, 1, M, K, w_dtype, do_gelu ? 1 : 0, stream));
+    else
+        kvattnCheck(kvattn_gemv_ex(out, pre_gelu, W, scale, x, bias, 1, M, K, w_dtype, out_dtype,
+                                   do_gelu ? 1 : 0, stream));
 }
 
 }  // namespace kvattn_gpt2

@@ -105,7 +105,6 @@ ALIGNED = 1 << 20
     (dict(K=0), 4),
     (dict(M=0), 4),
     (dict(B=0), 4),
-    (dict(K=8192, w_dtype=0), 4),       # 32 KB FP32 rows exceed the register-resident row
     (dict(w_dtype=7), 5),               # KVATTN_ERR_DTYPE
     (dict(w_dtype=2, w_scale=None), 5),  # 8-bit weights without row scales
     (dict(W=None), 1),                  # KVATTN_ERR_NULL_POINTER
@@ -120,6 +119,23 @@ def test_gemv_argument_errors(kw, status):
     a.update(kw)
     st = kvattn.lib().kvattn_gemv(a["out"], a["pre"], a["W"], a["w_scale"], a["x"], a["bias"], a["B"], a["M"],
                                   a["K"], a["w_dtype"], a["gelu"], None)
+    assert st == status, kvattn.strerror(st)
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(out_dtype=2), 5),             # out must be float or bf16 -> KVATTN_ERR_DTYPE
+    (dict(out_dtype=7), 5),
+    (dict(out=ALIGNED + 2), 2),         # float out, 2-byte aligned -> KVATTN_ERR_MISALIGNED
+    (dict(K=24), 4),
+])
+def test_gemv_ex_argument_errors(kw, status):
+    """kvattn_gemv_ex's output type and alignment checks (made before any HIP call)."""
+    from cuda_gpt2_inference_amd import kvattn
+    a = dict(out=ALIGNED, pre=None, W=ALIGNED, w_scale=ALIGNED, x=ALIGNED, bias=None, B=1, M=50304, K=768,
+             w_dtype=2, out_dtype=0, gelu=0)
+    a.update(kw)
+    st = kvattn.lib().kvattn_gemv_ex(a["out"], a["pre"], a["W"], a["w_scale"], a["x"], a["bias"], a["B"], a["M"],
+                                     a["K"], a["w_dtype"], a["out_dtype"], a["gelu"], None)
     assert st == status, kvattn.strerror(st)
 
 

@@ -62,15 +62,19 @@ def _make(dtype, B, M, K, seed, with_bias=True):
     return dev, host
 
 
-def _run(dev_t, dtype, B, M, K, gelu, want_pre):
+def _run(dev_t, dtype, B, M, K, gelu, want_pre, out_dtype=None):
+    """kvattn_gemv (out in the activation type), or kvattn_gemv_ex with out_dtype."""
     import torch
     kvattn = _kv()
     d = {k: (None if v is None else v.to("cuda:0")) for k, v in dev_t.items()}
-    act = torch.float32 if dtype == "f32" else torch.bfloat16
-    out = torch.full((B * M,), float("nan"), dtype=act, device="cuda:0")
-    pre = torch.full((B * M,), float("nan"), dtype=act, device="cuda:0") if want_pre else None
+    if out_dtype is None:
+        odt = torch.float32 if dtype == "f32" else torch.bfloat16
+    else:
+        odt = torch.float32 if out_dtype == "f32" else torch.bfloat16
+    out = torch.full((B * M,), float("nan"), dtype=odt, device="cuda:0")
+    pre = torch.full((B * M,), float("nan"), dtype=odt, device="cuda:0") if want_pre else None
     kvattn.gemv(out, d["W"], d["x"], B, M, K, w_dtype=dtype, w_scale=d.get("scale"), bias=d["bias"],
-                pre_gelu=pre, gelu=gelu)
+                pre_gelu=pre, gelu=gelu, out_dtype=out_dtype)
     torch.cuda.synchronize()
     return out.float().cpu().numpy(), (None if pre is None else pre.float().cpu().numpy())
 
@@ -110,6 +114,63 @@ def test_gemv_ragged_shapes(dev, dtype, M, K):
     got, _ = _run(d, dtype, 2, M, K, False, False)
     ref = oracle.gemv(h["W"], h["x"], 2, M, K, w_scale=h["scale"])
     _check(got, ref, dtype, 2, M, f"M={M} K={K} {dtype}")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "int8", "fp8"])
+def test_gemv_vocabulary_projection_float_out(dev, dtype):
+    """The reference engine's vocabulary projection, launch_GEMV6_w8x2<float, floatX> over the
+    8-bit embedding table into float logits (inference_gpt2_opt.cu:389-394): Vp = 50304 rows
+    of C = 768, no bias, float output (kvattn_gemv_ex), taken by the tall-matrix shape (several
+    rows per wave).  The same call with bf16 output must equal the float result rounded."""
+    M, K = 50304, 768
+    d, h = _make(dtype, 1, M, K, seed=5030 + len(dtype), with_bias=False)
+    got, _ = _run(d, dtype, 1, M, K, False, False, out_dtype="f32")
+    ref = oracle.gemv(h["W"], h["x"], 1, M, K, w_scale=h["scale"])
+    _check(got, ref, "f32" if dtype == "f32" else dtype, 1, M, f"logits {dtype} float out")
+    got_b, _ = _run(d, dtype, 1, M, K, False, False, out_dtype="bf16")
+    assert np.array_equal(got_b.view(np.uint32), oracle.bf16_decode(oracle.bf16_round(got)).view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "int8", "fp8"])
+@pytest.mark.parametrize("M", [37, 8195])
+def test_gemv_rows_beyond_one_block(dev, dtype, M):
+    """Rows longer than one block of a wave's registers: with one row per wave (37 rows) a
+    block is 64 x 16 chunks, so rows of 32 KB (FP32), 24 KB (bf16) and 20 KB (8-bit) take two
+    blocks; with the tall shape (8195 rows, 4 rows per wave, a partial last wave) a block is
+    64 x 4 chunks, and 4608-element rows take 2 to 5 blocks.  B = 1 and B = 3 (the weights
+    are read again per vector); with bias and GELU."""
+    if M < 8192:
+        K = {"f32": 8192, "bf16": 12288, "int8": 20480, "fp8": 20480}[dtype]
+    else:
+        K = 4608
+    for B in (1, 3):
+        d, h = _make(dtype, B, M, K, seed=M + B + K)
+        got, pre = _run(d, dtype, B, M, K, True, True)
+        ref, rpre = oracle.gemv(h["W"], h["x"], B, M, K, w_scale=h["scale"], bias=h["bias"], gelu=True,
+                                want_pre=True)
+        _check(got, ref, dtype, B, M, f"M={M} K={K} {dtype} B={B}")
+        _check(pre, rpre, dtype, B, M, f"M={M} K={K} {dtype} B={B} pre_gelu")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "int8"])
+def test_gemv_tall_shape_equals_one_row_per_wave(dev, dtype):
+    """A tall matrix (several rows per wave) against the same rows computed in pieces of
+    fewer than 8192 rows (one row per wave): bit-identical, since both sum each row's chunks
+    in the same order."""
+    import torch
+    M, K = 12288, 1024
+    d, _ = _make(dtype, 2, M, K, seed=91)
+    whole, _ = _run(d, dtype, 2, M, K, False, False)
+    parts = []
+    for m0 in range(0, M, 4096):
+        sub = dict(d)
+        sub["W"] = d["W"][m0:m0 + 4096].contiguous()
+        sub["bias"] = d["bias"][m0:m0 + 4096].contiguous()
+        if d.get("scale") is not None:
+            sub["scale"] = d["scale"][m0:m0 + 4096].contiguous()
+        p, _ = _run(sub, dtype, 2, 4096, K, False, False)
+        parts.append(p.reshape(2, 4096))
+    assert np.array_equal(whole.reshape(2, M), np.concatenate(parts, axis=1))
 
 
 @pytest.mark.parametrize("dtype,kv", [("f32", "f32"), ("bf16", "bf16"), ("int8", "bf16"), ("bf16", "int8"),
