@@ -136,8 +136,7 @@ def traffic(fetch_dir: str, write_dir: str, cmd_fetch: str, cmd_write: str) -> s
            "|---|---|---|---|---|"]
     lines = []
     for k in sorted(fetch, key=lambda x: -fetch[x]):
-        if k.startswith(CALIB_KERNEL) or "split_kernel" not in k and "merge_kernel" not in k \
-                and "fused_single" not in k:
+        if k.startswith(CALIB_KERNEL) or not any(o in k for o in OWN_KERNELS):
             continue
         f = fetch[k]
         w = write.get(k, float("nan"))
