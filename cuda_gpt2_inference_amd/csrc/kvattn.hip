@@ -121,7 +121,8 @@ template <int DT> constexpr int kUnrollFused =
 // 128-row designated segment is then one full tile per wave of a 4-wave workgroup.  Each
 // tile's arithmetic runs over all its row slots, valid or masked, and at GPT-2's sizes it is
 // on the call's critical path: 64-row tiles, half of them masked, cost C2 0.24 µs per call.
-// (The device-planned designated instance keeps KVATTN_LAT_ROWS: see split_ptr.)
+// The device-planned designated instance takes them too: its segment 0, up to kFusedMaxRows
+// rows, gives each wave up to two tiles, both requested before the first is consumed.
 #ifndef KVATTN_SPLIT_LAT_ROWS
 #define KVATTN_SPLIT_LAT_ROWS 32
 #endif
@@ -1072,10 +1073,9 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
     // Designated segments planned on the device (kDesignatedDev) are designated_base_rows()
     // long at every length from kFusedMaxRows + 1 up to 64 segments' worth, so every
     // workgroup guesses that length (there is no hint to go by).  Segment 0 is also the
-    // whole length up to kFusedMaxRows, so its waves split that range, and only those whose
-    // share lies inside the first designated_base_rows() rows request it early; the others
-    // request theirs once the length shows that they have rows.  A segment the length plans
-    // otherwise (doubled rows) drops the guess and requests its true first tile.
+    // whole length up to kFusedMaxRows: wave w requests tile w of the segment's first kW tiles
+    // early, and tile w of the next kW once the length shows they hold rows.  A segment the
+    // length plans otherwise (doubled rows) drops the guess and requests its true first tile.
     constexpr bool kDev = kMode == kDesignatedDev;
     // The guess: first tile, q slice and fresh row; whether it was made and holds this
     // wave's tile; this wave's rows of the nominal range; the nominal range [g_j0, g_end).
@@ -1094,7 +1094,11 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
         // tiles cost 8-bit calls more than the length's round trip they hide.
         const bool allowed = !(R::k8bit && kDev && !first);
         if (allowed && bh0 < a.B * a.NH && (kDev || j0 < a.spec_rows) && j0 < nend) {
-            const int per = ceil_div_i(nend - j0, kW);
+            // Segment 0 of the device plan may hold up to kFusedMaxRows rows: wave w takes tile w of
+            // the first kW tiles now, and tile w of the next kW once the length shows it has rows
+            // (segment lambda below); every other guess splits the nominal rows over the waves.
+            constexpr int kTileRows = kRowsPerLoad<DT> * kU;
+            const int per = first ? kTileRows : ceil_div_i(nend - j0, kW);
             g_w0 = min(j0 + wave * per, nend);
             g_w1 = min(g_w0 + per, nend);
             g_j0 = j0;
@@ -1161,9 +1165,19 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                                                            fr, a.kv_out, a.kv_scale_out, cur, m, l, acc);
                 } else {
                     sl = make_slot<DT>(a.kv, a.kv_scale, a.B, a.NH, a.maxT, bh, slice);
+                    // Device-planned segment 0 beyond its first kW tiles (128 < length <= 256): this
+                    // wave's second tile, kW tiles further on, requested before the first is consumed.
+                    constexpr int kTileRows = kRowsPerLoad<DT> * kU;
+                    int x0 = 0, x1 = 0;
+                    Tile<DT, kU> tx;
                     if (spec && (!kDev || (j0 == spec_j0 && j1 <= spec_end))) {
+                        if (kDev && j0 == 0 && designated_base_rows(a.B * a.NH) < kFusedMaxRows) {
+                            x0 = w0 + kW * kTileRows;
+                            x1 = min(x0 + kTileRows, j1);
+                        }
                         w1 = min(w1, j1);
                         if (kDev && !spec_tile && w0 < w1) load_tile<DT, kU, true>(t0, sl, w0, w1, slot_row);
+                        if (kDev && x0 < x1) load_tile<DT, kU, true>(tx, sl, x0, x1, slot_row);
                     } else {
                         const int per_wave = ceil_div_i(j1 - j0, kW);
                         w0 = min(j0 + wave * per_wave, j1);
@@ -1175,6 +1189,8 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                     if constexpr (kFresh)
                         fd = fresh_dst(a.kv_out, a.kv_scale_out, a.B, a.NH, a.maxT, bh, slice, cur);
                     online_rows_from<DT, kU, kFresh>(t0, q0, sl, w0, w1, slot_row, a.qscale, fr, fd, cur, m, l, acc);
+                    if (kDev && x0 < x1)
+                        online_rows_from<DT, kU, kFresh>(tx, q0, sl, x0, x1, slot_row, a.qscale, fr, fd, cur, m, l, acc);
                 }
 
                 // Combine the row slots of this wave, then the 4 waves.
@@ -1717,12 +1733,7 @@ const void* split_ptr_shape(int mode, bool fresh, bool paged) {
 
 template <int DT>
 const void* split_ptr(int mode, bool lat, bool fresh, bool paged) {
-    if (lat) {
-        // The device-planned designated instance keeps the 64-row tiles: its segment 0 splits
-        // up to kFusedMaxRows rows over its waves from the first request on (one tile each).
-        if (mode == kDesignatedDev) return split_ptr_shape<DT, kWavesLat, kUnrollLat<DT>>(mode, fresh, paged);
-        return split_ptr_shape<DT, kWavesLat, kUnrollSplitLat<DT>>(mode, fresh, paged);
-    }
+    if (lat) return split_ptr_shape<DT, kWavesLat, kUnrollSplitLat<DT>>(mode, fresh, paged);
     return split_ptr_shape<DT, kWaves, kUnroll<DT>>(mode, fresh, paged);
 }
 
