@@ -54,16 +54,15 @@ struct GemvArgs {
     // QKV projection with the KV append in its epilogue (kv != nullptr): out is qkv
     // [B][3][NH][64], and its K and V rows also go to column cur_len of the cache
     // [2][B][NH][maxT][64], in the activation type or (kv_dtype 8-bit) as codes with a row
-    // scale in kv_scale [2][B][NH][maxT].  8-bit rows pass through `stage` (float
-    // [B][2][NH][64]) and `arrivals` (u32 [B][2][NH] at a stride of kArrivalStride words,
-    // zero between calls).
+    // scale in kv_scale [2][B][NH][maxT].  8-bit rows pass through `words` (tagged u64
+    // [B][2][NH][64]), their wait bounded by `polls`.
     uint8_t* kv;
     const int* cur_len;
     int lens_per_seq, NH, maxT;
     int kv_dtype;
     float* kv_scale;
-    float* stage;
-    unsigned* arrivals;
+    unsigned long long* words;
+    int polls;
 };
 
 // The x values one 16-byte weight chunk multiplies: 16 bytes (4 floats or 8 bf16), or 32
@@ -146,7 +145,10 @@ __device__ __forceinline__ float gelu_tanh(float v) {
 }
 
 constexpr int kHd = 64;   // head size of the QKV epilogue
-constexpr int kArrivalStride = 64;   // u32 words between two rows' arrival words (256 bytes)
+constexpr int kHeadRowGroups = kHd / kGemvWaves;   // workgroups of one head row (64 channels, one row per wave)
+// The epilogue of a launch (a template parameter, so that the plain GEMV carries none of it).
+enum GemvEpilogue { kEpiNone = 0, kEpiAppend = 1, kEpiAppend8 = 2 };
+constexpr int kGeluFlag = 1, kXcdLocalFlag = 2;   // bits of the preloaded gelu argument
 
 // Cache row (in units of kHd elements) of part 1 (K) or 2 (V), head h, sequence b at the
 // position being appended: column cur_len, clamped to [0, maxT - 1] as the append does.
@@ -163,14 +165,16 @@ __device__ __forceinline__ size_t cache_row(const GemvArgs& a, int b, int part, 
 // (14 dwords, preloaded into SGPRs at wave launch: the library is built with kernel-argument
 // preloading), so the weight and x loads issue without a scalar load of the argument block.
 // kC: 16-byte chunks per lane and row in one block of the row; kR: rows per wave; kOutF32:
-// out and pre_gelu as float (else bf16).  Rows of more than 64*kC chunks take several blocks
-// (the weights are then read again for each input vector).
-template <int WT, int kC, int kR, bool kOutF32>
+// out and pre_gelu as float (else bf16); kEpi: the QKV epilogue (GemvEpilogue).  Rows of more
+// than 64*kC chunks take several blocks (the weights are then read again for each input
+// vector).  pk_gelu: bit 0 GELU, bit 1 the XCD-local layout of kEpiAppend8.
+template <int WT, int kC, int kR, bool kOutF32, int kEpi>
 __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(const uint8_t* pk_W, const uint8_t* pk_x,
                                                                   const float* pk_w_scale, const void* pk_bias,
                                                                   int pk_B, int pk_M, int pk_K, void* pk_out,
                                                                   int pk_gelu, GemvArgs a) {
     static_assert(kR * kC <= kGemvMaxRowChunks && (kR == 1 || kR == 4), "weight registers");
+    static_assert(kEpi == kEpiNone || kR == 1, "the QKV epilogue takes one row per wave");
     a.W = pk_W;
     a.x = pk_x;
     a.w_scale = pk_w_scale;
@@ -179,11 +183,14 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(const uint8_t*
     a.M = pk_M;
     a.K = pk_K;
     a.out = pk_out;
-    a.gelu = pk_gelu;
+    a.gelu = pk_gelu & kGeluFlag;
     using F = WFmt<WT>;
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    const int m0 = (blockIdx.x * kGemvWaves + wave) * kR;
-    if (m0 >= a.M) return;   // whole wave; the one barrier (8-bit QKV epilogue, kR = 1) has M % kGemvWaves == 0
+    // kEpiAppend8 with the XCD-local layout: the 16 workgroups of a head row share an XCD.
+    const bool xl = kEpi == kEpiAppend8 && (pk_gelu & kXcdLocalFlag) != 0;
+    const int wg = xl ? xcd_slot(blockIdx.x, kHeadRowGroups) : (int)blockIdx.x;
+    const int m0 = (wg * kGemvWaves + wave) * kR;
+    if (m0 >= a.M) return;   // whole wave (no barrier follows)
     const int nch = a.K * F::kWBytes / 16;
     constexpr int kBlk = kWave * kC;                 // chunks of a row in one block
     const int nblk = (nch + kBlk - 1) / kBlk;
@@ -226,7 +233,7 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(const uint8_t*
         bias[r] = a.bias ? braw : 0.0f;
         ws[r] = F::k8bit ? a.w_scale[mr] : 1.0f;
     }
-    const int len0 = (a.kv ? a.cur_len : reinterpret_cast<const int*>(a.x))[0];   // the QKV epilogue's column
+    const int len0 = kEpi != kEpiNone ? a.cur_len[0] : 0;   // the QKV epilogue's column
     for (int b = 0; b < a.B; ++b) {
         float accr[kR];
 #pragma unroll
@@ -257,7 +264,7 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(const uint8_t*
                 if (a.pre_gelu) store_res<kOutF32>(a.pre_gelu, o, pre);
                 if (a.gelu) pre = gelu_tanh(pre);
                 store_res<kOutF32>(a.out, o, pre);
-                if (kR == 1 && a.kv && a.kv_dtype == (F::kActF32 ? KVATTN_KV_F32 : KVATTN_KV_BF16)) {
+                if constexpr (kEpi == kEpiAppend) {
                     // Output m is channel c of head h of part q/k/v; K and V also land in the cache
                     // row of position cur_len, as the separate append would copy them.
                     const int part = m / (a.NH * kHd);
@@ -268,55 +275,75 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(const uint8_t*
                 }
             }
         }
-        const int m = m0;
-        const float acc = accr[0];
-        if (kR == 1 && a.kv && (a.kv_dtype == KVATTN_KV_INT8 || a.kv_dtype == KVATTN_KV_FP8_E4M3)) {
-            // An 8-bit row's scale needs the amax of the head's 64 channels, which 16
-            // workgroups compute (4 channels each; M = 3*NH*64 is a multiple of 4, so every
-            // wave of the workgroup is here and part/h are the same for all four).  The four
-            // values (the bf16 values the qkv output holds, which the append quantises) meet
-            // in LDS; wave 0 stages them (lanes 0-3, coherent stores), waits for them, and
-            // counts the workgroup in the row's arrival word, which has a 256-byte line of its
-            // own (arrivals of one line serialise at the memory side).  The 16th to arrive
-            // reads the row back, lane c channel c, quantises it with the append's arithmetic
-            // (the same function), and re-arms the word.  s_val is double-buffered by b: a
-            // wave can refill slot b&1 only after the next barrier, which wave 0 reaches after
-            // reading it.
-            __shared__ float s_val[2][kGemvWaves];
+        if constexpr (kEpi == kEpiAppend8) {
+            // An 8-bit row's scale needs the amax of the head's 64 channels, which the 64 waves of
+            // 16 workgroups compute.  Each wave publishes its channel's value (the bf16 value the
+            // qkv output holds, which the append quantises) as a tagged word; the wave of channel
+            // 0 (workgroup 0 of the head row, first in dispatch order) polls the row's 64 words,
+            // lane c channel c, and quantises it with the append's arithmetic (the same
+            // function).  With the XCD-local layout the words stay in the XCD's L2 (plain
+            // stores, agent-scope loads).  The wait is bounded (a.polls rounds): channels still
+            // missing then are computed by this wave itself, row by row with the producers'
+            // arithmetic, so the codes never depend on where or when the producers run.
+            const int m = m0;
             const int part = m / (a.NH * kHd);
             if (part > 0) {
-                const int h = (m - part * a.NH * kHd) / kHd;
-                if (lane == 0) s_val[b & 1][wave] = bf16_to_f32(f32_to_bf16(acc * ws[0] + bias[0]));
-                __syncthreads();
-                if (wave == 0) {
-                    const size_t rid = ((size_t)b * 2 + (part - 1)) * a.NH + h;
-                    const int c0 = m - part * a.NH * kHd - h * kHd;   // channel of wave 0's row
-                    if (lane < kGemvWaves)
-                        __hip_atomic_store(a.stage + rid * kHd + c0 + lane, s_val[b & 1][lane], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-                    wait_vm_stores();   // the staged values have landed (the count is per wave)
-                    unsigned prev = 0;
-                    if (lane == 0)
-                        prev = __hip_atomic_fetch_add(a.arrivals + rid * kArrivalStride, 1u, __ATOMIC_RELAXED,
-                                                      __HIP_MEMORY_SCOPE_AGENT);
-                    prev = __shfl(prev, 0);
-                    if (prev == kHd / kGemvWaves - 1) {
-                        const float x = __hip_atomic_load(a.stage + rid * kHd + lane, __ATOMIC_RELAXED,
-                                                          __HIP_MEMORY_SCOPE_AGENT);
-                        const float amax = wave_max(fabsf(x));
-                        const size_t row = cache_row(a, b, part, h, len0);
-                        if (a.kv_dtype == KVATTN_KV_FP8_E4M3) {
-                            const float scale = amax / kW8Limit<KVATTN_KV_FP8_E4M3>;
-                            a.kv[row * kHd + lane] = w8_code<KVATTN_KV_FP8_E4M3>(x, scale);
-                            if (lane == 0) a.kv_scale[row] = scale;
-                        } else {
-                            const float scale = amax / kW8Limit<KVATTN_KV_INT8>;
-                            a.kv[row * kHd + lane] = w8_code<KVATTN_KV_INT8>(x, scale);
-                            if (lane == 0) a.kv_scale[row] = scale;
+                const int h = (m - part * a.NH * kHd) / kHd, c = m - part * a.NH * kHd - h * kHd;
+                const size_t rid = ((size_t)b * 2 + (part - 1)) * a.NH + h;
+                unsigned long long* row_words = a.words + rid * kHd;
+                const uint32_t tag = call_tag();
+                const float v = bf16_to_f32(f32_to_bf16(accr[0] * ws[0] + bias[0]));
+                if (lane == 0) publish_word(row_words + c, tagged_word(v, tag), xl);
+                if (c == 0) {
+                    unsigned long long wv = 0;
+                    bool ok = false;
+                    for (int r = 0; r < a.polls; ++r) {
+                        wv = get_word(row_words + lane);
+                        ok = word_is(wv, tag);
+                        if (__all(ok)) break;
+                    }
+                    float x = word_value(wv);
+                    unsigned long long missing = __ballot(!ok);
+                    // Fallback: the missing channels, one row at a time (the wave's chunks, the
+                    // same order of sums as the wave that owns the row).
+                    while (missing) {
+                        const int cm = __ffsll((long long)missing) - 1;
+                        missing &= missing - 1;
+                        const int mr = m + cm;
+                        const uint8_t* wrow = a.W + (size_t)mr * row_bytes;
+                        const uint8_t* xb = a.x + (size_t)b * a.K * kActBytes;
+                        float acc = 0.0f;
+                        for (int kb = 0; kb < nblk; ++kb) {
+                            uint4 wr[kC];
+                            XRaw<WT> xq[kC];
+#pragma unroll
+                            for (int i = 0; i < kC; ++i) {
+                                const int ci = min(kb * kBlk + lane + i * kWave, nch - 1);
+                                wr[i] = load16(wrow + (size_t)ci * 16);
+                                xq[i] = load_x<WT>(xb + (size_t)ci * F::kXBytes);
+                            }
+#pragma unroll
+                            for (int i = 0; i < kC; ++i) {
+                                const float d = acc + chunk_dot<WT>(wr[i], xq[i]);
+                                acc = kb * kBlk + lane + i * kWave < nch ? d : acc;
+                            }
                         }
-                        if (lane == 0)
-                            __hip_atomic_store(a.arrivals + rid * kArrivalStride, 0u, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
+                        acc = wave_sum(acc);
+                        const float wsr = F::k8bit ? a.w_scale[mr] : 1.0f;
+                        const float br = a.bias ? load_act<WT>(a.bias, mr) : 0.0f;
+                        const float vr = bf16_to_f32(f32_to_bf16(acc * wsr + br));
+                        x = lane == cm ? vr : x;
+                    }
+                    const float amax = wave_max(fabsf(x));
+                    const size_t row = cache_row(a, b, part, h, len0);
+                    if (a.kv_dtype == KVATTN_KV_FP8_E4M3) {
+                        const float scale = amax / kW8Limit<KVATTN_KV_FP8_E4M3>;
+                        a.kv[row * kHd + lane] = w8_code<KVATTN_KV_FP8_E4M3>(x, scale);
+                        if (lane == 0) a.kv_scale[row] = scale;
+                    } else {
+                        const float scale = amax / kW8Limit<KVATTN_KV_INT8>;
+                        a.kv[row * kHd + lane] = w8_code<KVATTN_KV_INT8>(x, scale);
+                        if (lane == 0) a.kv_scale[row] = scale;
                     }
                 }
             }
@@ -333,29 +360,41 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(const uint8_t*
 #endif
 constexpr int kGemvTallRows = KVATTN_GEMV_TALL_ROWS;
 
-template <int WT, bool kOut>
+template <int WT, bool kOut, int kEpi>
 const void* gemv_ptr(int chunks_per_lane, int rows) {
-    if (rows == 4) {
-        if (chunks_per_lane <= 1) return (const void*)&gemv_kernel<WT, 1, 4, kOut>;
-        if (chunks_per_lane <= 2) return (const void*)&gemv_kernel<WT, 2, 4, kOut>;
-        return (const void*)&gemv_kernel<WT, 4, 4, kOut>;
+    if constexpr (kEpi == kEpiNone) {
+        if (rows == 4) {
+            if (chunks_per_lane <= 1) return (const void*)&gemv_kernel<WT, 1, 4, kOut, kEpi>;
+            if (chunks_per_lane <= 2) return (const void*)&gemv_kernel<WT, 2, 4, kOut, kEpi>;
+            return (const void*)&gemv_kernel<WT, 4, 4, kOut, kEpi>;
+        }
     }
-    if (chunks_per_lane <= 1) return (const void*)&gemv_kernel<WT, 1, 1, kOut>;
-    if (chunks_per_lane <= 2) return (const void*)&gemv_kernel<WT, 2, 1, kOut>;
-    if (chunks_per_lane <= 4) return (const void*)&gemv_kernel<WT, 4, 1, kOut>;
-    if (chunks_per_lane <= 8) return (const void*)&gemv_kernel<WT, 8, 1, kOut>;
-    return (const void*)&gemv_kernel<WT, kGemvMaxChunks, 1, kOut>;
+    if (chunks_per_lane <= 1) return (const void*)&gemv_kernel<WT, 1, 1, kOut, kEpi>;
+    if (chunks_per_lane <= 2) return (const void*)&gemv_kernel<WT, 2, 1, kOut, kEpi>;
+    if (chunks_per_lane <= 4) return (const void*)&gemv_kernel<WT, 4, 1, kOut, kEpi>;
+    if (chunks_per_lane <= 8) return (const void*)&gemv_kernel<WT, 8, 1, kOut, kEpi>;
+    return (const void*)&gemv_kernel<WT, kGemvMaxChunks, 1, kOut, kEpi>;
 }
 
+// The QKV epilogue writes qkv in the activation type, so only the plain GEMV takes another
+// output type.
 template <int WT>
-const void* gemv_ptr_out(int chunks_per_lane, int rows, bool out_f32) {
-    return out_f32 ? gemv_ptr<WT, true>(chunks_per_lane, rows) : gemv_ptr<WT, false>(chunks_per_lane, rows);
+const void* gemv_ptr_out(int chunks_per_lane, int rows, bool out_f32, int epi) {
+    constexpr bool kAct = WFmt<WT>::kActF32;
+    if (epi == kEpiAppend) return gemv_ptr<WT, kAct, kEpiAppend>(chunks_per_lane, 1);
+    if (epi == kEpiAppend8) {
+        if constexpr (kAct) return nullptr;   // 8-bit caches sit behind bf16 activations
+        else return gemv_ptr<WT, false, kEpiAppend8>(chunks_per_lane, 1);
+    }
+    return out_f32 ? gemv_ptr<WT, true, kEpiNone>(chunks_per_lane, rows)
+                   : gemv_ptr<WT, false, kEpiNone>(chunks_per_lane, rows);
 }
 
 }  // namespace
 
 namespace kvattn_internal {
 void set_last_hip_error(int e);   // kvattn.hip: read back by kvattn_last_hip_error
+int merge_poll_limit();           // kvattn.hip: kvattn_set_merge_poll_limit's bound
 }
 
 namespace {
@@ -381,22 +420,31 @@ int launch_gemv(GemvArgs a, int w_dtype, bool out_f32, void* stream) {
         return KVATTN_ERR_MISALIGNED;
     const int nch = K * wbytes / 16;
     const int per_lane = (nch + kWave - 1) / kWave;
-    // The QKV epilogue needs one row per wave (its workgroups meet per four channels).
     // Measured at 50304 x 768 (per call, graph of calls over weights beyond the Infinity
     // Cache): 4 rows per wave 9.2 / 13.8 / 24.9 us (INT8 / BF16 / FP32), 8 rows 9.8 / 15.5 /
-    // 24.9, one row 16.8 / 19.0 / 26.6.
+    // 24.9, one row 16.8 / 19.0 / 26.6.  The QKV epilogue takes one row per wave.
     const int rows = a.kv || M < kGemvTallRows ? 1 : 4;
+    const bool kv8 = a.kv && (a.kv_dtype == KVATTN_KV_INT8 || a.kv_dtype == KVATTN_KV_FP8_E4M3);
+    const int epi = !a.kv ? kEpiNone : (kv8 ? kEpiAppend8 : kEpiAppend);
     const void* fn = nullptr;
     switch (w_dtype) {
-        case KVATTN_KV_F32: fn = gemv_ptr_out<KVATTN_KV_F32>(per_lane, rows, out_f32); break;
-        case KVATTN_KV_BF16: fn = gemv_ptr_out<KVATTN_KV_BF16>(per_lane, rows, out_f32); break;
-        case KVATTN_KV_INT8: fn = gemv_ptr_out<KVATTN_KV_INT8>(per_lane, rows, out_f32); break;
-        default: fn = gemv_ptr_out<KVATTN_KV_FP8_E4M3>(per_lane, rows, out_f32); break;
+        case KVATTN_KV_F32: fn = gemv_ptr_out<KVATTN_KV_F32>(per_lane, rows, out_f32, epi); break;
+        case KVATTN_KV_BF16: fn = gemv_ptr_out<KVATTN_KV_BF16>(per_lane, rows, out_f32, epi); break;
+        case KVATTN_KV_INT8: fn = gemv_ptr_out<KVATTN_KV_INT8>(per_lane, rows, out_f32, epi); break;
+        default: fn = gemv_ptr_out<KVATTN_KV_FP8_E4M3>(per_lane, rows, out_f32, epi); break;
     }
-    const long long waves = ((long long)M + rows - 1) / rows;
-    void* params[] = {&a.W, &a.x, &a.w_scale, &a.bias, &a.B, &a.M, &a.K, &a.out, &a.gelu, &a};
-    const hipError_t e = hipLaunchKernel(fn, dim3((unsigned)((waves + kGemvWaves - 1) / kGemvWaves)),
-                                         dim3(kGemvWaves * kWave), params, 0, (hipStream_t)stream);
+    if (!fn) return KVATTN_ERR_DTYPE;
+    long long groups = ((M + rows - 1) / rows + kGemvWaves - 1) / kGemvWaves;
+    int flags = a.gelu ? kGeluFlag : 0;
+    // 8-bit epilogue: the 16 workgroups of each of the 3*NH head rows on one XCD, once there are
+    // enough head rows to give every XCD one (the grid is padded to whole rounds of 8).
+    if (epi == kEpiAppend8 && 3 * a.NH >= 8) {
+        groups = 8ll * ((3 * a.NH + 7) / 8) * kHeadRowGroups;
+        flags |= kXcdLocalFlag;
+    }
+    void* params[] = {&a.W, &a.x, &a.w_scale, &a.bias, &a.B, &a.M, &a.K, &a.out, &flags, &a};
+    const hipError_t e = hipLaunchKernel(fn, dim3((unsigned)groups), dim3(kGemvWaves * kWave), params, 0,
+                                         (hipStream_t)stream);
     if (e != hipSuccess) {
         kvattn_internal::set_last_hip_error((int)e);
         return KVATTN_ERR_HIP;
@@ -409,7 +457,7 @@ int launch_gemv(GemvArgs a, int w_dtype, bool out_f32, void* stream) {
 extern "C" int kvattn_gemv(void* out, void* pre_gelu, const void* W, const float* w_scale, const void* x,
                            const void* bias, int B, int M, int K, int w_dtype, int gelu, void* stream) {
     GemvArgs a{out, pre_gelu, (const uint8_t*)W, w_scale, (const uint8_t*)x, bias, B, M, K, gelu ? 1 : 0,
-               nullptr, nullptr, 0, 0, 0, 0, nullptr, nullptr, nullptr};
+               nullptr, nullptr, 0, 0, 0, 0, nullptr, nullptr, 0};
     return launch_gemv(a, w_dtype, w_dtype == KVATTN_KV_F32, stream);
 }
 
@@ -418,14 +466,14 @@ extern "C" int kvattn_gemv_ex(void* out, void* pre_gelu, const void* W, const fl
                               void* stream) {
     if (out_dtype != KVATTN_KV_F32 && out_dtype != KVATTN_KV_BF16) return KVATTN_ERR_DTYPE;
     GemvArgs a{out, pre_gelu, (const uint8_t*)W, w_scale, (const uint8_t*)x, bias, B, M, K, gelu ? 1 : 0,
-               nullptr, nullptr, 0, 0, 0, 0, nullptr, nullptr, nullptr};
+               nullptr, nullptr, 0, 0, 0, 0, nullptr, nullptr, 0};
     return launch_gemv(a, w_dtype, out_dtype == KVATTN_KV_F32, stream);
 }
 
 extern "C" size_t kvattn_gemv_qkv_append_workspace_bytes(int B, int NH) {
     if (B < 1 || NH < 1 || (long long)B * NH > (1ll << 24)) return 0;
-    const size_t rows = (size_t)B * 2 * NH;
-    return rows * kHd * sizeof(float) + rows * kArrivalStride * sizeof(unsigned);
+    const size_t rows = (size_t)B * 2 * NH;   // one tagged word per channel of every appended K and V row
+    return rows * kHd * sizeof(unsigned long long);
 }
 
 extern "C" int kvattn_gemv_qkv_append(void* qkv, const void* W, const float* w_scale, const void* x,
@@ -440,14 +488,12 @@ extern "C" int kvattn_gemv_qkv_append(void* qkv, const void* W, const float* w_s
     const int act = w_dtype == KVATTN_KV_F32 ? KVATTN_KV_F32 : KVATTN_KV_BF16;
     if (!kv8 && kv_dtype != act) return KVATTN_ERR_DTYPE;          // the cache holds the activation type
     if (kv8 && (w_dtype == KVATTN_KV_F32 || !kv_scale)) return KVATTN_ERR_DTYPE;
-    float* stage = nullptr;
-    unsigned* arrivals = nullptr;
+    unsigned long long* words = nullptr;
     if (kv8) {
         const size_t need = kvattn_gemv_qkv_append_workspace_bytes(B, NH);
         if (!workspace || workspace_bytes < need) return KVATTN_ERR_WORKSPACE;
         if (((uintptr_t)workspace & 255u) || ((uintptr_t)kv_scale & 3u)) return KVATTN_ERR_MISALIGNED;
-        stage = (float*)workspace;
-        arrivals = (unsigned*)((uint8_t*)workspace + (size_t)B * 2 * NH * kHd * sizeof(float));
+        words = (unsigned long long*)workspace;
     }
     if (!d_cur_len) {
         int* sym = nullptr;
@@ -456,6 +502,7 @@ extern "C" int kvattn_gemv_qkv_append(void* qkv, const void* W, const float* w_s
         d_cur_len = sym;
     }
     GemvArgs a{qkv, nullptr, (const uint8_t*)W, w_scale, (const uint8_t*)x, bias, B, 3 * NH * hs, K, 0,
-               (uint8_t*)kv_cache, d_cur_len, lens_per_seq ? 1 : 0, NH, maxT, kv_dtype, kv_scale, stage, arrivals};
+               (uint8_t*)kv_cache, d_cur_len, lens_per_seq ? 1 : 0, NH, maxT, kv_dtype, kv_scale, words,
+               kvattn_internal::merge_poll_limit()};
     return launch_gemv(a, w_dtype, w_dtype == KVATTN_KV_F32, stream);
 }

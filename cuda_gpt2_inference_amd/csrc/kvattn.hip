@@ -41,10 +41,6 @@
 #include "kvattn.h"
 #include "lanes.hpp"
 
-// The 64-bit dispatch id of the running kernel dispatch (LLVM's llvm.amdgcn.dispatch.id; it
-// has no clang builtin).  Kernels that call it receive it in two user SGPRs at wave launch.
-extern "C" __device__ unsigned long long kvattn_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
-
 namespace {
 
 constexpr int kHeadDim = 64;
@@ -951,30 +947,10 @@ __device__ __forceinline__ float get(const float* p) {
 // producer only.
 constexpr int kDefaultMergePolls = 1 << 16;  // the designated merger's polls before it computes missing segments
 constexpr int kMlStride = 16;                // u64 words per slot in tag_ml: {max, exp-sum}, one 128-byte line
-__device__ __forceinline__ uint32_t call_tag() { return (uint32_t)kvattn_dispatch_id() | 0x80000000u; }
-__device__ __forceinline__ void publish_word(unsigned long long* p, unsigned long long w, bool xcd_local) {
-    if (xcd_local) *p = w;
-    else __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ unsigned long long get_word(const unsigned long long* p) {
-    return __hip_atomic_load(const_cast<unsigned long long*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ unsigned long long tagged_word(float v, uint32_t tag) {
-    return ((unsigned long long)tag << 32) | __float_as_uint(v);
-}
-__device__ __forceinline__ bool word_is(unsigned long long w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
-__device__ __forceinline__ float word_value(unsigned long long w) { return __uint_as_float((uint32_t)w); }
 
-// XCD placement of a designated grid.  The hardware hands consecutive workgroups of a
-// dispatch to the XCDs in turn (workgroup x to XCD (x + c) % 8, c fixed per dispatch), so
-// workgroups x and x + 8 share an XCD.  Workgroup x works on slot xcd_slot(x, S) of the
-// (b,h)-major slot order: segment s of head 8k + r is workgroup 8 (S k + s) + r.  The grid
-// is 8 * ceil(B*NH / 8) * S workgroups; those of heads beyond B*NH exit at once.
-__host__ __device__ __forceinline__ int xcd_slot(int x, int S) {
-    const int r = x & 7, j = x >> 3;
-    const int k = j / S, s = j - k * S;
-    return ((k << 3) + r) * S + s;
-}
+// XCD placement of a designated grid (xcd_slot, lanes.hpp): segment s of head 8k + r is
+// workgroup 8 (S k + s) + r, so every segment of a head runs on one XCD.  The grid is
+// 8 * ceil(B*NH / 8) * S workgroups; those of heads beyond B*NH exit at once.
 // The layout is used from kXcdLocalHeads heads on: with fewer, whole XCDs would sit idle
 // while the ones holding a head stream all of its bytes; those grids keep the dense slot
 // order, and their producers publish with write-through (sc1) stores, which an agent-scope
@@ -2337,6 +2313,7 @@ int check_partials(const float* po, const float* pl, const float* pm, int S) {
 // Shared with the other translation units of the library (not exported).
 namespace kvattn_internal {
 __attribute__((visibility("hidden"))) void set_last_hip_error(int e) { t_last_hip_error = e; }
+__attribute__((visibility("hidden"))) int merge_poll_limit() { return g_merge_polls.load(std::memory_order_relaxed); }
 }  // namespace kvattn_internal
 
 // ======================================================================================

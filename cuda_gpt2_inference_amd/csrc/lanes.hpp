@@ -7,6 +7,10 @@
 
 #include "kvattn.h"
 
+// The 64-bit dispatch id of the running kernel dispatch (LLVM's llvm.amdgcn.dispatch.id; it
+// has no clang builtin).  Kernels that call it receive it in two user SGPRs at wave launch.
+extern "C" __device__ unsigned long long kvattn_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
+
 namespace {
 
 constexpr int kWave = 64;
@@ -170,6 +174,39 @@ __device__ __forceinline__ uint8_t w8_code(float x, float scale) {
         qv = qv < -127 ? -127 : (qv > 127 ? 127 : qv);
         return (uint8_t)(int8_t)qv;
     }
+}
+
+// ------------------------------------------------------------------------------------
+// Tagged words handed between workgroups: a float in the low half, the call's tag (the
+// dispatch id with the top bit set, so that a zeroed buffer holds no valid word) in the
+// high half.  A word counts only for the dispatch that wrote it, so slots need no clearing.
+// Published with plain stores when writer and reader run on one XCD (the word lands in that
+// XCD's L2, where the reader's agent-scope loads hit it), else with write-through (sc1)
+// stores, which agent-scope loads see from any XCD.
+// ------------------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t call_tag() { return (uint32_t)kvattn_dispatch_id() | 0x80000000u; }
+__device__ __forceinline__ void publish_word(unsigned long long* p, unsigned long long w, bool xcd_local) {
+    if (xcd_local) *p = w;
+    else __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long get_word(const unsigned long long* p) {
+    return __hip_atomic_load(const_cast<unsigned long long*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long tagged_word(float v, uint32_t tag) {
+    return ((unsigned long long)tag << 32) | __float_as_uint(v);
+}
+__device__ __forceinline__ bool word_is(unsigned long long w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
+__device__ __forceinline__ float word_value(unsigned long long w) { return __uint_as_float((uint32_t)w); }
+
+// XCD placement.  The hardware hands consecutive workgroups of a dispatch to the 8 XCDs in
+// turn (workgroup x to XCD (x + c) % 8, c fixed per dispatch), so workgroups x and x + 8
+// share an XCD.  With groups of S consecutive logical workgroups that must share an XCD,
+// workgroup x takes logical index xcd_slot(x, S): member s of group 8k + r is workgroup
+// 8 (S k + s) + r.  A grid of 8 * ceil(groups / 8) * S covers every group.
+__host__ __device__ __forceinline__ int xcd_slot(int x, int S) {
+    const int r = x & 7, j = x >> 3;
+    const int k = j / S, s = j - k * S;
+    return ((k << 3) + r) * S + s;
 }
 
 // s_waitcnt vmcnt(0) (GFX9 encoding: expcnt and lgkmcnt fields left at their maximum),

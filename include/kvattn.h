@@ -337,9 +337,9 @@ int kvattn_gemv_ex(void* out, void* pre_gelu, const void* W, const float* w_scal
  *     kv_scale [2][B][NH][maxT], from the bf16 values in qkv with the append's quantiser.
  *     The 64 channels of a row come from 16 workgroups, so they meet in the workspace:
  *     kvattn_gemv_qkv_append_workspace_bytes(B, NH) bytes, 256-byte aligned, zeroed once
- *     (kvattn_workspace_init); every call re-arms its arrival counters, so the workspace
- *     needs no clearing between calls.  Calls sharing a workspace must be ordered (one
- *     stream).
+ *     (kvattn_workspace_init); each word there carries the call that wrote it, so the
+ *     workspace needs no clearing between calls.  Calls sharing a workspace must be ordered
+ *     (one stream).
  * d_cur_len as in kvattn_decode (NULL: the library's device length).  hs must be 64.
  * Replaces the QKV GEMV followed by the append launch (inference_gpt2_opt.cu:290-303, 329;
  * the append kernels attention_kvcache.cuh:46-64, attention_kvcache_w8.cuh:115-155), one

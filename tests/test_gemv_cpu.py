@@ -172,9 +172,9 @@ def test_gemv_qkv_append_argument_errors(kw, status):
 
 
 def test_gemv_qkv_append_workspace_bytes():
-    """One float per channel of the 2*B*NH staged rows plus one arrival word per row on a
-    256-byte line of its own; 0 for shapes out of range."""
+    """One tagged 8-byte word per channel of the 2*B*NH appended K and V rows; 0 for shapes
+    out of range."""
     from cuda_gpt2_inference_amd import kvattn
     for B, NH in ((1, 12), (3, 12), (64, 16), (1, 1)):
-        assert kvattn.gemv_qkv_append_workspace_bytes(B, NH) == 2 * B * NH * (64 * 4 + 256)
+        assert kvattn.gemv_qkv_append_workspace_bytes(B, NH) == 2 * B * NH * 64 * 8
     assert kvattn.gemv_qkv_append_workspace_bytes(0, 12) == 0

@@ -182,7 +182,7 @@ def test_gemv_qkv_append_equals_gemv_then_append(dev, dtype, kv, lens):
     other row; for 8-bit caches the codes and the row scales), at GPT-2's QKV shape (NH = 12:
     2304 x 768), with one device length, per-sequence lengths (one of them beyond maxT,
     clamped), and the library's own length.  8-bit caches run two calls in a row on one
-    workspace, so the second finds the arrival words re-armed by the first."""
+    workspace, so the second must not take the words the first staged there."""
     import torch
     kvattn = _kv()
     NH, HS, K, maxT = 12, 64, 768, 96
@@ -234,17 +234,12 @@ def test_gemv_qkv_append_equals_gemv_then_append(dev, dtype, kv, lens):
         if w8:
             assert torch.equal(s_a.view(torch.int32), s_b.view(torch.int32)), f"{tag}: row scales"
         assert not torch.equal(c_a.view(cview), cache.view(cview)), f"{tag}: nothing appended"
-    if w8:
-        # The arrival words (after the staged rows, one per 256 bytes) are back at zero.
-        off = 2 * B * NH * HS * 4
-        arrivals = ws[off:off + 2 * B * NH * 256].view(torch.int32)
-        assert int(arrivals.abs().sum()) == 0, f"{dtype} {kv} {lens}: arrival words left armed"
 
 
 @pytest.mark.parametrize("kv", ["int8", "fp8"])
 def test_gemv_qkv_append_8bit_graph_replays(dev, kv):
-    """The 8-bit QKV epilogue captured in a graph: its arrival words are re-armed by the
-    kernel itself (no memset node), so every replay must quantise afresh.  Three replays
+    """The 8-bit QKV epilogue captured in a graph: its staged words carry the dispatch that
+    wrote them (no memset node), so every replay must quantise afresh.  Three replays
     with new inputs and eager work in between, each against kvattn_gemv +
     kvattn_cache_write on a copy of the cache: qkv, codes and row scales bit for bit."""
     import torch
@@ -287,3 +282,48 @@ def test_gemv_qkv_append_8bit_graph_replays(dev, kv):
         assert torch.equal(qkv.view(torch.int16), q_ref.view(torch.int16)), f"{kv} replay {rep}: qkv"
         assert torch.equal(cache, c_ref), f"{kv} replay {rep}: codes"
         assert torch.equal(kscale.view(torch.int32), s_ref.view(torch.int32)), f"{kv} replay {rep}: row scales"
+
+
+@pytest.mark.parametrize("kv", ["int8", "fp8"])
+def test_gemv_qkv_append_8bit_fallback_and_dense_layout(dev, kv):
+    """The 8-bit QKV epilogue (a) with its quantising wave's wait forced to give up from the
+    host (poll bound 0: it computes every channel of its head row itself, with the owning
+    waves' arithmetic) and (b) with 2 heads (6 head rows: the dense layout with write-through
+    words instead of the XCD-local one), each against kvattn_gemv + kvattn_cache_write on a
+    copy of the cache: qkv, codes and row scales bit for bit, two calls in a row."""
+    import torch
+    kvattn = _kv()
+    HS, K, maxT, B = 64, 768, 48, 2
+    for NH, bound in ((12, 0), (2, None), (2, 0)):
+        M = 3 * NH * HS
+        d, _ = _make("int8", B, M, K, seed=93 + NH)
+        W, scale = d["W"].to(dev), d["scale"].to(dev)
+        bias = d["bias"].to(dev)
+        x = d["x"].to(dev).contiguous()
+        cur = torch.tensor([3, 30], dtype=torch.int32, device=dev)
+        ws_bytes = kvattn.gemv_qkv_append_workspace_bytes(B, NH)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        kvattn.workspace_init(ws, ws_bytes)
+        cache = torch.zeros(2 * B * NH * maxT * HS, dtype=torch.uint8, device=dev)
+        kscale = torch.zeros(2 * B * NH * maxT, device=dev)
+        qkv = torch.empty(B * M, dtype=torch.bfloat16, device=dev)
+        for call in range(2):
+            cur.add_(call)
+            c_ref, s_ref = cache.clone(), kscale.clone()
+            q_ref = torch.empty_like(qkv)
+            kvattn.gemv(q_ref, W, x, B, M, K, w_dtype="int8", w_scale=scale, bias=bias)
+            kvattn.kv_cache_write(c_ref, q_ref, B, NH, HS, maxT, kv_dtype=kv, kv_scale=s_ref, cur_len=cur,
+                                  lens_per_seq=True)
+            prev = kvattn.set_merge_poll_limit(bound) if bound is not None else None
+            try:
+                kvattn.gemv_qkv_append(qkv, W, x, B, NH, HS, K, cache, maxT, w_dtype="int8", kv_dtype=kv,
+                                       w_scale=scale, bias=bias, kv_scale=kscale, cur_len=cur, lens_per_seq=True,
+                                       workspace=ws, workspace_nbytes=ws_bytes)
+                torch.cuda.synchronize()
+            finally:
+                if prev is not None:
+                    kvattn.set_merge_poll_limit(prev)
+            what = f"NH={NH} bound={bound} call {call}"
+            assert torch.equal(qkv.view(torch.int16), q_ref.view(torch.int16)), what + ": qkv"
+            assert torch.equal(cache, c_ref), what + ": codes"
+            assert torch.equal(kscale.view(torch.int32), s_ref.view(torch.int32)), what + ": row scales"
