@@ -551,6 +551,33 @@ def test_designated_merger_workspace_reuse(dev):
         assert_close(out.float().cpu().numpy(), case.reference(), "bf16", f"call {i} {strategy} S={S}")
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "int8"])
+@pytest.mark.parametrize("B,NH", [(1, 7), (1, 8), (3, 3), (1, 12), (17, 1), (2, 12), (5, 8)])
+def test_designated_head_counts_around_the_xcd_layout(dev, dtype, B, NH):
+    """From 8 (b,h) rows the designated grid places each row's segments on one XCD and pads
+    the grid to whole groups of 8 rows (the padding workgroups exit); below 8 it keeps the
+    dense order.  Row counts 7, 8, 9, 12, 17, 24 and 40 with ragged lengths, planned on the
+    host (hint 1024), on the device (no hint) and with 16 explicit segments, each against
+    the oracle, with the workspace status left at zero."""
+    import torch
+    kvattn = _kv()
+    maxT = 1024
+    lens = np.array([1, 37, 256, 257, 700, 1024, 513], np.int32)
+    totals = lens[np.arange(B) % len(lens)]
+    case = make_case(dtype, B, NH, maxT, totals - 1, seed=1100 + 10 * B + NH)
+    ref = case.reference()
+    for len_hint, S in ((maxT - 1, 0), (-1, 0), (maxT - 1, 16)):
+        got = _run(case, dev, "designated", S=S, len_hint=len_hint)
+        assert_close(got, ref, dtype, f"designated B={B} NH={NH} hint={len_hint} S={S}")
+    ws = kvattn.Workspace(B, NH, maxT, 16)
+    qkv, cache, scale, cur = to_device(case, dev)
+    out = out_tensor(case, dev)
+    kvattn.decode(out, qkv, cache, B, NH, HS, maxT, kv_dtype=dtype, kv_scale=scale, cur_len=cur,
+                  lens_per_seq=True, S=16, strategy="designated", **ws.kwargs())
+    torch.cuda.synchronize()
+    assert ws.status() == 0
+
+
 def test_designated_merger_grid_beyond_residency(dev):
     """An explicit designated plan whose grid exceeds what the GPU holds at once (12,288
     workgroups) is refused: its mergers wait for producers that would have to be dispatched
