@@ -730,13 +730,8 @@ __global__ __launch_bounds__(kThreads) void fused_single_kernel(
     }
 
     l = slot_reduce<R::kLanes, false>(l);
-#pragma unroll
-    for (int e = 0; e < R::kElems; ++e) acc[e] = slot_reduce<R::kLanes, false>(acc[e]);
     if (lane == 0) s_l[wave] = l;
-    if (slot_row == 0) {
-#pragma unroll
-        for (int e = 0; e < R::kElems; ++e) s_acc[wave][slice * R::kElems + e] = acc[e];
-    }
+    s_acc[wave][slice * R::kElems + slot_row] = slot_reduce_scatter<R::kLanes, R::kElems>(acc);
     __syncthreads();
     if (threadIdx.x < kHeadDim) {
         const int c = threadIdx.x;
@@ -1174,12 +1169,9 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                 const float f = exp2_fast(m - mw);
                 l = slot_reduce<R::kLanes, false>(l * f);
 #pragma unroll
-                for (int e = 0; e < R::kElems; ++e) acc[e] = slot_reduce<R::kLanes, false>(acc[e] * f);
+                for (int e = 0; e < R::kElems; ++e) acc[e] *= f;
                 if (lane == 0) { s_m[wave] = mw; s_l[wave] = l; }
-                if (slot_row == 0) {
-#pragma unroll
-                    for (int e = 0; e < R::kElems; ++e) s_acc[wave][slice * R::kElems + e] = acc[e];
-                }
+                s_acc[wave][slice * R::kElems + slot_row] = slot_reduce_scatter<R::kLanes, R::kElems>(acc);
                 __syncthreads();
                 if (wave == 0) {
                     float Mb = s_m[0];
@@ -1251,21 +1243,40 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                             }
                             // Merge this wave's partial (segment 0) and the producers' partials, in
                             // segment order, with merge_partials' arithmetic.
+                            // Lanes from n on hold -FLT_MAX and 0, so with up to 8 (16) segments the
+                            // reductions stop after the first 8 (16) lanes: the same steps, the same
+                            // result, a shorter chain of dependent instructions.
                             const float pm = lane == 0 ? Mb * kLn2 : (need ? word_value(wm) : kEmptyMax);
                             const float pl = lane == 0 ? L : (need ? word_value(wl) : 0.0f);
-                            const float Mx = wave_max(pm);
-                            const float LL = wave_sum(exp2_fast((pm - Mx) * kLog2e) * pl);
+                            float Mx, Ls;
+                            if (n <= 8) {
+                                Mx = row_max<8>(pm);
+                                Ls = row_sum<8>(exp2_fast((pm - Mx) * kLog2e) * pl);
+                            } else if (n <= 16) {
+                                Mx = row_max<16>(pm);
+                                Ls = row_sum<16>(exp2_fast((pm - Mx) * kLog2e) * pl);
+                            } else {
+                                Mx = wave_max(pm);
+                                Ls = wave_sum(exp2_fast((pm - Mx) * kLog2e) * pl);
+                            }
+                            const float LL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(Ls), 0));
                             const float e = exp2_fast((pm - Mx) * kLog2e);
+                            // The first batch (segments 1 .. 16) arrived with the poll; later batches
+                            // (more than 17 segments) are polled for in a loop of their own, which keeps
+                            // its address arithmetic off the common path.
                             float O = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), 0)) * A;
-                            for (int k = 1; k < n && !lost; k += kBatch) {
-                                if (k > 1) {
-                                    for (int r = 0;; ++r) {
-                                        if (r >= a.merge_polls) { lost = true; break; }
-                                        load_batch(k, w);
-                                        if (__all(batch_ok(w))) break;
-                                    }
-                                    if (lost) break;
+#pragma unroll
+                            for (int u = 0; u < kBatch; ++u)
+                                if (1 + u < n)
+                                    O = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), 1 + u)),
+                                             word_value(w[u]), O);
+                            for (int k = 1 + kBatch; k < n && !lost; k += kBatch) {
+                                for (int r = 0;; ++r) {
+                                    if (r >= a.merge_polls) { lost = true; break; }
+                                    load_batch(k, w);
+                                    if (__all(batch_ok(w))) break;
                                 }
+                                if (lost) break;
 #pragma unroll
                                 for (int u = 0; u < kBatch; ++u)
                                     if (k + u < n)

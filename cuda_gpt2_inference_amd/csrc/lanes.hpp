@@ -22,12 +22,13 @@ __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w 
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
-// float -> bfloat16 bits, round to nearest even; NaN stays a quiet NaN.
+// float -> bfloat16 bits, round to nearest even; NaN stays a quiet NaN.  Written as a select
+// rather than an early return, so that it compiles without a branch.
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
+    const uint32_t u = __float_as_uint(f);
+    const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    const uint32_t quiet = (u >> 16) | 0x40u;
+    return (uint16_t)((u & 0x7fffffffu) > 0x7f800000u ? quiet : rounded);
 }
 
 // Sixteen 8-bit codes of one 16-byte chunk as floats: FP8 through the hardware OCP E4M3
@@ -71,6 +72,7 @@ constexpr int kDppRowRor4 = 0x124;    // rotate 16-lane row by 4
 constexpr int kDppRowRor8 = 0x128;    // rotate 16-lane row by 8
 constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i inside each 8-lane half row
 constexpr int kDppRowMirror = 0x140;  // lane i <-> 15-i inside each 16-lane row
+constexpr int kDppQuadRev = 0x1B;     // quad_perm [3,2,1,0]
 
 template <int kCtrl>
 __device__ __forceinline__ float dpp(float x) {
@@ -114,6 +116,60 @@ __device__ __forceinline__ float slot_reduce(float x) {
     x = op_xor16<kMax>(x);
     x = op_xor32<kMax>(x);
     return x;
+}
+
+// Maximum over aligned groups of kLanes (4, 8 or 16) lanes: the first steps of wave_max, so
+// that a group whose other lanes hold -FLT_MAX gets wave_max's result bit for bit.
+template <int kLanes>
+__device__ __forceinline__ float row_max(float x) {
+    x = fmaxf(x, dpp<kDppQuadXor1>(x));
+    x = fmaxf(x, dpp<kDppQuadXor2>(x));
+    if constexpr (kLanes >= 8) x = fmaxf(x, dpp<kDppHalfMirror>(x));
+    if constexpr (kLanes >= 16) x = fmaxf(x, dpp<kDppRowMirror>(x));
+    return x;
+}
+
+// Reduce-scatter over the row slots of a wave.  Lane = slot * kLanes + slice holds, for its
+// row slot, kElems values: elements 0 .. kElems-1 of its slice.  There are as many row slots
+// as elements (64 / kLanes = kElems), so afterwards each lane returns one sum over all row
+// slots: element `slot` of its slice, channel slice * kElems + slot.  Each step pairs lanes that
+// differ in one slot bit; the lane with the bit clear keeps the lower half of its values, its
+// partner the upper half, and each adds the half that its partner sends.  permlane32_swap and
+// permlane16_swap of (lower, upper) hand both operands of those sums over in one instruction
+// (the lane with the bit clear receives its partner's lower half, and the partner the upper);
+// inside a 16-lane row, row_ror:8 pairs lanes 8 apart, and a quad reversal followed by a
+// half-row mirror pairs lanes 4 apart.
+template <int kLanes, int kElems>
+__device__ __forceinline__ float slot_reduce_scatter(float (&a)[kElems]) {
+    static_assert(kLanes * kElems == kWave && kElems >= 4 && kElems <= 16, "one channel per lane");
+    const int lane = threadIdx.x & (kWave - 1);
+    constexpr int h32 = kElems / 2, h16 = kElems / 4, h8 = kElems / 8, h4 = kElems / 16;
+#pragma unroll
+    for (int i = 0; i < h32; ++i) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a[i]), __float_as_uint(a[h32 + i]), false,
+                                                        false);
+        a[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+#pragma unroll
+    for (int i = 0; i < h16; ++i) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a[i]), __float_as_uint(a[h16 + i]), false,
+                                                        false);
+        a[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    if constexpr (h8 > 0) {
+        const bool hi = (lane & 8) != 0;
+#pragma unroll
+        for (int i = 0; i < h8; ++i) {
+            const float send = hi ? a[i] : a[h8 + i];
+            a[i] = (hi ? a[h8 + i] : a[i]) + dpp<kDppRowRor8>(send);
+        }
+    }
+    if constexpr (h4 > 0) {
+        const bool hi = (lane & 4) != 0;
+        const float send = hi ? a[0] : a[1];
+        a[0] = (hi ? a[1] : a[0]) + dpp<kDppHalfMirror>(dpp<kDppQuadRev>(send));
+    }
+    return a[0];
 }
 
 __device__ __forceinline__ float wave_max(float x) {
