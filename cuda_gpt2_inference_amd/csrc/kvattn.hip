@@ -140,14 +140,28 @@ __device__ __forceinline__ void decode(const uint4& d, float (&x)[Row<DT>::kElem
     }
 }
 
+// A lane's share of a score: q slice . row chunk.  BF16 rows take the hardware bf16 dot
+// (v_dot2_f32_bf16: two bf16 products, exact in fp32, added to an fp32 accumulator) on the
+// packed q pairs that convert_q leaves in q[0..3], then the scale in q[4].
+typedef __bf16 Bf16x2 __attribute__((ext_vector_type(2)));
 template <int DT>
 __device__ __forceinline__ float dot_chunk(const float (&q)[Row<DT>::kElems], const uint4& d) {
-    float x[Row<DT>::kElems];
-    decode<DT>(d, x);
-    float s = 0.0f;
+    if constexpr (DT == KVATTN_KV_BF16) {
+        auto pair = [](uint32_t u) { return __builtin_bit_cast(Bf16x2, u); };
+        auto qp = [&](int i) { return pair(__float_as_uint(q[i])); };
+        float s = __builtin_amdgcn_fdot2_f32_bf16(pair(d.x), qp(0), 0.0f, false);
+        s = __builtin_amdgcn_fdot2_f32_bf16(pair(d.y), qp(1), s, false);
+        s = __builtin_amdgcn_fdot2_f32_bf16(pair(d.z), qp(2), s, false);
+        s = __builtin_amdgcn_fdot2_f32_bf16(pair(d.w), qp(3), s, false);
+        return s * q[4];
+    } else {
+        float x[Row<DT>::kElems];
+        decode<DT>(d, x);
+        float s = 0.0f;
 #pragma unroll
-    for (int e = 0; e < Row<DT>::kElems; ++e) s = fmaf(q[e], x[e], s);
-    return s;
+        for (int e = 0; e < Row<DT>::kElems; ++e) s = fmaf(q[e], x[e], s);
+        return s;
+    }
 }
 
 // Attended positions of sequence b: device length clamped to [0, maxT-1], plus one.
@@ -175,10 +189,19 @@ __device__ __forceinline__ QRaw<DT> load_q(const void* qkv, int b, int h, int NH
     return r;
 }
 
-// q as float, multiplied by scale*log2(e) so dot products come out in base-2 units.
+// q as float, multiplied by scale*log2(e) so dot products come out in base-2 units.  BF16
+// caches keep q as the raw packed bf16 pairs in q[0..3] (bit patterns) and the scale in q[4]:
+// dot_chunk takes the hardware bf16 dot and scales the lane's sum.
 template <int DT>
 __device__ __forceinline__ void convert_q(const QRaw<DT>& r, float qscale, float (&q)[Row<DT>::kElems]) {
-    if constexpr (Row<DT>::kActF32) {
+    if constexpr (DT == KVATTN_KV_BF16) {
+        q[0] = __uint_as_float(r.w[0].x);
+        q[1] = __uint_as_float(r.w[0].y);
+        q[2] = __uint_as_float(r.w[0].z);
+        q[3] = __uint_as_float(r.w[0].w);
+        q[4] = qscale;
+        q[5] = q[6] = q[7] = 0.0f;
+    } else if constexpr (Row<DT>::kActF32) {
         q[0] = __uint_as_float(r.w[0].x) * qscale;
         q[1] = __uint_as_float(r.w[0].y) * qscale;
         q[2] = __uint_as_float(r.w[0].z) * qscale;
