@@ -140,13 +140,15 @@ __device__ __forceinline__ void decode(const uint4& d, float (&x)[Row<DT>::kElem
     }
 }
 
-// A lane's share of a score: q slice . row chunk.  BF16 rows take the hardware bf16 dot
-// (v_dot2_f32_bf16: two bf16 products, exact in fp32, added to an fp32 accumulator) on the
-// packed q pairs that convert_q leaves in q[0..3], then the scale in q[4].
+// A lane's share of a score: q slice . row chunk.  kHw (the latency-bound kernels): BF16
+// rows take the hardware bf16 dot (v_dot2_f32_bf16: two bf16 products, exact in fp32, added
+// to an fp32 accumulator) on the packed q pairs that convert_q<DT, true> leaves in q[0..3],
+// then the scale in q[4].  The streaming kernel keeps the fma form: measured, the dot costs
+// its 64-sequence call 2 % (A/B, both the one-chain and the two-chain form).
 typedef __bf16 Bf16x2 __attribute__((ext_vector_type(2)));
-template <int DT>
+template <int DT, bool kHw = false>
 __device__ __forceinline__ float dot_chunk(const float (&q)[Row<DT>::kElems], const uint4& d) {
-    if constexpr (DT == KVATTN_KV_BF16) {
+    if constexpr (kHw && DT == KVATTN_KV_BF16) {
         auto pair = [](uint32_t u) { return __builtin_bit_cast(Bf16x2, u); };
         auto qp = [&](int i) { return pair(__float_as_uint(q[i])); };
         float s = __builtin_amdgcn_fdot2_f32_bf16(pair(d.x), qp(0), 0.0f, false);
@@ -189,12 +191,12 @@ __device__ __forceinline__ QRaw<DT> load_q(const void* qkv, int b, int h, int NH
     return r;
 }
 
-// q as float, multiplied by scale*log2(e) so dot products come out in base-2 units.  BF16
-// caches keep q as the raw packed bf16 pairs in q[0..3] (bit patterns) and the scale in q[4]:
-// dot_chunk takes the hardware bf16 dot and scales the lane's sum.
-template <int DT>
+// q as float, multiplied by scale*log2(e) so dot products come out in base-2 units.  With
+// kHw, BF16 caches keep q as the raw packed bf16 pairs in q[0..3] (bit patterns) and the
+// scale in q[4]: dot_chunk<DT, true> takes the hardware bf16 dot and scales the lane's sum.
+template <int DT, bool kHw = false>
 __device__ __forceinline__ void convert_q(const QRaw<DT>& r, float qscale, float (&q)[Row<DT>::kElems]) {
-    if constexpr (DT == KVATTN_KV_BF16) {
+    if constexpr (kHw && DT == KVATTN_KV_BF16) {
         q[0] = __uint_as_float(r.w[0].x);
         q[1] = __uint_as_float(r.w[0].y);
         q[2] = __uint_as_float(r.w[0].z);
@@ -416,7 +418,7 @@ __device__ __forceinline__ void mask_tile_v(Tile<DT, U>& t, int r, int r1, int s
     }
 }
 
-template <int DT, int U, bool kChecked>
+template <int DT, int U, bool kChecked, bool kHw = false>
 __device__ __forceinline__ void consume_tile(const Tile<DT, U>& t, int r, int r1, int slot_row,
                                              const float (&q)[Row<DT>::kElems], float& m, float& l,
                                              float (&acc)[Row<DT>::kElems]) {
@@ -426,7 +428,7 @@ __device__ __forceinline__ void consume_tile(const Tile<DT, U>& t, int r, int r1
     float mt = m;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        s[u] = row_sum<R::kLanes>(dot_chunk<DT>(q, t.k[u]));
+        s[u] = row_sum<R::kLanes>(dot_chunk<DT, kHw>(q, t.k[u]));
         if constexpr (R::k8bit) s[u] *= t.ks[u];
         if (kChecked && r + u * kRPL + slot_row >= r1) s[u] = -INFINITY;
         mt = fmaxf(mt, s[u]);
@@ -455,7 +457,7 @@ __device__ __forceinline__ void consume_tile(const Tile<DT, U>& t, int r, int r1
 // rows of that tile at or beyond r1 are masked.  The q slice is requested after the tile's
 // K/V loads, so nothing that depends on q is scheduled ahead of them.  kFresh: the row
 // `cur` (if inside [r0, r1)) is taken from f instead of the cache.
-template <int DT, int kU, bool kFresh>
+template <int DT, int kU, bool kFresh, bool kHw = false>
 __device__ __forceinline__ void online_rows_from(Tile<DT, kU>& t0, const QRaw<DT>& qr,
                                                  const Slot& sl, int r0, int r1, int slot_row, float qscale,
                                                  const FreshRaw<DT>& fr, const FreshDst& fd, int cur,
@@ -463,22 +465,22 @@ __device__ __forceinline__ void online_rows_from(Tile<DT, kU>& t0, const QRaw<DT
     constexpr int kTile = kRowsPerLoad<DT> * kU;
     if (r0 >= r1) return;
     float q[Row<DT>::kElems];
-    convert_q<DT>(qr, qscale, q);
+    convert_q<DT, kHw>(qr, qscale, q);
     // Only the wave whose rows [r, min(r + kTile, r1)) contain cur patches (and stores).
     auto holds = [&](int r) { return kFresh && cur >= r && cur < min(r + kTile, r1); };
     if (holds(r0)) patch_tile<DT, kU>(t0, fr, fd, r0, slot_row, cur);
-    consume_tile<DT, kU, true>(t0, r0, r1, slot_row, q, m, l, acc);
+    consume_tile<DT, kU, true, kHw>(t0, r0, r1, slot_row, q, m, l, acc);
     Tile<DT, kU> t;
     int r = r0 + kTile;
     for (; r + kTile <= r1; r += kTile) {
         load_tile<DT, kU, false>(t, sl, r, r1, slot_row);
         if (holds(r)) patch_tile<DT, kU>(t, fr, fd, r, slot_row, cur);
-        consume_tile<DT, kU, false>(t, r, r1, slot_row, q, m, l, acc);
+        consume_tile<DT, kU, false, kHw>(t, r, r1, slot_row, q, m, l, acc);
     }
     if (r < r1) {
         load_tile<DT, kU, true>(t, sl, r, r1, slot_row);
         if (holds(r)) patch_tile<DT, kU>(t, fr, fd, r, slot_row, cur);
-        consume_tile<DT, kU, true>(t, r, r1, slot_row, q, m, l, acc);
+        consume_tile<DT, kU, true, kHw>(t, r, r1, slot_row, q, m, l, acc);
     }
 }
 
@@ -513,7 +515,7 @@ __device__ __forceinline__ Slot page_slot(const PagedView& pv, int page, int h, 
 
 // Online softmax over rows [j0, j1) of (b, h) (j0 a multiple of kTile) by one wave of kW.
 // kFresh: the row `cur` is taken from fr and written through the table.
-template <int DT, int kU, int kW, bool kFresh>
+template <int DT, int kU, int kW, bool kFresh, bool kHw = false>
 __device__ __forceinline__ void online_tiles_paged(const PagedView& pv, int b, int h, int j0, int j1, int wave,
                                                    int slot_row, int slice, const QRaw<DT>& qr, float qscale,
                                                    const FreshRaw<DT>& fr, uint8_t* kv_out, float* kv_scale_out,
@@ -525,7 +527,7 @@ __device__ __forceinline__ void online_tiles_paged(const PagedView& pv, int b, i
     const int tr = j0 + (wave + lane * kW) * kTile;     // first row of this lane's tile
     const int pid = tr < j1 ? row_table[tr / P] : -1;
     float q[Row<DT>::kElems];
-    convert_q<DT>(qr, qscale, q);
+    convert_q<DT, kHw>(qr, qscale, q);
     Tile<DT, kU> t;
     int i = 0;
     for (int r = j0 + wave * kTile; r < j1; r += kW * kTile, ++i) {
@@ -545,11 +547,11 @@ __device__ __forceinline__ void online_tiles_paged(const PagedView& pv, int b, i
         if (r + kTile <= j1) {
             load_tile<DT, kU, false>(t, sp, r - pr0, j1 - pr0, slot_row);
             fresh();
-            consume_tile<DT, kU, false>(t, r - pr0, j1 - pr0, slot_row, q, m, l, acc);
+            consume_tile<DT, kU, false, kHw>(t, r - pr0, j1 - pr0, slot_row, q, m, l, acc);
         } else {
             load_tile<DT, kU, true>(t, sp, r - pr0, j1 - pr0, slot_row);
             fresh();
-            consume_tile<DT, kU, true>(t, r - pr0, j1 - pr0, slot_row, q, m, l, acc);
+            consume_tile<DT, kU, true, kHw>(t, r - pr0, j1 - pr0, slot_row, q, m, l, acc);
         }
     }
 }
@@ -558,7 +560,7 @@ __device__ __forceinline__ void online_tiles_paged(const PagedView& pv, int b, i
 // fused_single: one workgroup per (b,h), grid B*NH.  Pass 1 writes every score to LDS
 // and finds the exact maximum; pass 2 weights V with exp2(score - max).
 // ------------------------------------------------------------------------------------
-template <int DT, int U, bool kChecked, bool kFresh>
+template <int DT, int U, bool kChecked, bool kFresh, bool kHw = false>
 __device__ __forceinline__ void score_tile(const Slot& sl, int r, int total, int slot_row, int slice,
                                            const float (&q)[Row<DT>::kElems], float* scores, float& mloc,
                                            const FreshRaw<DT>& fr, const FreshDst& fd) {
@@ -592,7 +594,7 @@ __device__ __forceinline__ void score_tile(const Slot& sl, int r, int total, int
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        float s = row_sum<R::kLanes>(dot_chunk<DT>(q, kd[u]));
+        float s = row_sum<R::kLanes>(dot_chunk<DT, kHw>(q, kd[u]));
         if constexpr (R::k8bit) s *= ks[u];
         const int row = r + u * kRPL + slot_row;
         if (!kChecked || row < total) {
@@ -700,7 +702,7 @@ __global__ __launch_bounds__(kThreads) void fused_single_kernel(
             load_tile<DT, kU, true>(t, sl, r, total, slot_row);
             qr = load_q<DT>(qkv, b, h, NH, slice);
         }
-        convert_q<DT>(qr, qscale, q);
+        convert_q<DT, true>(qr, qscale, q);
         if (kFresh && cur >= r && cur < r + kTile) patch_tile<DT, kU>(t, fr, fd, r, slot_row, cur);
         // A tile requested for a longer hinted length holds rows at or beyond `total`.
         mask_tile_v<DT, kU>(t, r, total, slot_row);
@@ -708,7 +710,7 @@ __global__ __launch_bounds__(kThreads) void fused_single_kernel(
         float mloc = kStartMax;
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
-            s[u] = row_sum<R::kLanes>(dot_chunk<DT>(q, t.k[u]));
+            s[u] = row_sum<R::kLanes>(dot_chunk<DT, true>(q, t.k[u]));
             if constexpr (R::k8bit) s[u] *= t.ks[u];
             if (r + u * kRPL + slot_row < total) mloc = fmaxf(mloc, s[u]);
             else s[u] = -INFINITY;
@@ -732,13 +734,13 @@ __global__ __launch_bounds__(kThreads) void fused_single_kernel(
     } else {
         // Scores staged in LDS.  Pass 1: tiles of kTile rows go round-robin to the waves,
         // every score is written to LDS and the exact maximum is found.
-        convert_q<DT>(load_q<DT>(qkv, b, h, NH, slice), qscale, q);
+        convert_q<DT, true>(load_q<DT>(qkv, b, h, NH, slice), qscale, q);
         float mloc = kStartMax;
         const int full = total / kTile * kTile;
         for (int r = wave * kTile; r < full; r += kW * kTile)
-            score_tile<DT, kU, false, kFresh>(sl, r, total, slot_row, slice, q, s_scores, mloc, fr, fd);
+            score_tile<DT, kU, false, kFresh, true>(sl, r, total, slot_row, slice, q, s_scores, mloc, fr, fd);
         for (int r = full + wave * kTile; r < total; r += kW * kTile)
-            score_tile<DT, kU, true, kFresh>(sl, r, total, slot_row, slice, q, s_scores, mloc, fr, fd);
+            score_tile<DT, kU, true, kFresh, true>(sl, r, total, slot_row, slice, q, s_scores, mloc, fr, fd);
         mloc = wave_max(mloc);
         if (lane == 0) s_max[wave] = mloc;
         __syncthreads();
@@ -1046,6 +1048,8 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
     a.spec_rows = pk_spec < 0 ? 0 : pk_spec;
     a.qscale = kQScale;
     using R = Row<DT>;
+    // The latency shape (tiles of KVATTN_SPLIT_LAT_ROWS rows) takes the hardware bf16 dot.
+    constexpr bool kHwDot = kU == kUnrollSplitLat<DT>;
     __shared__ float s_m[kW];
     __shared__ float s_l[kW];
     __shared__ float s_acc[kW][kHeadDim];
@@ -1155,7 +1159,8 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                     q0 = load_q<DT>(a.qkv, it.b, it.h, a.NH, slice);
                     if constexpr (kFresh) fr = load_fresh<DT>(a.qkv, it.b, it.h, a.NH, slice);
                     pv = PagedView{a.kv, a.kv_scale, a.table, a.max_pages, a.page_rows, a.num_pages, a.NH};
-                    online_tiles_paged<DT, kU, kW, kFresh>(pv, it.b, it.h, j0, j1, wave, slot_row, slice, q0, a.qscale,
+                    online_tiles_paged<DT, kU, kW, kFresh, kHwDot>(pv, it.b, it.h, j0, j1, wave, slot_row, slice, q0,
+                                                                   a.qscale,
                                                            fr, a.kv_out, a.kv_scale_out, cur, m, l, acc);
                 } else {
                     sl = make_slot<DT>(a.kv, a.kv_scale, a.B, a.NH, a.maxT, bh, slice);
@@ -1182,9 +1187,11 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                     }
                     if constexpr (kFresh)
                         fd = fresh_dst(a.kv_out, a.kv_scale_out, a.B, a.NH, a.maxT, bh, slice, cur);
-                    online_rows_from<DT, kU, kFresh>(t0, q0, sl, w0, w1, slot_row, a.qscale, fr, fd, cur, m, l, acc);
+                    online_rows_from<DT, kU, kFresh, kHwDot>(t0, q0, sl, w0, w1, slot_row, a.qscale, fr, fd, cur, m, l,
+                                                             acc);
                     if (kDev && x0 < x1)
-                        online_rows_from<DT, kU, kFresh>(tx, q0, sl, x0, x1, slot_row, a.qscale, fr, fd, cur, m, l, acc);
+                        online_rows_from<DT, kU, kFresh, kHwDot>(tx, q0, sl, x0, x1, slot_row, a.qscale, fr, fd, cur, m,
+                                                                 l, acc);
                 }
 
                 // Combine the row slots of this wave, then the 4 waves.
@@ -1322,14 +1329,14 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                                     if (sj1 > sj0) {
                                         if constexpr (kPaged) {
                                             for (int w2 = 0; w2 < kW; ++w2)
-                                                online_tiles_paged<DT, kU, kW, kFresh>(
+                                                online_tiles_paged<DT, kU, kW, kFresh, kHwDot>(
                                                     pv, it.b, it.h, sj0, sj1, w2, slot_row, slice, q0, a.qscale, fr,
                                                     a.kv_out, a.kv_scale_out, cur, mm, ll, ac);
                                         } else {
                                             Tile<DT, kU> tf;
                                             load_tile<DT, kU, true>(tf, sl, sj0, sj1, slot_row);
-                                            online_rows_from<DT, kU, kFresh>(tf, q0, sl, sj0, sj1, slot_row, a.qscale,
-                                                                             fr, fd, cur, mm, ll, ac);
+                                            online_rows_from<DT, kU, kFresh, kHwDot>(tf, q0, sl, sj0, sj1, slot_row,
+                                                                                     a.qscale, fr, fd, cur, mm, ll, ac);
                                         }
                                     }
                                     const float mw2 = slot_reduce<R::kLanes, true>(mm);
