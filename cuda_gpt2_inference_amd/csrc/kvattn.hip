@@ -1084,7 +1084,7 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
     int g_w0 = 0, g_w1 = 0, g_j0 = 0, g_end = 0;
     if (!kPaged && kMode != kPartialsStrided && !a.lens_per_seq && (kDev || a.seg_rows > 0)) {
         const int nom = kDev ? designated_base_rows(a.B * a.NH) : a.seg_rows;
-        const int bh0 = vbx / a.S;   // beyond B * NH only in a designated grid padded to whole XCD rounds
+        const int bh0 = div_uniform(vbx, a.S);   // beyond B * NH only in a designated grid padded to whole XCD rounds
         const int j0 = (vbx - bh0 * a.S) * nom;
         const bool first = kDev && j0 == 0 && nom < kFusedMaxRows;
         const int nend = min(j0 + (first ? kFusedMaxRows : nom), a.maxT);
@@ -1102,9 +1102,12 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
             g_j0 = j0;
             g_end = nend;
             g_has_tile = !first || g_w1 <= j0 + nom;
-            const int b0 = bh0 / a.NH;
             const Slot sl0 = make_slot<DT>(a.kv, a.kv_scale, a.B, a.NH, a.maxT, bh0, slice);
             if (g_has_tile) load_tile<DT, kU, true>(g_tile, sl0, g_w0, g_w1, slot_row);
+            // The sequence index (a division by NH) is needed only for q's address: keep it
+            // behind the tile's requests.
+            __builtin_amdgcn_sched_barrier(0);
+            const int b0 = a.B == 1 ? 0 : bh0 / a.NH;
             g_q = load_q<DT>(a.qkv, b0, bh0 - b0 * a.NH, a.NH, slice);
             if constexpr (kFresh) g_fresh = load_fresh<DT>(a.qkv, b0, bh0 - b0 * a.NH, a.NH, slice);
             g_on = true;

@@ -259,9 +259,16 @@ __device__ __forceinline__ float word_value(unsigned long long w) { return __uin
 // share an XCD.  With groups of S consecutive logical workgroups that must share an XCD,
 // workgroup x takes logical index xcd_slot(x, S): member s of group 8k + r is workgroup
 // 8 (S k + s) + r.  A grid of 8 * ceil(groups / 8) * S covers every group.
+// x / d for x >= 0 and a wave-uniform d > 0: a shift when d is a power of two (the planned
+// segment counts are), else the division.  Integer division by a run-time value expands to
+// ~25 instructions, which at kernel start delay the first K/V request.
+__host__ __device__ __forceinline__ int div_uniform(int x, int d) {
+    return (d & (d - 1)) == 0 ? x >> __builtin_ctz((unsigned)d) : x / d;
+}
+
 __host__ __device__ __forceinline__ int xcd_slot(int x, int S) {
     const int r = x & 7, j = x >> 3;
-    const int k = j / S, s = j - k * S;
+    const int k = div_uniform(j, S), s = j - k * S;
     return ((k << 3) + r) * S + s;
 }
 
