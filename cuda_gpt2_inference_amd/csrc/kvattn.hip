@@ -668,7 +668,7 @@ __global__ __launch_bounds__(kThreads) void fused_single_kernel(
     __shared__ float s_acc[kW][kHeadDim];
 
     const int bh = blockIdx.x;
-    const int b = bh / NH, h = bh - b * NH;
+    const int b = B == 1 ? 0 : bh / NH, h = bh - b * NH;   // the grid is B * NH: bh < NH when B == 1
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int slot_row = lane / R::kLanes, slice = lane % R::kLanes;
     const Slot sl = make_slot<DT>(kv, kv_scale, B, NH, maxT, bh, slice);
@@ -715,7 +715,7 @@ __global__ __launch_bounds__(kThreads) void fused_single_kernel(
             if (r + u * kRPL + slot_row < total) mloc = fmaxf(mloc, s[u]);
             else s[u] = -INFINITY;
         }
-        mloc = wave_max(mloc);
+        mloc = slot_reduce<R::kLanes, true>(mloc);   // a row's lanes hold the same scores
         if (lane == 0) s_max[wave] = mloc;
         __syncthreads();
         float M = s_max[0];
@@ -741,7 +741,7 @@ __global__ __launch_bounds__(kThreads) void fused_single_kernel(
             score_tile<DT, kU, false, kFresh, true>(sl, r, total, slot_row, slice, q, s_scores, mloc, fr, fd);
         for (int r = full + wave * kTile; r < total; r += kW * kTile)
             score_tile<DT, kU, true, kFresh, true>(sl, r, total, slot_row, slice, q, s_scores, mloc, fr, fd);
-        mloc = wave_max(mloc);
+        mloc = slot_reduce<R::kLanes, true>(mloc);   // a row's lanes hold the same scores
         if (lane == 0) s_max[wave] = mloc;
         __syncthreads();
         float M = s_max[0];
