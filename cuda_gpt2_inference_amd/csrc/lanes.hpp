@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include "kvattn.h"
+#include "layout.hpp"
 
 // The 64-bit dispatch id of the running kernel dispatch (LLVM's llvm.amdgcn.dispatch.id; it
 // has no clang builtin).  Kernels that call it receive it in two user SGPRs at wave launch.
@@ -254,23 +255,8 @@ __device__ __forceinline__ unsigned long long tagged_word(float v, uint32_t tag)
 __device__ __forceinline__ bool word_is(unsigned long long w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
 __device__ __forceinline__ float word_value(unsigned long long w) { return __uint_as_float((uint32_t)w); }
 
-// XCD placement.  The hardware hands consecutive workgroups of a dispatch to the 8 XCDs in
-// turn (workgroup x to XCD (x + c) % 8, c fixed per dispatch), so workgroups x and x + 8
-// share an XCD.  With groups of S consecutive logical workgroups that must share an XCD,
-// workgroup x takes logical index xcd_slot(x, S): member s of group 8k + r is workgroup
-// 8 (S k + s) + r.  A grid of 8 * ceil(groups / 8) * S covers every group.
-// x / d for x >= 0 and a wave-uniform d > 0: a shift when d is a power of two (the planned
-// segment counts are), else the division.  Integer division by a run-time value expands to
-// ~25 instructions, which at kernel start delay the first K/V request.
-__host__ __device__ __forceinline__ int div_uniform(int x, int d) {
-    return (d & (d - 1)) == 0 ? x >> __builtin_ctz((unsigned)d) : x / d;
-}
-
-__host__ __device__ __forceinline__ int xcd_slot(int x, int S) {
-    const int r = x & 7, j = x >> 3;
-    const int k = div_uniform(j, S), s = j - k * S;
-    return ((k << 3) + r) * S + s;
-}
+using kvattn_layout::div_uniform;
+using kvattn_layout::xcd_slot;
 
 // s_waitcnt vmcnt(0) (GFX9 encoding: expcnt and lgkmcnt fields left at their maximum),
 // fenced against compiler reordering on both sides.
