@@ -513,19 +513,29 @@ __device__ __forceinline__ Slot page_slot(const PagedView& pv, int page, int h, 
     return s;
 }
 
+// Page ids of one wave's tiles of rows [j0, j1) of sequence b: lane i gets the page of the
+// wave's tile i (tiles go round-robin to the kW waves), -1 past j1.
+template <int DT, int kU, int kW>
+__device__ __forceinline__ int paged_tile_ids(const PagedView& pv, int b, int j0, int j1, int wave) {
+    constexpr int kTile = kRowsPerLoad<DT> * kU;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int tr = j0 + (wave + lane * kW) * kTile;     // first row of this lane's tile
+    return tr < j1 ? pv.table[(size_t)b * pv.max_pages + tr / pv.page_rows] : -1;
+}
+
 // Online softmax over rows [j0, j1) of (b, h) (j0 a multiple of kTile) by one wave of kW.
 // kFresh: the row `cur` is taken from fr and written through the table.
 template <int DT, int kU, int kW, bool kFresh, bool kHw = false>
 __device__ __forceinline__ void online_tiles_paged(const PagedView& pv, int b, int h, int j0, int j1, int wave,
                                                    int slot_row, int slice, const QRaw<DT>& qr, float qscale,
                                                    const FreshRaw<DT>& fr, uint8_t* kv_out, float* kv_scale_out,
-                                                   int cur, float& m, float& l, float (&acc)[Row<DT>::kElems]) {
+                                                   int cur, float& m, float& l, float (&acc)[Row<DT>::kElems],
+                                                   int pid_in = -1, bool have_pid = false) {
     constexpr int kTile = kRowsPerLoad<DT> * kU;
-    const int lane = threadIdx.x & (kWave - 1);
     const int P = pv.page_rows;
-    const int* row_table = pv.table + (size_t)b * pv.max_pages;
-    const int tr = j0 + (wave + lane * kW) * kTile;     // first row of this lane's tile
-    const int pid = tr < j1 ? row_table[tr / P] : -1;
+    // Lane i: the page of this wave's tile i (requested here, or earlier by the caller:
+    // paged_tile_ids with the same arguments).
+    const int pid = have_pid ? pid_in : paged_tile_ids<DT, kU, kW>(pv, b, j0, j1, wave);
     float q[Row<DT>::kElems];
     convert_q<DT, kHw>(qr, qscale, q);
     Tile<DT, kU> t;
@@ -1119,9 +1129,11 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
     // parameters (spec: made; spec_tile: holds this wave's tile; [spec_j0, spec_end): its
     // nominal range), so that the strided loop below passes an empty one and carries no
     // tile from one segment to the next.
+    // pid_in / have_pid (paged caches): this wave's page ids for the segment, requested
+    // earlier by the caller (paged_tile_ids), or not.
     auto segment = [&](const Item& it, const bool active, Tile<DT, kU>& t0, QRaw<DT>& q0, FreshRaw<DT>& fr,
                        const bool spec, const bool spec_tile, int w0, int w1, const int spec_j0,
-                       const int spec_end) {
+                       const int spec_end, const int pid_in = -1, const bool have_pid = false) {
         const int bh = it.b * a.NH + it.h;
         const size_t pidx = (size_t)bh * a.S + it.s;
         constexpr bool kCoh = kMode == kLastBlockMerge || kMode == kCoopMerge;
@@ -1163,8 +1175,8 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                     if constexpr (kFresh) fr = load_fresh<DT>(a.qkv, it.b, it.h, a.NH, slice);
                     pv = PagedView{a.kv, a.kv_scale, a.table, a.max_pages, a.page_rows, a.num_pages, a.NH};
                     online_tiles_paged<DT, kU, kW, kFresh, kHwDot>(pv, it.b, it.h, j0, j1, wave, slot_row, slice, q0,
-                                                                   a.qscale,
-                                                           fr, a.kv_out, a.kv_scale_out, cur, m, l, acc);
+                                                                   a.qscale, fr, a.kv_out, a.kv_scale_out, cur, m, l,
+                                                                   acc, pid_in, have_pid);
                 } else {
                     sl = make_slot<DT>(a.kv, a.kv_scale, a.B, a.NH, a.maxT, bh, slice);
                     // Device-planned segment 0 beyond its first kW tiles (128 < length <= 256): this
@@ -1466,7 +1478,7 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
         }
         __syncthreads();
         const int count = s_seg_end[a.B - 1];
-        for (int x = blockIdx.x; x < count; x += gridDim.x) {
+        auto item_at = [&](int x) {
             Item it;
             int b = -1;
             for (int b0 = 0; b < 0; b0 += kWave) {
@@ -1480,10 +1492,30 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
             const int local = x - (b > 0 ? s_seg_end[b - 1] : 0);
             it.h = local / it.n_seg;
             it.s = local - it.h * it.n_seg;
+            return it;
+        };
+        // Paged caches: the page ids of the workgroup's next segment are requested before the
+        // current one is worked on, so that its first tiles wait for one round trip, not two.
+        int pid_next = -1;
+        bool have_next = false;
+        for (int x = blockIdx.x; x < count; x += gridDim.x) {
+            const Item it = item_at(x);
+            const int pid_now = pid_next;
+            const bool have_now = have_next;
+            have_next = false;
+            if constexpr (kPaged) {
+                if (x + (int)gridDim.x < count) {
+                    const Item nx = item_at(x + (int)gridDim.x);
+                    const int nj0 = nx.s * nx.rows;
+                    const PagedView npv{a.kv, a.kv_scale, a.table, a.max_pages, a.page_rows, a.num_pages, a.NH};
+                    pid_next = paged_tile_ids<DT, kU, kW>(npv, nx.b, nj0, min(nj0 + nx.rows, nx.total), wave);
+                    have_next = true;
+                }
+            }
             Tile<DT, kU> t;
             QRaw<DT> q;
             FreshRaw<DT> f{};
-            segment(it, true, t, q, f, false, true, 0, 0, 0, 0);
+            segment(it, true, t, q, f, false, true, 0, 0, 0, 0, pid_now, have_now);
             __syncthreads();   // the next segment reuses s_m, s_l, s_acc
         }
     } else {
