@@ -37,6 +37,7 @@
 #include <map>
 #include <mutex>
 #include <tuple>
+#include <type_traits>
 
 #include "kvattn.h"
 #include "lanes.hpp"
@@ -1258,75 +1259,85 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                             if (lane < n) seg_range(lane, uj0, uj1);
                             const bool need = lane >= 1 && lane < n && uj1 > uj0 && !lost;
                             const unsigned long long prod = __ballot(need);   // segments a producer publishes
-                            const unsigned long long kHave = (unsigned long long)tag << 32;  // a slot not waited for
-                            // Channel words of up to 16 segments per batch; the first batch is
-                            // requested together with the maxima and exp-sums, so up to 17
-                            // segments merge after one memory round trip.
-                            constexpr int kBatch = 16;
-                            auto load_batch = [&](int k, unsigned long long (&w)[kBatch]) {
-#pragma unroll
-                                for (int u = 0; u < kBatch; ++u)
-                                    w[u] = k + u < n && ((prod >> (k + u)) & 1ull)
-                                               ? get_word(a.tag_out + (p0 + k + u) * kHeadDim + lane)
-                                               : kHave;
-                            };
-                            auto batch_ok = [&](const unsigned long long (&w)[kBatch]) {
-                                bool ok = true;
-#pragma unroll
-                                for (int u = 0; u < kBatch; ++u) ok = ok && word_is(w[u], tag);
-                                return ok;
-                            };
-                            unsigned long long wm = kHave, wl = kHave, w[kBatch];
-                            for (int r = 0; !lost; ++r) {
-                                if (r >= a.merge_polls) { lost = true; break; }
-                                if (need) {
-                                    wm = get_word(a.tag_ml + kMlStride * (p0 + lane));
-                                    wl = get_word(a.tag_ml + kMlStride * (p0 + lane) + 1);
-                                }
-                                load_batch(1, w);
-                                if (__all(word_is(wm, tag) && word_is(wl, tag) && batch_ok(w))) break;
-                            }
-                            // Merge this wave's partial (segment 0) and the producers' partials, in
-                            // segment order, with merge_partials' arithmetic.
-                            // Lanes from n on hold -FLT_MAX and 0, so with up to 8 (16) segments the
-                            // reductions stop after the first 8 (16) lanes: the same steps, the same
-                            // result, a shorter chain of dependent instructions.
-                            const float pm = lane == 0 ? Mb * kLn2 : (need ? word_value(wm) : kEmptyMax);
-                            const float pl = lane == 0 ? L : (need ? word_value(wl) : 0.0f);
-                            float Mx, Ls;
-                            if (n <= 8) {
-                                Mx = row_max<8>(pm);
-                                Ls = row_sum<8>(exp2_fast((pm - Mx) * kLog2e) * pl);
-                            } else if (n <= 16) {
-                                Mx = row_max<16>(pm);
-                                Ls = row_sum<16>(exp2_fast((pm - Mx) * kLog2e) * pl);
-                            } else {
-                                Mx = wave_max(pm);
-                                Ls = wave_sum(exp2_fast((pm - Mx) * kLog2e) * pl);
-                            }
-                            const float LL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(Ls), 0));
-                            const float e = exp2_fast((pm - Mx) * kLog2e);
-                            // The first batch (segments 1 .. 16) arrived with the poll; later batches
-                            // (more than 17 segments) are polled for in a loop of their own, which keeps
-                            // its address arithmetic off the common path.
-                            float O = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), 0)) * A;
-#pragma unroll
-                            for (int u = 0; u < kBatch; ++u)
-                                if (1 + u < n)
-                                    O = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), 1 + u)),
-                                             word_value(w[u]), O);
-                            for (int k = 1 + kBatch; k < n && !lost; k += kBatch) {
+                            // Channel words of up to 16 segments per batch (8 when there are at most
+                            // 8 segments); the first batch is requested together with the maxima and
+                            // exp-sums, so up to 17 segments merge after one memory round trip.  A
+                            // poll round has no branch: every word is requested (slots past the last
+                            // one clamped to it) and the check masks what nothing is published for
+                            // (lane 0's own slot, empty segments, slots past n).
+                            const int last = n - 1;   // n >= 2 here
+                            float O = 0.0f, LL = 1.0f;
+                            auto merge_batches = [&](auto batch) {
+                                constexpr int kB = decltype(batch)::value;
+                                const size_t ml = (size_t)kMlStride * (p0 + min(lane, last));
+                                unsigned long long wm, wl, w[kB];
                                 for (int r = 0;; ++r) {
-                                    if (r >= a.merge_polls) { lost = true; break; }
-                                    load_batch(k, w);
-                                    if (__all(batch_ok(w))) break;
-                                }
-                                if (lost) break;
+                                    if (r >= a.merge_polls) { lost = true; return; }
+                                    wm = get_word(a.tag_ml + ml);
+                                    wl = get_word(a.tag_ml + ml + 1);
 #pragma unroll
-                                for (int u = 0; u < kBatch; ++u)
-                                    if (k + u < n)
-                                        O = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), k + u)),
+                                    for (int u = 0; u < kB; ++u)
+                                        w[u] = get_word(a.tag_out + (p0 + min(1 + u, last)) * kHeadDim + lane);
+                                    uint32_t bad = need ? (((uint32_t)(wm >> 32) ^ tag) | ((uint32_t)(wl >> 32) ^ tag))
+                                                        : 0u;
+#pragma unroll
+                                    for (int u = 0; u < kB; ++u)
+                                        bad |= ((prod >> (1 + u)) & 1ull) ? ((uint32_t)(w[u] >> 32) ^ tag) : 0u;
+                                    if (__all(bad == 0u)) break;
+                                }
+                                // Merge this wave's partial (segment 0) and the producers' partials,
+                                // in segment order, with merge_partials' arithmetic.  Lanes from n on
+                                // hold -FLT_MAX and 0, so with up to 8 (16) segments the reductions stop
+                                // after the first 8 (16) lanes: the same steps, the same result, a
+                                // shorter chain of dependent instructions.
+                                const float pm = lane == 0 ? Mb * kLn2 : (need ? word_value(wm) : kEmptyMax);
+                                const float pl = lane == 0 ? L : (need ? word_value(wl) : 0.0f);
+                                float Mx, Ls;
+                                if (n <= 8) {
+                                    Mx = row_max<8>(pm);
+                                    Ls = row_sum<8>(exp2_fast((pm - Mx) * kLog2e) * pl);
+                                } else if (n <= 16) {
+                                    Mx = row_max<16>(pm);
+                                    Ls = row_sum<16>(exp2_fast((pm - Mx) * kLog2e) * pl);
+                                } else {
+                                    Mx = wave_max(pm);
+                                    Ls = wave_sum(exp2_fast((pm - Mx) * kLog2e) * pl);
+                                }
+                                LL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(Ls), 0));
+                                const float e = exp2_fast((pm - Mx) * kLog2e);
+                                O = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), 0)) * A;
+#pragma unroll
+                                for (int u = 0; u < kB; ++u)
+                                    if (1 + u < n)
+                                        O = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), 1 + u)),
                                                  word_value(w[u]), O);
+                                // Later batches (more than 17 segments), each polled for in turn.
+                                if constexpr (kB == 16) {
+                                    for (int k = 1 + kB; k < n; k += kB) {
+                                        for (int r = 0;; ++r) {
+                                            if (r >= a.merge_polls) { lost = true; return; }
+#pragma unroll
+                                            for (int u = 0; u < kB; ++u)
+                                                w[u] = get_word(a.tag_out + (p0 + min(k + u, last)) * kHeadDim + lane);
+                                            uint32_t bad2 = 0u;
+#pragma unroll
+                                            for (int u = 0; u < kB; ++u)
+                                                bad2 |= (k + u < n && ((prod >> (k + u)) & 1ull))
+                                                            ? ((uint32_t)(w[u] >> 32) ^ tag) : 0u;
+                                            if (__all(bad2 == 0u)) break;
+                                        }
+#pragma unroll
+                                        for (int u = 0; u < kB; ++u)
+                                            if (k + u < n)
+                                                O = fmaf(__int_as_float(
+                                                             __builtin_amdgcn_readlane(__float_as_int(e), k + u)),
+                                                         word_value(w[u]), O);
+                                    }
+                                }
+                            };
+                            if (!lost) {
+                                if (n <= 8) merge_batches(std::integral_constant<int, 8>{});
+                                else merge_batches(std::integral_constant<int, 16>{});
                             }
                             float res = O / LL;
                             if (lost) {
