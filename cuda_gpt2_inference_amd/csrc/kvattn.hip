@@ -1304,13 +1304,16 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                                     Ls = wave_sum(exp2_fast((pm - Mx) * kLog2e) * pl);
                                 }
                                 LL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(Ls), 0));
+                                // Words of slots nothing is published for (empty segments, slots past
+                                // n, whose clamped words may be stale) enter as 0, so the fold of the
+                                // first batch needs no branch and no stale value reaches it; their
+                                // weights are finite, so they drop out exactly.
                                 const float e = exp2_fast((pm - Mx) * kLog2e);
                                 O = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), 0)) * A;
 #pragma unroll
                                 for (int u = 0; u < kB; ++u)
-                                    if (1 + u < n)
-                                        O = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), 1 + u)),
-                                                 word_value(w[u]), O);
+                                    O = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), 1 + u)),
+                                             ((prod >> (1 + u)) & 1ull) ? word_value(w[u]) : 0.0f, O);
                                 // Later batches (more than 17 segments), each polled for in turn.
                                 if constexpr (kB == 16) {
                                     for (int k = 1 + kB; k < n; k += kB) {
@@ -1331,7 +1334,7 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                                             if (k + u < n)
                                                 O = fmaf(__int_as_float(
                                                              __builtin_amdgcn_readlane(__float_as_int(e), k + u)),
-                                                         word_value(w[u]), O);
+                                                         ((prod >> (k + u)) & 1ull) ? word_value(w[u]) : 0.0f, O);
                                     }
                                 }
                             };

@@ -179,6 +179,35 @@ def test_designated_fallback_matches_oracle_and_workspace_stays_usable(dev, dtyp
         assert ws.status() == 0
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_designated_empty_segments_ignore_stale_words(dev, dtype):
+    """The reference partition leaves segments empty when the length is short (10 positions
+    over 8 segments: segments 5..7).  Their slots publish nothing, so they still hold the words
+    of an earlier call: here NaN partials, from a call whose V rows are all NaN.  The merger
+    requests every slot of its batch and must drop those words by more than a zero weight
+    (0 x NaN is NaN): the second call matches the oracle."""
+    import torch
+    kvattn = _kv()
+    B, NH, maxT, S = 1, 12, 1024, 8
+    ws = kvattn.Workspace(B, NH, maxT, S)
+    first = make_case(dtype, B, NH, maxT, [maxT - 1], seed=431)
+    qkv, cache, scale, cur = to_device(first, dev)
+    cache.view(2, -1)[1].fill_(float("nan"))
+    out = out_tensor(first, dev)
+    kvattn.decode(out, qkv, cache, B, NH, HS, maxT, kv_dtype=dtype, kv_scale=scale, cur_len=cur, len_hint=maxT - 1,
+                  S=S, strategy="designated", **ws.kwargs())
+    torch.cuda.synchronize()
+    assert torch.isnan(out.float()).all(), "the first call should have published NaN partials"
+    second = make_case(dtype, B, NH, maxT, [9], seed=432)
+    qkv2, cache2, scale2, cur2 = to_device(second, dev)
+    out2 = out_tensor(second, dev)
+    kvattn.decode(out2, qkv2, cache2, B, NH, HS, maxT, kv_dtype=dtype, kv_scale=scale2, cur_len=cur2, len_hint=9,
+                  S=S, strategy="designated", **ws.kwargs())
+    torch.cuda.synchronize()
+    assert_close(out2.float().cpu().numpy(), second.reference(), dtype, "short length after NaN partials")
+    assert ws.status() == 0
+
+
 @pytest.mark.parametrize("dtype", ALL_DT)
 def test_designated_fallback_with_fresh_row_equals_normal_path(dev, dtype):
     """Append and attend in one launch with the merger's fallback forced (poll bound 0): the
