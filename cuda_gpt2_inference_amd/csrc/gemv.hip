@@ -3,14 +3,14 @@
 // tanh GELU, for FP32, BF16 and 8-bit (INT8 / FP8-E4M3 codes with one FP32 scale per row)
 // weights.  The attention output projection consumes the attention output this way.
 //
-// One wave per kR output rows (kR = 1 for the per-layer shapes, 4 for tall matrices such as
+// One wave per kR output rows (kR = 1 for the per-layer shapes, 2 for tall matrices such as
 // the vocabulary projection).  A row of K weights is K*wbytes/16 chunks of 16
 // bytes; lane l holds chunks l, l+64, ... of a block of 64*kC chunks of each of its rows in
 // registers (all requested at once), multiplies them with the matching x chunks of every
 // input vector, and a wave reduction (DPP + permlane) finishes each dot product.  Rows longer
 // than one block loop over blocks.  At GPT-2's per-layer sizes (0.6 to 4.7 MB of weights) a
 // call is bound by launch and memory latency, and one row per wave gives the most waves; a
-// tall matrix (50304 x 768) streams, and 4 rows per wave keep 3-12 KB per wave in flight.
+// tall matrix (50304 x 768) streams, and 2 rows per wave keep 1.5-6 KB per wave in flight.
 // MFMA is not used (B is a handful of decode tokens, 1-2 flops per byte).
 #include <hip/hip_runtime.h>
 #include <math.h>
@@ -173,7 +173,7 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(const uint8_t*
                                                                   const float* pk_w_scale, const void* pk_bias,
                                                                   int pk_B, int pk_M, int pk_K, void* pk_out,
                                                                   int pk_gelu, GemvArgs a) {
-    static_assert(kR * kC <= kGemvMaxRowChunks && (kR == 1 || kR == 4), "weight registers");
+    static_assert(kR * kC <= kGemvMaxRowChunks && (kR == 1 || kR == 2), "weight registers");
     static_assert(kEpi == kEpiNone || kR == 1, "the QKV epilogue takes one row per wave");
     a.W = pk_W;
     a.x = pk_x;
@@ -351,7 +351,7 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(const uint8_t*
     }
 }
 
-// Rows per wave: one for the per-layer shapes (latency bound: the most waves), 4 from
+// Rows per wave: one for the per-layer shapes (latency bound: the most waves), 2 from
 // kGemvTallRows rows on (bandwidth bound: more bytes in flight per wave).  kC: chunks per
 // lane and row in one block, the fewest that hold the row, at most kGemvMaxRowChunks / kR
 // (longer rows loop over blocks).
@@ -363,10 +363,11 @@ constexpr int kGemvTallRows = KVATTN_GEMV_TALL_ROWS;
 template <int WT, bool kOut, int kEpi>
 const void* gemv_ptr(int chunks_per_lane, int rows) {
     if constexpr (kEpi == kEpiNone) {
-        if (rows == 4) {
-            if (chunks_per_lane <= 1) return (const void*)&gemv_kernel<WT, 1, 4, kOut, kEpi>;
-            if (chunks_per_lane <= 2) return (const void*)&gemv_kernel<WT, 2, 4, kOut, kEpi>;
-            return (const void*)&gemv_kernel<WT, 4, 4, kOut, kEpi>;
+        if (rows == 2) {
+            if (chunks_per_lane <= 1) return (const void*)&gemv_kernel<WT, 1, 2, kOut, kEpi>;
+            if (chunks_per_lane <= 2) return (const void*)&gemv_kernel<WT, 2, 2, kOut, kEpi>;
+            if (chunks_per_lane <= 4) return (const void*)&gemv_kernel<WT, 4, 2, kOut, kEpi>;
+            return (const void*)&gemv_kernel<WT, 8, 2, kOut, kEpi>;
         }
     }
     if (chunks_per_lane <= 1) return (const void*)&gemv_kernel<WT, 1, 1, kOut, kEpi>;
@@ -421,9 +422,10 @@ int launch_gemv(GemvArgs a, int w_dtype, bool out_f32, void* stream) {
     const int nch = K * wbytes / 16;
     const int per_lane = (nch + kWave - 1) / kWave;
     // Measured at 50304 x 768 (per call, graph of calls over weights beyond the Infinity
-    // Cache): 4 rows per wave 9.2 / 13.8 / 24.9 us (INT8 / BF16 / FP32), 8 rows 9.8 / 15.5 /
-    // 24.9, one row 16.8 / 19.0 / 26.6.  The QKV epilogue takes one row per wave.
-    const int rows = a.kv || M < kGemvTallRows ? 1 : 4;
+    // Cache): 2 rows per wave 9.0 / 13.3 / 24.2 us (INT8 / BF16 / FP32), 4 rows 9.3 / 13.8 /
+    // 24.9, 8 rows 9.8 / 15.5 / 24.9, one row 16.8 / 19.0 / 26.6.  Workgroups of 8 or 16 waves
+    // instead of 4: +0.5 to +2.6 us.  The QKV epilogue takes one row per wave.
+    const int rows = a.kv || M < kGemvTallRows ? 1 : 2;
     const bool kv8 = a.kv && (a.kv_dtype == KVATTN_KV_INT8 || a.kv_dtype == KVATTN_KV_FP8_E4M3);
     const int epi = !a.kv ? kEpiNone : (kv8 ? kEpiAppend8 : kEpiAppend);
     const void* fn = nullptr;
