@@ -3,14 +3,14 @@
 // tanh GELU, for FP32, BF16 and 8-bit (INT8 / FP8-E4M3 codes with one FP32 scale per row)
 // weights.  The attention output projection consumes the attention output this way.
 //
-// One wave per kR output rows (kR = 1 for the per-layer shapes, 2 for tall matrices such as
-// the vocabulary projection).  A row of K weights is K*wbytes/16 chunks of 16
+// One wave per kR output rows (kR = 1 for the per-layer shapes; for tall matrices such as
+// the vocabulary projection 4 with 8-bit weights, 2 otherwise).  A row of K weights is K*wbytes/16 chunks of 16
 // bytes; lane l holds chunks l, l+64, ... of a block of 64*kC chunks of each of its rows in
 // registers (all requested at once), multiplies them with the matching x chunks of every
 // input vector, and a wave reduction (DPP + permlane) finishes each dot product.  Rows longer
 // than one block loop over blocks.  At GPT-2's per-layer sizes (0.6 to 4.7 MB of weights) a
 // call is bound by launch and memory latency, and one row per wave gives the most waves; a
-// tall matrix (50304 x 768) streams, and 2 rows per wave keep 1.5-6 KB per wave in flight.
+// tall matrix (50304 x 768) streams, and 2-4 rows per wave keep 3-6 KB per wave in flight.
 // MFMA is not used (B is a handful of decode tokens, 1-2 flops per byte).
 #include <hip/hip_runtime.h>
 #include <math.h>
@@ -173,7 +173,7 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(const uint8_t*
                                                                   const float* pk_w_scale, const void* pk_bias,
                                                                   int pk_B, int pk_M, int pk_K, void* pk_out,
                                                                   int pk_gelu, GemvArgs a) {
-    static_assert(kR * kC <= kGemvMaxRowChunks && (kR == 1 || kR == 2), "weight registers");
+    static_assert(kR * kC <= kGemvMaxRowChunks && (kR == 1 || kR == 2 || kR == 4), "weight registers");
     static_assert(kEpi == kEpiNone || kR == 1, "the QKV epilogue takes one row per wave");
     a.W = pk_W;
     a.x = pk_x;
@@ -185,7 +185,11 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(const uint8_t*
     a.out = pk_out;
     a.gelu = pk_gelu & kGeluFlag;
     using F = WFmt<WT>;
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    // With 4 rows per wave the row index is made wave-uniform (an SGPR), so the rows' base
+    // addresses, scales and bias are scalar: 61 VGPRs and 8 waves per SIMD for 8-bit weights
+    // (81 and 5 without).  At 1-2 rows per wave the vector form measured faster.
+    const int wave = kR == 4 ? (int)__builtin_amdgcn_readfirstlane(threadIdx.x / kWave) : (int)(threadIdx.x / kWave);
     // kEpiAppend8 with the XCD-local layout: the 16 workgroups of a head row share an XCD.
     const bool xl = kEpi == kEpiAppend8 && (pk_gelu & kXcdLocalFlag) != 0;
     const int wg = xl ? xcd_slot(blockIdx.x, kHeadRowGroups) : (int)blockIdx.x;
@@ -351,8 +355,9 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(const uint8_t*
     }
 }
 
-// Rows per wave: one for the per-layer shapes (latency bound: the most waves), 2 from
-// kGemvTallRows rows on (bandwidth bound: more bytes in flight per wave).  kC: chunks per
+// Rows per wave: one for the per-layer shapes (latency bound: the most waves); from
+// kGemvTallRows rows on (bandwidth bound: more bytes in flight per wave) 4 for 8-bit weights
+// and 2 for the wider ones, the most that keep 8 waves per SIMD.  kC: chunks per
 // lane and row in one block, the fewest that hold the row, at most kGemvMaxRowChunks / kR
 // (longer rows loop over blocks).
 #ifndef KVATTN_GEMV_TALL_ROWS
@@ -363,7 +368,13 @@ constexpr int kGemvTallRows = KVATTN_GEMV_TALL_ROWS;
 template <int WT, bool kOut, int kEpi>
 const void* gemv_ptr(int chunks_per_lane, int rows) {
     if constexpr (kEpi == kEpiNone) {
-        if (rows == 2) {
+        if constexpr (WFmt<WT>::k8bit) {
+            if (rows == 4) {
+                if (chunks_per_lane <= 1) return (const void*)&gemv_kernel<WT, 1, 4, kOut, kEpi>;
+                if (chunks_per_lane <= 2) return (const void*)&gemv_kernel<WT, 2, 4, kOut, kEpi>;
+                return (const void*)&gemv_kernel<WT, 4, 4, kOut, kEpi>;
+            }
+        } else if (rows == 2) {
             if (chunks_per_lane <= 1) return (const void*)&gemv_kernel<WT, 1, 2, kOut, kEpi>;
             if (chunks_per_lane <= 2) return (const void*)&gemv_kernel<WT, 2, 2, kOut, kEpi>;
             if (chunks_per_lane <= 4) return (const void*)&gemv_kernel<WT, 4, 2, kOut, kEpi>;
@@ -422,10 +433,11 @@ int launch_gemv(GemvArgs a, int w_dtype, bool out_f32, void* stream) {
     const int nch = K * wbytes / 16;
     const int per_lane = (nch + kWave - 1) / kWave;
     // Measured at 50304 x 768 (per call, graph of calls over weights beyond the Infinity
-    // Cache): 2 rows per wave 9.0 / 13.3 / 24.2 us (INT8 / BF16 / FP32), 4 rows 9.3 / 13.8 /
-    // 24.9, 8 rows 9.8 / 15.5 / 24.9, one row 16.8 / 19.0 / 26.6.  Workgroups of 8 or 16 waves
+    // Cache), INT8 / BF16 / FP32: 2 rows per wave 9.0-9.1 / 13.1-13.3 / 23.9-24.2 us; 4 rows
+    // with the wave-uniform row index 8.6 / 14.0-14.2 / 25.0, without it 9.3 / 13.8 / 24.9;
+    // 8 rows 9.8 / 15.5 / 24.9; one row 16.8 / 19.0 / 26.6.  Workgroups of 8 or 16 waves
     // instead of 4: +0.5 to +2.6 us.  The QKV epilogue takes one row per wave.
-    const int rows = a.kv || M < kGemvTallRows ? 1 : 2;
+    const int rows = a.kv || M < kGemvTallRows ? 1 : (w8 ? 4 : 2);
     const bool kv8 = a.kv && (a.kv_dtype == KVATTN_KV_INT8 || a.kv_dtype == KVATTN_KV_FP8_E4M3);
     const int epi = !a.kv ? kEpiNone : (kv8 ? kEpiAppend8 : kEpiAppend);
     const void* fn = nullptr;

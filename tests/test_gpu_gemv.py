@@ -136,8 +136,9 @@ def test_gemv_vocabulary_projection_float_out(dev, dtype):
 def test_gemv_rows_beyond_one_block(dev, dtype, M):
     """Rows longer than one block of a wave's registers: with one row per wave (37 rows) a
     block is 64 x 16 chunks, so rows of 32 KB (FP32), 24 KB (bf16) and 20 KB (8-bit) take two
-    blocks; with the tall shape (8195 rows, 2 rows per wave, a partial last wave) a block is
-    64 x 8 chunks, and 9216-element rows take 2 (8-bit) to 5 (FP32) blocks.  B = 1 and B = 3 (the weights
+    blocks; with the tall shape (8195 rows, 2 rows per wave or 4 for 8-bit weights, a partial
+    last wave) a block is 64 x 8 chunks (64 x 4 for 8-bit), and 9216-element rows take 3 to 5
+    blocks.  B = 1 and B = 3 (the weights
     are read again per vector); with bias and GELU."""
     if M < 8192:
         K = {"f32": 8192, "bf16": 12288, "int8": 20480, "fp8": 20480}[dtype]
