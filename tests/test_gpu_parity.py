@@ -701,3 +701,39 @@ def test_device_length_out_of_range_is_clamped(dev):
                           **ws.kwargs())
             torch.cuda.synchronize()
             assert_close(out.cpu().numpy(), case.reference(), "f32", f"clamped {bad} {strategy}")
+
+
+def test_seeded_shape_sweep(dev):
+    """48 calls drawn from a fixed seed across the plan space, each against the oracle:
+    B in 1..5, NH in 1..16, maxT in 16..2048 with per-sequence lengths anywhere in
+    [1, maxT], every cache type, AUTO and each explicit strategy but the cooperative one
+    (covered above), with S of the reference partition (S > 0), fixed rows per segment
+    (S < 0) or the library's choice (S = 0), and a length hint that is absent, exact or
+    stale (any value below maxT: the hint steers the plan only).  An explicit designated
+    plan whose grid the GPU cannot hold at once is refused with ERR_GRID_TOO_LARGE; that
+    case then runs with the last-block merge of the same S."""
+    kvattn = _kv()
+    rng = np.random.RandomState(2026)
+    strategies = ["auto", "fused_single", "split_merge", "lastblock", "designated", "graph"]
+    for i in range(48):
+        dtype = ALL_DT[rng.randint(len(ALL_DT))]
+        B, NH = int(rng.randint(1, 6)), int(rng.randint(1, 17))
+        maxT = int(rng.choice([16, 64, 100, 256, 300, 777, 1024, 2048]))
+        lens = rng.randint(1, maxT + 1, B).astype(np.int32)
+        strategy = strategies[rng.randint(len(strategies))]
+        S = 0
+        if strategy not in ("auto", "fused_single"):
+            kind = rng.randint(3)
+            S = int(rng.randint(1, 33)) if kind == 1 else (-int(rng.choice([32, 64, 128, 256])) if kind == 2 else 0)
+        hint_kind = rng.randint(3)
+        len_hint = -1 if hint_kind == 0 else (int(lens.max()) - 1 if hint_kind == 1 else int(rng.randint(0, maxT)))
+        name = f"case {i}: {dtype} B={B} NH={NH} maxT={maxT} {strategy} S={S} hint={len_hint} lens={lens.tolist()}"
+        print(name, flush=True)
+        case = make_case(dtype, B, NH, maxT, lens - 1, seed=9000 + i)
+        try:
+            got = _run(case, dev, strategy, S=S, len_hint=len_hint)
+        except kvattn.KvAttnError as e:
+            assert strategy == "designated" and e.status == kvattn.ERR_GRID_TOO_LARGE, f"{name}: {e}"
+            print(f"  refused ({e}); last-block instead", flush=True)
+            got = _run(case, dev, "lastblock", S=S, len_hint=len_hint)
+        assert_close(got, case.reference(), dtype, name)
