@@ -328,3 +328,33 @@ def test_gemv_qkv_append_8bit_fallback_and_dense_layout(dev, kv):
             assert torch.equal(qkv.view(torch.int16), q_ref.view(torch.int16)), what + ": qkv"
             assert torch.equal(cache, c_ref), what + ": codes"
             assert torch.equal(kscale.view(torch.int32), s_ref.view(torch.int32)), what + ": row scales"
+
+
+def test_gemv_seeded_shape_sweep(dev):
+    """32 calls drawn from a fixed seed, each against the oracle: every weight type, B in
+    1..4, M from 1 row to beyond the tall-matrix threshold (8192, with partial last waves),
+    K any multiple of 16 up to 3072 (one or several blocks of a row), with and without
+    bias and GELU, and float, bf16 or activation-typed output.  The bar follows the output
+    type (bf16 outputs 1e-2)."""
+    rng = np.random.RandomState(4242)
+    for i in range(32):
+        dtype = ["f32", "bf16", "int8", "fp8"][rng.randint(4)]
+        B = int(rng.randint(1, 5))
+        kind = rng.randint(3)
+        M = int(rng.randint(1, 300)) if kind == 0 else (int(rng.randint(8190, 8201)) if kind == 1
+                                                        else int(rng.randint(300, 12000)))
+        K = 16 * int(rng.randint(1, 193))
+        gelu = bool(rng.randint(2))
+        with_bias = bool(rng.randint(2))
+        out_dtype = [None, "f32", "bf16"][rng.randint(3)]
+        name = f"case {i}: {dtype} B={B} M={M} K={K} gelu={gelu} bias={with_bias} out={out_dtype}"
+        print(name, flush=True)
+        d, h = _make(dtype, B, M, K, seed=7000 + i, with_bias=with_bias)
+        got, pre = _run(d, dtype, B, M, K, gelu, want_pre=gelu, out_dtype=out_dtype)
+        ref, rpre = oracle.gemv(h["W"], h["x"], B, M, K, w_scale=h["scale"], bias=h["bias"], gelu=gelu,
+                                want_pre=True)
+        out_bf16 = out_dtype == "bf16" or (out_dtype is None and dtype != "f32")
+        key = "bf16" if out_bf16 else dtype
+        _check(got, ref, key, B, M, name)
+        if gelu:
+            _check(pre, rpre, key, B, M, name + " pre_gelu")
