@@ -311,3 +311,47 @@ def test_paged_c5_shape_matches_contiguous(dev):
         q1[0, 0, 0] = q_h[b, 0, h]
         ref = oracle.attention_f32(q1.reshape(-1), np.stack([kk, vv]).reshape(-1), T, 1, 1, HS, T)
         assert_close(a[b, h].cpu().numpy(), ref, "bf16", f"paged C5 b={b} h={h} T={T}")
+
+
+def test_paged_seeded_shape_sweep(dev):
+    """24 paged calls drawn from a fixed seed, each against the oracle on the contiguous
+    values: page rows 64 / 128 / 256 / 512, B 1..4, NH 1..12, up to 16 pages per sequence
+    with ragged lengths, every cache type, AUTO and the explicit split strategies, device-
+    planned or fixed rows per segment (multiples of 64), and an absent, exact or stale
+    length hint.  An explicit designated plan the library refuses (a grid beyond residency,
+    or segments longer than a wave walks) runs with the last-block merge instead."""
+    import torch
+    kvattn = _kv()
+    rng = np.random.RandomState(777)
+    strategies = ("auto", "lastblock", "designated", "split_merge", "graph")
+    for i in range(24):
+        dtype = ["f32", "bf16", "int8", "fp8"][rng.randint(4)]
+        P = int(rng.choice([64, 128, 256, 512]))
+        B, NH = int(rng.randint(1, 5)), int(rng.randint(1, 13))
+        maxT = P * int(rng.randint(1, 17))
+        lens = rng.randint(1, maxT + 1, B).astype(np.int32)
+        strategy = strategies[rng.randint(len(strategies))]
+        S = 0 if strategy == "auto" or rng.randint(2) == 0 else -64 * int(rng.randint(1, 9))
+        hint_kind = rng.randint(3)
+        hint = -1 if hint_kind == 0 else (int(lens.max()) - 1 if hint_kind == 1 else int(rng.randint(0, maxT)))
+        name = (f"case {i}: {dtype} P={P} B={B} NH={NH} maxT={maxT} {strategy} S={S} hint={hint} "
+                f"lens={lens.tolist()}")
+        print(name, flush=True)
+        case = make_case(dtype, B, NH, maxT, lens - 1, seed=8000 + i)
+        pg = Paged(case, P, dev, seed=i)
+        cur = torch.from_numpy(case.cur_lens.copy()).to(dev)
+        qkv = torch.from_numpy(case.qkv_raw.view(np.int16 if dtype != "f32" else np.float32)).to(dev)
+        if dtype != "f32":
+            qkv = qkv.view(torch.bfloat16)
+        ws = kvattn.Workspace(B, NH, maxT, S)
+        out = out_tensor(case, dev)
+        kw = dict(kv_dtype=dtype, cur_len=cur, lens_per_seq=True, len_hint=hint, S=S, **ws.kwargs())
+        try:
+            kvattn.paged_decode(out, qkv, pg.cache, B, NH, HS, strategy=strategy, **kw)
+        except kvattn.KvAttnError as e:
+            assert strategy == "designated" and e.status in (kvattn.ERR_GRID_TOO_LARGE, kvattn.ERR_SPLIT), \
+                f"{name}: {e}"
+            print(f"  refused ({e}); last-block instead", flush=True)
+            kvattn.paged_decode(out, qkv, pg.cache, B, NH, HS, strategy="lastblock", **kw)
+        torch.cuda.synchronize()
+        assert_close(out.float().cpu().numpy(), case.reference(), dtype, name)
