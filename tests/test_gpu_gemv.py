@@ -358,3 +358,63 @@ def test_gemv_seeded_shape_sweep(dev):
         _check(got, ref, key, B, M, name)
         if gelu:
             _check(pre, rpre, key, B, M, name + " pre_gelu")
+
+
+def test_gemv_qkv_append_seeded_sweep(dev):
+    """16 calls of kvattn_gemv_qkv_append drawn from a fixed seed, each against kvattn_gemv +
+    kvattn_cache_write on a copy of the cache (qkv, cache bytes and 8-bit row scales bit for
+    bit): every valid weight / cache type pair, NH 1..16 (the 8-bit epilogue's dense and
+    XCD-local layouts), B 1..4, K up to 1536, maxT 1..200, one length or per-sequence
+    lengths (some beyond maxT, clamped)."""
+    import torch
+    kvattn = _kv()
+    pairs = [("f32", "f32"), ("bf16", "bf16"), ("int8", "bf16"), ("fp8", "bf16"), ("bf16", "int8"),
+             ("bf16", "fp8"), ("int8", "int8"), ("fp8", "fp8"), ("int8", "fp8")]
+    rng = np.random.RandomState(5150)
+    HS = 64
+    for i in range(16):
+        dtype, kv = pairs[rng.randint(len(pairs))]
+        NH, B = int(rng.randint(1, 17)), int(rng.randint(1, 5))
+        K = 16 * int(rng.randint(1, 97))
+        maxT = int(rng.randint(1, 201))
+        per_seq = bool(rng.randint(2))
+        lens = rng.randint(0, maxT + 8, B if per_seq else 1).astype(np.int32)
+        name = f"case {i}: {dtype} weights, {kv} cache, NH={NH} B={B} K={K} maxT={maxT} cur_len={lens.tolist()}"
+        print(name, flush=True)
+        M = 3 * NH * HS
+        d, _ = _make(dtype, B, M, K, seed=5200 + i, with_bias=bool(rng.randint(2)))
+        W, x = d["W"].to(dev), d["x"].to(dev).contiguous()
+        bias = None if d["bias"] is None else d["bias"].to(dev)
+        scale = None if d.get("scale") is None else d["scale"].to(dev)
+        act = torch.float32 if dtype == "f32" else torch.bfloat16
+        w8 = kv in ("int8", "fp8")
+        g = torch.Generator(device=dev)
+        g.manual_seed(5300 + i)
+        if w8:
+            cache = torch.randint(0, 256, (2 * B * NH * maxT * HS,), generator=g, device=dev, dtype=torch.uint8)
+            kscale = torch.rand(2 * B * NH * maxT, generator=g, device=dev)
+            ws_bytes = kvattn.gemv_qkv_append_workspace_bytes(B, NH)
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+            kvattn.workspace_init(ws, ws_bytes)
+        else:
+            cache = torch.randn(2 * B * NH * maxT * HS, generator=g, device=dev).to(act)
+            kscale, ws, ws_bytes = None, None, 0
+        cur = torch.from_numpy(lens).to(dev)
+        iview = torch.int32 if dtype == "f32" else torch.int16
+        cview = torch.uint8 if w8 else iview
+        c_a, c_b = cache.clone(), cache.clone()
+        s_a = None if kscale is None else kscale.clone()
+        s_b = None if kscale is None else kscale.clone()
+        q_a = torch.empty(B * M, dtype=act, device=dev)
+        q_b = torch.empty_like(q_a)
+        kvattn.gemv(q_a, W, x, B, M, K, w_dtype=dtype, w_scale=scale, bias=bias)
+        kvattn.kv_cache_write(c_a, q_a, B, NH, HS, maxT, kv_dtype=kv, kv_scale=s_a, cur_len=cur,
+                              lens_per_seq=per_seq)
+        kvattn.gemv_qkv_append(q_b, W, x, B, NH, HS, K, c_b, maxT, w_dtype=dtype, kv_dtype=kv, w_scale=scale,
+                               bias=bias, kv_scale=s_b, cur_len=cur, lens_per_seq=per_seq, workspace=ws,
+                               workspace_nbytes=ws_bytes)
+        torch.cuda.synchronize()
+        assert torch.equal(q_a.view(iview), q_b.view(iview)), f"{name}: qkv"
+        assert torch.equal(c_a.view(cview), c_b.view(cview)), f"{name}: cache"
+        if w8:
+            assert torch.equal(s_a.view(torch.int32), s_b.view(torch.int32)), f"{name}: row scales"
