@@ -148,7 +148,9 @@ constexpr int kHd = 64;   // head size of the QKV epilogue
 constexpr int kHeadRowGroups = kHd / kGemvWaves;   // workgroups of one head row (64 channels, one row per wave)
 // The epilogue of a launch (a template parameter, so that the plain GEMV carries none of it).
 enum GemvEpilogue { kEpiNone = 0, kEpiAppend = 1, kEpiAppend8 = 2 };
-constexpr int kGeluFlag = 1, kXcdLocalFlag = 2;   // bits of the preloaded gelu argument
+// Bits of the preloaded M argument above the row count (M < 2^29): GELU, and the XCD-local
+// layout of kEpiAppend8.
+constexpr int kGeluFlag = 1 << 29, kXcdLocalFlag = 1 << 30, kRowMask = (1 << 29) - 1;
 
 // Cache row (in units of kHd elements) of part 1 (K) or 2 (V), head h, sequence b at the
 // position being appended: column cur_len, clamped to [0, maxT - 1] as the append does.
@@ -162,17 +164,20 @@ __device__ __forceinline__ size_t cache_row(const GemvArgs& a, int b, int part, 
 }
 
 // The weights, x, scales, bias, shape and output also come as leading scalar parameters
-// (14 dwords, preloaded into SGPRs at wave launch: the library is built with kernel-argument
+// (13 dwords, preloaded into SGPRs at wave launch: the library is built with kernel-argument
 // preloading), so the weight and x loads issue without a scalar load of the argument block.
 // kC: 16-byte chunks per lane and row in one block of the row; kR: rows per wave; kOutF32:
 // out and pre_gelu as float (else bf16); kEpi: the QKV epilogue (GemvEpilogue).  Rows of more
 // than 64*kC chunks take several blocks (the weights are then read again for each input
-// vector).  pk_gelu: bit 0 GELU, bit 1 the XCD-local layout of kEpiAppend8.
+// vector).  pk_M: the rows M with the GELU and XCD-local flags in bits 29 and 30.  The 8-bit
+// epilogue takes the dispatch id and the queue pointer (its tag) in user SGPRs, which leaves 10
+// dwords of preloaded arguments: W, x, the scales, the bias, M and K, all its first loads
+// need; B and out follow.
 template <int WT, int kC, int kR, bool kOutF32, int kEpi>
 __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(const uint8_t* pk_W, const uint8_t* pk_x,
                                                                   const float* pk_w_scale, const void* pk_bias,
-                                                                  int pk_B, int pk_M, int pk_K, void* pk_out,
-                                                                  int pk_gelu, GemvArgs a) {
+                                                                  int pk_M, int pk_K, int pk_B, void* pk_out,
+                                                                  GemvArgs a) {
     static_assert(kR * kC <= kGemvMaxRowChunks && (kR == 1 || kR == 2 || kR == 4), "weight registers");
     static_assert(kEpi == kEpiNone || kR == 1, "the QKV epilogue takes one row per wave");
     a.W = pk_W;
@@ -180,10 +185,13 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(const uint8_t*
     a.w_scale = pk_w_scale;
     a.bias = pk_bias;
     a.B = pk_B;
-    a.M = pk_M;
+    // B >= 1 (the host checks it): without it the code generator tests B before the first
+    // weight load, which would then wait for B's scalar load whenever B is not preloaded.
+    __builtin_assume(a.B >= 1);
+    a.M = pk_M & kRowMask;
     a.K = pk_K;
     a.out = pk_out;
-    a.gelu = pk_gelu & kGeluFlag;
+    a.gelu = (pk_M & kGeluFlag) != 0;
     using F = WFmt<WT>;
     const int lane = threadIdx.x & (kWave - 1);
     // With 4 rows per wave the row index is made wave-uniform (an SGPR), so the rows' base
@@ -191,7 +199,7 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(const uint8_t*
     // (81 and 5 without).  At 1-2 rows per wave the vector form measured faster.
     const int wave = kR == 4 ? (int)__builtin_amdgcn_readfirstlane(threadIdx.x / kWave) : (int)(threadIdx.x / kWave);
     // kEpiAppend8 with the XCD-local layout: the 16 workgroups of a head row share an XCD.
-    const bool xl = kEpi == kEpiAppend8 && (pk_gelu & kXcdLocalFlag) != 0;
+    const bool xl = kEpi == kEpiAppend8 && (pk_M & kXcdLocalFlag) != 0;
     const int wg = xl ? xcd_slot(blockIdx.x, kHeadRowGroups) : (int)blockIdx.x;
     const int m0 = (wg * kGemvWaves + wave) * kR;
     if (m0 >= a.M) return;   // whole wave (no barrier follows)
@@ -420,7 +428,7 @@ int launch_gemv(GemvArgs a, int w_dtype, bool out_f32, void* stream) {
     const size_t act = w_dtype == KVATTN_KV_F32 ? 4 : 2;
     const size_t osz = out_f32 ? 4 : 2;
     const int B = a.B, M = a.M, K = a.K;
-    if (B < 1 || M < 1 || K < 16 || K % 16 != 0) return KVATTN_ERR_SHAPE;
+    if (B < 1 || M < 1 || M > kRowMask || K < 16 || K % 16 != 0) return KVATTN_ERR_SHAPE;
     if ((long long)B * M >= (1ll << 31) || (long long)M * K * wbytes >= (1ll << 40) || (long long)B * K >= (1ll << 31))
         return KVATTN_ERR_SHAPE;
     if (!a.out || !a.W || !a.x) return KVATTN_ERR_NULL_POINTER;
@@ -449,14 +457,14 @@ int launch_gemv(GemvArgs a, int w_dtype, bool out_f32, void* stream) {
     }
     if (!fn) return KVATTN_ERR_DTYPE;
     long long groups = ((M + rows - 1) / rows + kGemvWaves - 1) / kGemvWaves;
-    int flags = a.gelu ? kGeluFlag : 0;
+    int pk_m = a.M | (a.gelu ? kGeluFlag : 0);
     // 8-bit epilogue: the 16 workgroups of each of the 3*NH head rows on one XCD, once there are
     // enough head rows to give every XCD one (the grid is padded to whole rounds of 8).
     if (epi == kEpiAppend8 && 3 * a.NH >= 8) {
         groups = 8ll * ((3 * a.NH + 7) / 8) * kHeadRowGroups;
-        flags |= kXcdLocalFlag;
+        pk_m |= kXcdLocalFlag;
     }
-    void* params[] = {&a.W, &a.x, &a.w_scale, &a.bias, &a.B, &a.M, &a.K, &a.out, &flags, &a};
+    void* params[] = {&a.W, &a.x, &a.w_scale, &a.bias, &pk_m, &a.K, &a.B, &a.out, &a};
     const hipError_t e = hipLaunchKernel(fn, dim3((unsigned)groups), dim3(kGemvWaves * kWave), params, 0,
                                          (hipStream_t)stream);
     if (e != hipSuccess) {

@@ -828,13 +828,22 @@ struct SplitArgs {
 
 // Kernel parameter arrays of split_kernel and merge_kernel (their leading scalars, then the
 // struct), for launches through hipLaunchKernel, cooperative launches and graph nodes.
-// split_spec(x) is the packed length hint pk_spec of split_kernel and split_pks(x, mode) its
-// packed slot count pk_S (bit 30: the designated grid's XCD-local layout); SPLIT_PARAMS needs
-// int lvalues `spec` and `pks` holding them.
+// split_spec(x) is the packed length hint pk_spec of split_kernel, split_pks(x, ...) its
+// packed slot word pk_S, split_pnh(x, ...) its pk_NH and x.B * x.NH its pk_BNH; SPLIT_PARAMS
+// needs int lvalues `spec`, `pks`, `pnh` and `bnh` holding them.
+// pk_S: bits 0-16 the segment slots S (at most kMaxSegments); bit 30 the designated grid's
+// XCD-local layout.  The designated instances take the dispatch id and the queue pointer in
+// user SGPRs (the call's tag), which leaves 10 dwords of preloaded arguments: pk_spec falls
+// out of them, so for those instances pk_S also carries what the first requests need of the
+// length hint: bits 17-23 the segments the hint covers (at most 64), bit 24 per-sequence
+// lengths.
 constexpr int kXcdLocalBit = 1 << 30;
+constexpr int kSlotMask = (1 << 17) - 1;
+constexpr int kHintSegShift = 17;
+constexpr int kLensBit = 1 << 24;
 inline int split_spec(const SplitArgs& a) { return a.lens_per_seq ? -1 : (a.spec_rows > 0 ? a.spec_rows : 0); }
-#define SPLIT_PARAMS(x) {&(x).kv, &(x).qkv, &(x).cur_len, &(x).B, &(x).NH, &(x).maxT, &pks, &(x).seg_rows, \
-                         &spec, &(x)}
+#define SPLIT_PARAMS(x) {&(x).kv, &(x).qkv, &(x).cur_len, &pnh, &(x).maxT, &pks, &(x).seg_rows, &bnh, \
+                         &spec, &(x).B, &(x)}
 #define MERGE_PARAMS(x) {&(x).part_max, &(x).part_lse, &(x).part_out, &(x).cur_len, &(x).B, &(x).NH, &(x).maxT, \
                          &(x).S, &(x).seg_rows, &(x).lens_per_seq, &(x)}
 
@@ -895,13 +904,9 @@ __device__ __forceinline__ int seg_count(int seg_rows, int total, int heads, int
 // the per-sequence segment counts, computed redundantly by every wave.  `dense`: the dense
 // grid whatever the lengths (designated grids, whose slot order places every segment of a
 // head on one XCD; slots beyond a head's segment count exit).
-__device__ __forceinline__ bool locate(const SplitArgs& a, int x, Item& it, bool dense) {
+__device__ __forceinline__ bool locate(const SplitArgs& a, int BNH, int x, Item& it, bool dense) {
     if (dense || !a.lens_per_seq || a.seg_rows == 0) {
-        const int bh = x / a.S;
-        it.s = x - bh * a.S;
-        it.b = bh / a.NH;
-        it.h = bh - it.b * a.NH;
-        if (it.b >= a.B) return false;
+        if (!dense_slot(x, a.S, BNH, a.NH, it.b, it.h, it.s)) return false;
         it.total = seq_total(a.cur_len, a.lens_per_seq, it.b, a.maxT);
         it.rows = 0;
         it.n_seg = a.seg_rows != 0 ? seg_count(a.seg_rows, it.total, a.B * a.NH, it.rows) : a.S;
@@ -992,6 +997,26 @@ __host__ __device__ __forceinline__ long long designated_grid(int B, int NH, int
     return xcd_local_layout(B, NH) ? 8ll * ((B * NH + 7) / 8) * S : (long long)B * NH * S;
 }
 
+// pk_S of a split launch: the slot count and, for the designated instances, the XCD-local
+// layout bit and the length hint in the form their first requests use (the segments the hint
+// puts in use, per-sequence lengths).
+inline int split_pks(const SplitArgs& a, bool des) {
+    int pks = a.S;
+    if (des) {
+        if (xcd_local_layout(a.B, a.NH)) pks |= kXcdLocalBit;
+        if (a.lens_per_seq) pks |= kLensBit;
+        else if (a.seg_rows > 0 && a.spec_rows > 0)
+            pks |= std::min(ceil_div_i(a.spec_rows, a.seg_rows), kMaxDesignatedSegments) << kHintSegShift;
+    }
+    return pks;
+}
+
+// pk_NH of a split launch: NH, and for the designated instances NH | B * NH << 16 (both below
+// 2^16: a designated grid has at least B * NH workgroups and must fit on the GPU at once).
+inline int split_pnh(const SplitArgs& a, bool des) {
+    return des ? (int)((unsigned)a.NH | (unsigned)(a.B * a.NH) << 16) : a.NH;
+}
+
 // Merge the n_seg partials of (b,h) = bh into out; executed by one full wave, lane c
 // producing channel c.  Lane s holds the max and exp-sum of segment s (64 segments per
 // round), and the weighted V partials are requested 16 segments at a time together with
@@ -1038,25 +1063,37 @@ __device__ __forceinline__ void merge_partials(void* out, const float* part_out,
 // cur_len takes that row from qkv and writes it to the cache).  kPaged: the cache is a page
 // pool addressed through a block table (segments then start at multiples of the tile).
 template <int DT, int kMode, int kW, int kU, bool kFresh, bool kPaged>
-__global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS : 1) void split_kernel(const uint8_t* pk_kv, const void* pk_qkv, const int* pk_len, int pk_B, int pk_NH,
-                                         int pk_maxT, int pk_S, int pk_seg_rows, int pk_spec, SplitArgs a) {
+__global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS : 1) void split_kernel(const uint8_t* pk_kv, const void* pk_qkv, const int* pk_len, int pk_NH, int pk_maxT,
+                                         int pk_S, int pk_seg_rows, int pk_BNH, int pk_spec, int pk_B, SplitArgs a) {
     // The fields that the first loads depend on also come as leading scalar parameters: the
     // library is built with kernel-argument preloading, so the hardware hands them over in
     // SGPRs at wave launch and the first K/V, q and length requests do not wait for a scalar
-    // load of the argument block.  They fit in 12 dwords, all that is left of the 16 user
-    // SGPRs once the designated instances also take the dispatch id: pk_spec is the length
-    // hint, or -1 for per-sequence lengths (the hint is not used then), and the q scale is
-    // the constant of hs = 64.  The struct keeps the rest.
+    // load of the argument block.  The designated instances also take the dispatch id and the
+    // queue pointer (their tag) in user SGPRs, which leaves 10 of the 16 for arguments: the
+    // first 10 dwords here are all their first requests need (NH and B * NH packed into pk_NH,
+    // both below 2^16 in any grid the GPU holds at once; the length hint packed into pk_S);
+    // pk_BNH, pk_spec (the length hint of the other instances; -1: per-sequence lengths, the
+    // hint not used) and B come after them (preloaded for the other instances, read later
+    // from the argument block by the designated ones).  The struct keeps the rest; the q
+    // scale is the constant of hs = 64.
+    constexpr bool kDesMode = kMode == kDesignated || kMode == kDesignatedDev;
     a.kv = pk_kv;
     a.qkv = pk_qkv;
     a.cur_len = pk_len;
-    a.B = pk_B;
-    a.NH = pk_NH;
+    a.NH = kDesMode ? (int)((unsigned)pk_NH & 0xFFFFu) : pk_NH;
     a.maxT = pk_maxT;
-    a.S = pk_S & (kXcdLocalBit - 1);
+    a.S = pk_S & kSlotMask;
     a.seg_rows = pk_seg_rows;
-    a.lens_per_seq = pk_spec < 0 ? 1 : 0;
-    a.spec_rows = pk_spec < 0 ? 0 : pk_spec;
+    a.B = pk_B;
+    const int BNH = kDesMode ? (int)((unsigned)pk_NH >> 16) : pk_BNH;
+    int hint_segs = 0;   // designated: segments the host's length hint puts in use
+    if constexpr (kDesMode) {
+        a.lens_per_seq = (pk_S & kLensBit) != 0 ? 1 : 0;
+        hint_segs = (pk_S >> kHintSegShift) & 127;
+    } else {
+        a.lens_per_seq = pk_spec < 0 ? 1 : 0;
+        a.spec_rows = pk_spec < 0 ? 0 : pk_spec;
+    }
     a.qscale = kQScale;
     using R = Row<DT>;
     // The latency shape (tiles of KVATTN_SPLIT_LAT_ROWS rows) takes the hardware bf16 dot.
@@ -1069,7 +1106,7 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
     const int slot_row = lane / R::kLanes, slice = lane % R::kLanes;
     // Designated grids of the XCD-local layout: the slot this workgroup works on (every segment
     // of a head on one XCD).
-    const bool xl = (kMode == kDesignated || kMode == kDesignatedDev) && (pk_S & kXcdLocalBit) != 0;
+    const bool xl = kDesMode && (pk_S & kXcdLocalBit) != 0;
     const int vbx = xl ? xcd_slot(blockIdx.x, a.S) : (int)blockIdx.x;
 
     // Uniform lengths with fixed-size segments: (b, h, s) and the segment's nominal rows
@@ -1094,31 +1131,34 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
     bool g_on = false, g_has_tile = true;
     int g_w0 = 0, g_w1 = 0, g_j0 = 0, g_end = 0;
     if (!kPaged && kMode != kPartialsStrided && !a.lens_per_seq && (kDev || a.seg_rows > 0)) {
-        const int nom = kDev ? designated_base_rows(a.B * a.NH) : a.seg_rows;
+        const int nom = kDev ? designated_base_rows(BNH) : a.seg_rows;
         const int bh0 = div_uniform(vbx, a.S);   // beyond B * NH only in a designated grid padded to whole XCD rounds
-        const int j0 = (vbx - bh0 * a.S) * nom;
+        const int s0 = vbx - bh0 * a.S;
+        const int j0 = s0 * nom;
         const bool first = kDev && j0 == 0 && nom < kFusedMaxRows;
-        const int nend = min(j0 + (first ? kFusedMaxRows : nom), a.maxT);
+        // Segment 0 of the device plan may hold up to kFusedMaxRows rows: wave w takes tile w of
+        // the first kW tiles now, and tile w of the next kW once the length shows it has rows
+        // (segment lambda below); every other guess splits the nominal rows over the waves.
+        constexpr int kTileRows = kRowsPerLoad<DT> * kU;
+        int nend, w0, w1;
+        guess_rows(s0, nom, first ? kFusedMaxRows : nom, a.maxT, first, kW, kTileRows, wave, nend, w0, w1);
         // 8-bit caches guess only in segment 0's early share: measured, the producers' early
         // tiles cost 8-bit calls more than the length's round trip they hide.
         const bool allowed = !(R::k8bit && kDev && !first);
-        if (allowed && bh0 < a.B * a.NH && (kDev || j0 < a.spec_rows) && j0 < nend) {
-            // Segment 0 of the device plan may hold up to kFusedMaxRows rows: wave w takes tile w of
-            // the first kW tiles now, and tile w of the next kW once the length shows it has rows
-            // (segment lambda below); every other guess splits the nominal rows over the waves.
-            constexpr int kTileRows = kRowsPerLoad<DT> * kU;
-            const int per = first ? kTileRows : ceil_div_i(nend - j0, kW);
-            g_w0 = min(j0 + wave * per, nend);
-            g_w1 = min(g_w0 + per, nend);
+        // In use by the host's hint: s0 * nom < hint, i.e. s0 below the hinted segment count.
+        const bool hinted = kDesMode ? s0 < hint_segs : j0 < a.spec_rows;
+        if (allowed && guess_slot_live(bh0, BNH) && (kDev || hinted) && j0 < nend) {
+            g_w0 = w0;
+            g_w1 = w1;
             g_j0 = j0;
             g_end = nend;
             g_has_tile = !first || g_w1 <= j0 + nom;
-            const Slot sl0 = make_slot<DT>(a.kv, a.kv_scale, a.B, a.NH, a.maxT, bh0, slice);
+            const Slot sl0 = make_slot<DT>(a.kv, a.kv_scale, 1, BNH, a.maxT, bh0, slice);
             if (g_has_tile) load_tile<DT, kU, true>(g_tile, sl0, g_w0, g_w1, slot_row);
             // The sequence index (a division by NH) is needed only for q's address: keep it
             // behind the tile's requests.
             __builtin_amdgcn_sched_barrier(0);
-            const int b0 = a.B == 1 ? 0 : bh0 / a.NH;
+            const int b0 = BNH == a.NH ? 0 : bh0 / a.NH;
             g_q = load_q<DT>(a.qkv, b0, bh0 - b0 * a.NH, a.NH, slice);
             if constexpr (kFresh) g_fresh = load_fresh<DT>(a.qkv, b0, bh0 - b0 * a.NH, a.NH, slice);
             g_on = true;
@@ -1186,7 +1226,7 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                     int x0 = 0, x1 = 0;
                     Tile<DT, kU> tx;
                     if (spec && (!kDev || (j0 == spec_j0 && j1 <= spec_end))) {
-                        if (kDev && j0 == 0 && designated_base_rows(a.B * a.NH) < kFusedMaxRows) {
+                        if (kDev && j0 == 0 && designated_base_rows(BNH) < kFusedMaxRows) {
                             x0 = w0 + kW * kTileRows;
                             x1 = min(x0 + kTileRows, j1);
                         }
@@ -1534,7 +1574,7 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
         }
     } else {
         Item it;
-        const bool active = locate(a, vbx, it, kMode == kDesignated || kMode == kDesignatedDev);
+        const bool active = locate(a, BNH, vbx, it, kDesMode);
         if constexpr (kMode != kCoopMerge) {
             if (!active) return;
         }
@@ -1671,6 +1711,15 @@ __device__ int g_cur_len = 0;
 // Zero n 32-bit words (grid-stride).
 __global__ __launch_bounds__(kBlock) void zero_words_kernel(uint32_t* __restrict__ p, size_t n) {
     for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (size_t)gridDim.x * kBlock) p[i] = 0u;
+}
+
+// The identity a tagged word carries for this dispatch: {dispatch id, queue pointer, tag}.
+__global__ __launch_bounds__(kWave) void call_identity_kernel(unsigned long long* __restrict__ out) {
+    if (threadIdx.x == 0) {
+        out[0] = kvattn_dispatch_id();
+        out[1] = (unsigned long long)(uintptr_t)__builtin_amdgcn_queue_ptr();
+        out[2] = call_tag();
+    }
 }
 
 // Stream-ordered write of the device length (one lane, one vector store).
@@ -1832,8 +1881,11 @@ int launch_split(const SplitArgs& a, int kv_dtype, int mode, bool lat, hipStream
     }
     const bool des = mode == kDesignated || mode == kDesignatedDev;
     if (des) grid = designated_grid(a.B, a.NH, a.S);
+    if (des && (long long)a.B * a.NH >= (1 << 16)) return KVATTN_ERR_GRID_TOO_LARGE;
     int spec = split_spec(args);
-    int pks = a.S | (des && xcd_local_layout(a.B, a.NH) ? kXcdLocalBit : 0);
+    int pks = split_pks(args, des);
+    int pnh = split_pnh(args, des);
+    int bnh = a.B * a.NH;
     void* params[] = SPLIT_PARAMS(args);
     KV_HIP(hipLaunchKernel(fn, dim3((unsigned)grid), dim3(threads), params, 0, stream));
     return KVATTN_OK;
@@ -1900,7 +1952,9 @@ int launch_coop(const SplitArgs& a, int kv_dtype, bool lat, hipStream_t stream) 
         if (blocks > cap) continue;
         SplitArgs args = a;
         int spec = split_spec(args);
-        int pks = args.S;
+        int pks = split_pks(args, false);
+        int pnh = split_pnh(args, false);
+        int bnh = a.B * a.NH;
         void* params[] = SPLIT_PARAMS(args);
         KV_HIP(hipLaunchCooperativeKernel(fn, dim3((unsigned)blocks), dim3(threads), params, 0, stream));
         return KVATTN_OK;
@@ -1955,7 +2009,9 @@ int launch_graph_pair(const SplitArgs& a, int kv_dtype, bool lat, hipStream_t st
         });
         SplitArgs args = a;
         int spec = split_spec(args);
-        int pks = args.S;
+        int pks = split_pks(args, false);
+        int pnh = split_pnh(args, false);
+        int bnh = a.B * a.NH;
         void* params[] = SPLIT_PARAMS(args);
         void* mparams[] = MERGE_PARAMS(args);
         hipGraph_t g = nullptr;
@@ -1990,17 +2046,16 @@ int launch_graph_pair(const SplitArgs& a, int kv_dtype, bool lat, hipStream_t st
     return KVATTN_OK;
 }
 
-// Workspace, every region 256-byte aligned:
+// Workspace (a caller's buffer or the static scratch), every region 256-byte aligned:
 //   status [64] u32                           sticky status words (kWsStatus*)
-//   counters [B*NH] u32                       last-block merge
+//   counters u32                              last-block merge, one per (b,h)
 //   part_max, part_lse [B*NH*S] f32, part_out [B*NH*S*64] f32   reference-format partials
-//   tag_ml [B*NH*S*2] u64, tag_out [B*NH*S*64] u64   designated merger
+//   tag_ml [B*NH*S*16] u64, tag_out [B*NH*S*64] u64   designated merger
 // kvattn_workspace_init zeroes it once; the last-block kernels leave the counters at 0, and
 // the designated merger's words carry the dispatch that wrote them, so they need no clearing.
-// The counters and partials are laid out from the front of the buffer and the tags from
-// its end, so that calls planned with different slot counts S on one buffer never put a
-// tag word where another call left a partial: a float pair read as a tagged word would
-// pass for a published partial.
+// A caller's buffer is laid out by kvattn_layout::ws_layout (layout.hpp), so that calls of
+// different plans on one buffer never find their counters or tags where another left
+// partials.
 struct Workspace {
     unsigned* status;
     unsigned* counters;
@@ -2011,42 +2066,26 @@ struct Workspace {
     unsigned long long* tag_out;
     size_t bytes;
 };
+static_assert(kvattn_layout::kWsStatusBytes == kWsStatusBytes && kvattn_layout::kWsMlWords == kMlStride &&
+                  kvattn_layout::kWsChannels == kHeadDim, "workspace layout constants");
 
-// Bytes of each region for B*NH heads of S slots, every one rounded up to 256.
-struct RegionSizes {
-    size_t nc, nm, no, ntm, nto;
-    size_t body() const { return 2 * nm + no + ntm + nto; }   // partials and tagged words
-};
-RegionSizes region_sizes(int B, int NH, int S) {
-    const size_t bh = (size_t)B * NH;
-    return {align_up(bh * sizeof(unsigned), 256), align_up(bh * S * sizeof(float), 256),
-            align_up(bh * S * kHeadDim * sizeof(float), 256),
-            align_up(bh * S * kMlStride * sizeof(unsigned long long), 256),
-            align_up(bh * S * kHeadDim * sizeof(unsigned long long), 256)};
-}
-
-// The partials from `body` on and the tagged words at the end of the `avail` bytes there
-// (avail below what they need: right after the partials).
-void carve_body(Workspace& w, uint8_t* body, const RegionSizes& z, size_t avail) {
-    w.part_max = (float*)body;
-    w.part_lse = (float*)(body + z.nm);
-    w.part_out = (float*)(body + 2 * z.nm);
-    const size_t end = avail >= z.body() ? avail / 256 * 256 : z.body();   // z.body() is a multiple of 256
-    w.tag_out = (unsigned long long*)(body + end - z.nto);
-    w.tag_ml = (unsigned long long*)(body + end - z.nto - z.ntm);
-}
-
-// avail: the caller's buffer size (0: the size query, the buffer exactly as large).
-Workspace carve(void* base, int B, int NH, int S, size_t avail = 0) {
-    const RegionSizes z = region_sizes(B, NH, S);
+Workspace at(uint8_t* p, const kvattn_layout::WsLayout& l) {
     Workspace w;
-    uint8_t* p = (uint8_t*)base;
     w.status = (unsigned*)p;
-    w.counters = (unsigned*)(p + kWsStatusBytes);
-    w.bytes = kWsStatusBytes + z.nc + z.body();
-    const size_t head = kWsStatusBytes + z.nc;
-    carve_body(w, p + head, z, avail >= head ? avail - head : 0);
+    w.counters = (unsigned*)(p + l.counters);
+    w.part_max = (float*)(p + l.part_max);
+    w.part_lse = (float*)(p + l.part_lse);
+    w.part_out = (float*)(p + l.part_out);
+    w.tag_ml = (unsigned long long*)(p + l.tag_ml);
+    w.tag_out = (unsigned long long*)(p + l.tag_out);
+    w.bytes = l.bytes;
     return w;
+}
+
+// avail: the caller's buffer size (0: the size query).  w.bytes is what the plan needs of a
+// buffer of that size: it fits iff w.bytes <= avail.
+Workspace carve(void* base, int B, int NH, int S, size_t avail = 0) {
+    return at((uint8_t*)base, kvattn_layout::ws_layout((long long)B * NH, S, avail));
 }
 
 // S > 0: reference partition, S slots.  S < 0: -S rows per segment.  S == 0: sized for
@@ -2259,34 +2298,6 @@ int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scal
     }
 }
 
-// A workspace the library owns for kvattn_forward_large's single launch, one per (device,
-// stream) so that calls on different streams never share one; allocated (and zeroed on the
-// stream) at the first call that needs it, grown when a later call needs more, and kept
-// until the process ends.  Calls on one stream are ordered, so they may share theirs.
-int stream_workspace(hipStream_t stream, size_t need, void*& base) {
-    int dev = 0;
-    KV_HIP(hipGetDevice(&dev));
-    static std::mutex mu;
-    static std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> owned;
-    std::lock_guard<std::mutex> lock(mu);
-    auto& w = owned[std::make_pair(dev, stream)];
-    if (w.second < need) {
-        if (w.first) {
-            KV_HIP(hipStreamSynchronize(stream));
-            KV_HIP(hipFree(w.first));
-            w = {nullptr, 0};
-        }
-        KV_HIP(hipMalloc(&w.first, need));
-        w.second = need;
-        const size_t words = need / 4;
-        hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)std::min<size_t>((words + kBlock - 1) / kBlock, 4096)),
-                           dim3(kBlock), 0, stream, (uint32_t*)w.first, words);
-        KV_HIP(hipGetLastError());
-    }
-    base = w.first;
-    return KVATTN_OK;
-}
-
 // ------------------------------------------------------------------------------------
 // kvattn_decode_static: the workspace in a static device array.
 // ------------------------------------------------------------------------------------
@@ -2326,13 +2337,9 @@ int scratch_base(hipStream_t stream, uint8_t*& base) {
 // The plan's workspace regions inside the scratch array; false when they do not fit.
 bool carve_scratch(uint8_t* base, int B, int NH, int S, Workspace& w) {
     if ((long long)B * NH > kScratchMaxHeads) return false;
-    const RegionSizes z = region_sizes(B, NH, S);
-    const size_t head = kWsStatusBytes + kScratchCounterBytes;
-    if (z.body() > kScratchBytes - head) return false;
-    w.status = (unsigned*)base;
-    w.counters = (unsigned*)(base + kWsStatusBytes);
-    w.bytes = head + z.body();
-    carve_body(w, base + head, z, kScratchBytes - head);
+    const kvattn_layout::WsLayout l = kvattn_layout::ws_layout((long long)B * NH, S, kScratchBytes, kScratchCounterBytes);
+    if (l.bytes > kScratchBytes) return false;
+    w = at(base, l);
     return true;
 }
 
@@ -2398,6 +2405,22 @@ int check_partials(const float* po, const float* pl, const float* pm, int S) {
     return KVATTN_OK;
 }
 
+
+// The sticky status words at st (a workspace's first 256 bytes, or the static scratch's):
+// waits for `stream`, reads the merge-timeout count, clears the words on request.
+int read_status(unsigned* st, int clear, hipStream_t stream, int* merge_timeouts) {
+    unsigned n = 0;
+    KV_HIP(hipMemcpyAsync(&n, st + kWsStatusMergeTimeouts, sizeof(n), hipMemcpyDeviceToHost, stream));
+    KV_HIP(hipStreamSynchronize(stream));
+    if (clear && n != 0) {
+        hipLaunchKernelGGL(zero_words_kernel, dim3(1), dim3(kBlock), 0, stream, (uint32_t*)st,
+                           kWsStatusBytes / sizeof(uint32_t));
+        KV_HIP(hipGetLastError());
+        KV_HIP(hipStreamSynchronize(stream));
+    }
+    if (merge_timeouts) *merge_timeouts = (int)n;
+    return n ? KVATTN_ERR_MERGE_TIMEOUT : KVATTN_OK;
+}
 }  // namespace
 
 // Shared with the other translation units of the library (not exported).
@@ -2520,22 +2543,26 @@ int kvattn_forward_large(void* out, const void* qkv, const void* kv_cache, const
         // The reference saves the merge launch for B == 1 with a cooperative launch.  On this
         // stack a cooperative dispatch costs ~20 us of GPU time even for an empty kernel
         // (2.4 us for an ordinary one), so the single launch here is the designated merger,
-        // over the reference partition, with a workspace the library keeps per stream.
+        // over the reference partition.  Its tagged partials live in the library's static
+        // scratch array (as kvattn_decode_static's do), so the call only enqueues: no
+        // allocation, no synchronisation.  A grid the GPU cannot hold at once, or tags that do
+        // not fit in the array, take the split + merge pair over the caller's partials.
         const void* fn = split_ptr_for(a, kv_dtype, kDesignated, lat);
         long long cap = 0;
         if (!fn) return KVATTN_ERR_DTYPE;
         KV_TRY(resident_capacity(fn, split_threads(lat), cap));
+        Workspace w{};
+        uint8_t* base = nullptr;
         if ((long long)B * NH * S <= cap) {
-            const size_t need = carve(nullptr, B, NH, S).bytes;
-            void* base = nullptr;
-            KV_TRY(stream_workspace(stream, need, base));
-            const Workspace w = carve(base, B, NH, S, need);
-            a.tag_ml = w.tag_ml;
-            a.tag_out = w.tag_out;
-            a.status = w.status;
-            a.barrier = reinterpret_cast<unsigned long long*>(w.status + kWsStatusBarrier);
-            a.merge_polls = g_merge_polls.load(std::memory_order_relaxed);
-            return launch_split(a, kv_dtype, kDesignated, lat, stream);
+            KV_TRY(scratch_base(stream, base));
+            if (carve_scratch(base, B, NH, S, w)) {
+                a.tag_ml = w.tag_ml;
+                a.tag_out = w.tag_out;
+                a.status = w.status;
+                a.barrier = reinterpret_cast<unsigned long long*>(w.status + kWsStatusBarrier);
+                a.merge_polls = g_merge_polls.load(std::memory_order_relaxed);
+                return launch_split(a, kv_dtype, kDesignated, lat, stream);
+            }
         }
     }
     KV_TRY(launch_split(a, kv_dtype, kPartialsOnly, lat, stream));
@@ -2592,19 +2619,22 @@ int kvattn_workspace_status(void* workspace, size_t workspace_bytes, int clear, 
     if (!workspace) return KVATTN_ERR_NULL_POINTER;
     if (!aligned16(workspace)) return KVATTN_ERR_MISALIGNED;
     if (workspace_bytes < kWsStatusBytes) return KVATTN_ERR_WORKSPACE;
+    return read_status((unsigned*)workspace, clear, (hipStream_t)stream_v, merge_timeouts);
+}
+
+int kvattn_call_identity(unsigned long long* out, void* stream) {
+    if (!out) return KVATTN_ERR_NULL_POINTER;
+    if ((uintptr_t)out & 7u) return KVATTN_ERR_MISALIGNED;
+    hipLaunchKernelGGL(call_identity_kernel, dim3(1), dim3(kWave), 0, (hipStream_t)stream, out);
+    KV_HIP(hipGetLastError());
+    return KVATTN_OK;
+}
+
+int kvattn_scratch_status(int clear, void* stream_v, int* merge_timeouts) {
     hipStream_t stream = (hipStream_t)stream_v;
-    unsigned* st = (unsigned*)workspace;
-    unsigned n = 0;
-    KV_HIP(hipMemcpyAsync(&n, st + kWsStatusMergeTimeouts, sizeof(n), hipMemcpyDeviceToHost, stream));
-    KV_HIP(hipStreamSynchronize(stream));
-    if (clear && n != 0) {
-        hipLaunchKernelGGL(zero_words_kernel, dim3(1), dim3(kBlock), 0, stream, (uint32_t*)st,
-                           kWsStatusBytes / sizeof(uint32_t));
-        KV_HIP(hipGetLastError());
-        KV_HIP(hipStreamSynchronize(stream));
-    }
-    if (merge_timeouts) *merge_timeouts = (int)n;
-    return n ? KVATTN_ERR_MERGE_TIMEOUT : KVATTN_OK;
+    uint8_t* base = nullptr;
+    KV_TRY(scratch_base(stream, base));
+    return read_status((unsigned*)base, clear, stream, merge_timeouts);
 }
 
 int kvattn_set_merge_poll_limit(int polls) {

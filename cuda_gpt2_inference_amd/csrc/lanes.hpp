@@ -234,14 +234,28 @@ __device__ __forceinline__ uint8_t w8_code(float x, float scale) {
 }
 
 // ------------------------------------------------------------------------------------
-// Tagged words handed between workgroups: a float in the low half, the call's tag (the
-// dispatch id with the top bit set, so that a zeroed buffer holds no valid word) in the
+// Tagged words handed between workgroups: a float in the low half, the call's tag in the
 // high half.  A word counts only for the dispatch that wrote it, so slots need no clearing.
 // Published with plain stores when writer and reader run on one XCD (the word lands in that
 // XCD's L2, where the reader's agent-scope loads hit it), else with write-through (sc1)
 // stores, which agent-scope loads see from any XCD.
+//
+// The tag is the dispatch id plus a per-queue offset, with the top bit set (so that a zeroed
+// buffer holds no valid word).  Dispatch ids count packets per HSA queue: every queue starts
+// at 0, and HIP spreads its streams over several queues (4 here), so two streams' calls carry
+// equal ids all the time.  The offset, a multiplicative hash of the queue's address (the
+// queue pointer the dispatch arrives with), keeps those apart: on one queue the tags of 2^31
+// consecutive dispatches are distinct; a word from another queue matches only when the two
+// queues' dispatch counts differ by exactly the difference of their offsets (mod 2^31), a
+// pseudo-random value fixed per pair of queues.
 // ------------------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t call_tag() { return (uint32_t)kvattn_dispatch_id() | 0x80000000u; }
+__device__ __forceinline__ uint32_t queue_salt() {
+    const uint64_t q = (uint64_t)(uintptr_t)__builtin_amdgcn_queue_ptr();
+    return (uint32_t)(((q >> 6) * 0x9E3779B97F4A7C15ull) >> 32);
+}
+__device__ __forceinline__ uint32_t call_tag() {
+    return ((uint32_t)kvattn_dispatch_id() + queue_salt()) | 0x80000000u;
+}
 __device__ __forceinline__ void publish_word(unsigned long long* p, unsigned long long w, bool xcd_local) {
     if (xcd_local) *p = w;
     else __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -255,7 +269,10 @@ __device__ __forceinline__ unsigned long long tagged_word(float v, uint32_t tag)
 __device__ __forceinline__ bool word_is(unsigned long long w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
 __device__ __forceinline__ float word_value(unsigned long long w) { return __uint_as_float((uint32_t)w); }
 
+using kvattn_layout::dense_slot;
 using kvattn_layout::div_uniform;
+using kvattn_layout::guess_rows;
+using kvattn_layout::guess_slot_live;
 using kvattn_layout::xcd_slot;
 
 // s_waitcnt vmcnt(0) (GFX9 encoding: expcnt and lgkmcnt fields left at their maximum),

@@ -89,6 +89,8 @@ SIGNATURES = {
     "kvattn_workspace_init": (_i, [_vp, _sz, _vp]),
     "kvattn_workspace_status": (_i, [_vp, _sz, _i, _vp, ctypes.POINTER(_i)]),
     "kvattn_set_merge_poll_limit": (_i, [_i]),
+    "kvattn_scratch_status": (_i, [_i, _vp, ctypes.POINTER(_i)]),
+    "kvattn_call_identity": (_i, [_vp, _vp]),
     "kvattn_plan": (_i, [_i, _i, _i, _i, _i, _i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i),
                          ctypes.POINTER(_i)]),
     "kvattn_decode": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp, _sz, _i, _i, _i, _vp]),
@@ -249,6 +251,23 @@ def workspace_status(workspace, nbytes, clear=False, stream=None) -> int:
     if st not in (OK, ERR_MERGE_TIMEOUT):
         _check(st, "kvattn_workspace_status")
     return n.value
+
+
+def scratch_status(clear=False, stream=None) -> int:
+    """Merges that stopped waiting in the library's static scratch array on the current device
+    (kvattn_scratch_status; the workspace of decode_static and of forward_large's single
+    launch; synchronises the stream).  Returns the count."""
+    n = _i()
+    st = lib().kvattn_scratch_status(int(bool(clear)), _stream(stream), ctypes.byref(n))
+    if st not in (OK, ERR_MERGE_TIMEOUT):
+        _check(st, "kvattn_scratch_status")
+    return n.value
+
+
+def call_identity(out, stream=None) -> None:
+    """Enqueue one dispatch that writes {dispatch id, queue address, tag} into out (3 int64
+    words on the device): the identity a tagged partial word of that stream carries."""
+    _check(lib().kvattn_call_identity(_ptr(out), _stream(stream)), "kvattn_call_identity")
 
 
 def set_merge_poll_limit(polls: int) -> int:

@@ -135,9 +135,16 @@ int kvattn_forward_small(void* out, const void* qkv, const void* kv_cache,
  * reference, B == 1 takes a single launch and B > 1 (or a capture) the split + merge pair
  * over the caller's partials.  The single launch is the designated merger (SPLIT_DESIGNATED
  * over the reference partition), not a cooperative launch: on this stack a cooperative
- * dispatch alone costs ~20 us of GPU time.  Its tagged partials live in a workspace the
- * library allocates per (device, stream) at the first such call and keeps; S > 64, or a grid
- * the GPU cannot hold at once, takes the split + merge pair instead.
+ * dispatch alone costs ~20 us of GPU time.  Its tagged partials live in the library's static
+ * scratch array (the one kvattn_decode_static uses), so the call only enqueues: it allocates
+ * nothing and never synchronises, as the reference's launches over caller-owned partials
+ * (inference_gpt2_opt.cu:710-716).  S > 64, a grid the GPU cannot hold at once, or more than
+ * about 9,200 slots (NH * S) take the split + merge pair instead.  Like kvattn_decode_static, calls
+ * that overlap in time on one GPU (unordered streams, concurrent host threads) share the
+ * array and may find each other's words: a merger never takes another call's word (each
+ * carries its call's identity), but may wait for its bound and compute its producers'
+ * segments itself (kvattn_scratch_status counts those).  Ordered calls, on one stream or
+ * across streams, do not interfere.
  * Replaces attention_forward_kv_large (Inference_gpt2/attention_kvcache.cuh:464-487) and
  * attention_forward_kv_large_w8 (Inference_gpt2/attention_kvcache_w8.cuh:541-566). */
 int kvattn_forward_large(void* out, const void* qkv, const void* kv_cache,
@@ -184,12 +191,29 @@ int kvattn_workspace_init(void* workspace, size_t workspace_bytes, void* stream)
  * cooperative merger that stops waiting at the grid barrier writes NaN for its (b,h).
  * *merge_timeouts (may be NULL) receives that number; clear != 0 resets it.
  * Returns KVATTN_ERR_MERGE_TIMEOUT when it is non-zero, else KVATTN_OK.  Partials left by
- * such a call are never taken for a later call's (each partial word carries the dispatch
- * that wrote it), so the workspace stays usable without re-initialising.
+ * such a call are never taken for a later call's (each partial word carries the dispatch that
+ * wrote it and that dispatch's hardware queue), so the workspace stays usable without
+ * re-initialising.
  * No reference counterpart: the reference has no in-kernel wait that can give up, and
  * reports errors by exiting (common.h:123-130). */
 int kvattn_workspace_status(void* workspace, size_t workspace_bytes, int clear, void* stream,
                             int* merge_timeouts);
+
+/* kvattn_workspace_status for the library's static scratch array on the current device (the
+ * workspace of kvattn_decode_static and of kvattn_forward_large's single launch): waits for
+ * `stream`, then *merge_timeouts (may be NULL) receives the number of merges that stopped
+ * waiting there since the array was first used or last cleared; clear != 0 resets it.
+ * Returns KVATTN_ERR_MERGE_TIMEOUT when it is non-zero, else KVATTN_OK.
+ * No reference counterpart (the reference has no in-kernel wait that can give up). */
+int kvattn_scratch_status(int clear, void* stream, int* merge_timeouts);
+
+/* Enqueue on `stream` one dispatch that writes the identity the tagged partial words of a
+ * dispatch on that stream carry: out[0] its dispatch id (counted per hardware queue),
+ * out[1] the address of its hardware queue, out[2] its 32-bit tag (the dispatch id plus a hash
+ * of the queue address, top bit set).  out: 3 device words, 8-byte aligned.
+ * No reference counterpart: a testing hook showing that calls on different streams, whose
+ * dispatch ids coincide, never share a tag. */
+int kvattn_call_identity(unsigned long long* out, void* stream);
 
 /* Bound on the polls of a designated merger waiting for its producers' partials (and of a
  * cooperative merger at the grid barrier), for launches (and captures) from this call on,
@@ -224,10 +248,17 @@ int kvattn_plan(int B, int NH, int hs, int maxT, int len_hint, int S, int strate
  *              device) and the per-sequence count from each length.
  *   workspace  device memory of kvattn_workspace_bytes(B, NH, hs, maxT, S) bytes,
  *              initialised once with kvattn_workspace_init; may be NULL for
- *              FUSED_SINGLE.  Calls sharing a workspace must be ordered (one stream).
- *   workspace_bytes  the buffer's actual size.  One buffer, sized for the largest plan,
- *              may serve calls planned with different S: the partials are laid out
- *              from its start and the designated merger's tagged words from its end.
+ *              FUSED_SINGLE.  Calls sharing a workspace must be ordered: on one stream,
+ *              or on several streams ordered by events (the designated merger's words
+ *              carry the dispatch and its hardware queue, so a word another stream's call
+ *              left is never taken for this call's).  Calls that overlap in time race.
+ *   workspace_bytes  the buffer's actual size, the same for every call on the buffer.
+ *              One buffer, sized for the largest plan, may serve calls of different
+ *              plans (other B, NH or S): the last-block counters sit in a region whose
+ *              size follows from workspace_bytes alone, the partials are laid out from
+ *              the region's end and the designated merger's tagged words from the
+ *              buffer's end, so no call finds its counters or tags where another left
+ *              partials.
  */
 int kvattn_decode(void* out, const void* qkv, const void* kv_cache, const float* kv_scale,
                   int B, int NH, int hs, int maxT,
@@ -245,9 +276,11 @@ int kvattn_decode(void* out, const void* qkv, const void* kv_cache, const float*
  * less its status words and counters) within 8 MiB - 64.25 KiB, else KVATTN_ERR_WORKSPACE;
  * strategies AUTO, FUSED_SINGLE, SPLIT_MERGE, SPLIT_LASTBLOCK, SPLIT_DESIGNATED (the
  * cooperative launch and the library's graph pair return KVATTN_ERR_STRATEGY: the runtime may
- * allocate for them).  Every call on one GPU shares that GPU's array, which keeps the last
- * call's contents: calls that overlap in time on one GPU (unordered streams, concurrent host
- * threads) race; calls ordered on one stream do not. */
+ * allocate for them).  Every call on one GPU shares that GPU's array (with
+ * kvattn_forward_large's single launch), which keeps the last call's contents: calls that
+ * overlap in time on one GPU (unordered streams, concurrent host threads) race; calls ordered
+ * on one stream, or across streams by events, do not.  kvattn_scratch_status reads its merge
+ * timeouts. */
 int kvattn_decode_static(void* out, const void* qkv, const void* kv_cache, const float* kv_scale,
                          int B, int NH, int hs, int maxT,
                          const int* d_cur_len, int lens_per_seq, int len_hint,

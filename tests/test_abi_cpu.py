@@ -51,14 +51,20 @@ def test_strerror_covers_every_status():
 
 def test_workspace_bytes():
     kvattn = _kv()
-    # 256 bytes of status words, counters (B*NH u32), part_max, part_lse (B*NH*S f32),
-    # part_out (B*NH*S*64 f32), the designated merger's tagged words ({max, exp-sum} in a
-    # 128-byte line per slot, B*NH*S*16 u64, and B*NH*S*64 u64 channel words), every region
-    # rounded up to 256 bytes.
+    # 256 bytes of status words, part_max, part_lse (B*NH*S f32), part_out (B*NH*S*64 f32), the
+    # designated merger's tagged words ({max, exp-sum} in a 128-byte line per slot, B*NH*S*16
+    # u64, and B*NH*S*64 u64 channel words), every region rounded up to 256 bytes; then room for
+    # a counter region of 4 bytes per 904 bytes of buffer (904 = the partial and tag bytes of
+    # one slot, so every plan the buffer holds finds a counter per head there): the smallest
+    # size x with x - (4 x / 904 + 255) >= that sum, rounded up to 256.
     def expect(B, NH, S):
         up = lambda x: (x + 255) // 256 * 256  # noqa: E731
-        return (256 + up(B * NH * 4) + 2 * up(B * NH * S * 4) + up(B * NH * S * 64 * 4)
-                + up(B * NH * S * 16 * 8) + up(B * NH * S * 64 * 8))
+        fixed = (256 + 2 * up(B * NH * S * 4) + up(B * NH * S * 64 * 4)
+                 + up(B * NH * S * 16 * 8) + up(B * NH * S * 64 * 8))
+        x = up(-(-(fixed + 255) * 904 // 900))
+        counters = up(x // 904 * 4)
+        assert x >= fixed + counters and counters >= B * NH * 4
+        return x
     assert kvattn.workspace_bytes(1, 12, 64, 1024, 8) == expect(1, 12, 8)
     assert kvattn.workspace_bytes(64, 12, 64, 8192, 0) == expect(64, 12, 8192 // 64)
     assert kvattn.workspace_bytes(2, 3, 64, 1000, -100) == expect(2, 3, 10)

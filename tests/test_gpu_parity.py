@@ -244,10 +244,10 @@ def test_merge_of_oracle_partials(dev):
 
 @pytest.mark.parametrize("B", [1, 2])
 def test_forward_large_reference_semantics(dev, B):
-    """attention_forward_kv_large: B == 1 -> one launch (the designated merger, with the
-    library's own per-stream workspace), B > 1 -> split + merge over caller-owned partials
-    of S = 8 segments (inference_gpt2_opt.cu:711-716).  Called twice per dtype, so that the
-    second call reuses the library's workspace."""
+    """attention_forward_kv_large: B == 1 -> one launch (the designated merger, its tagged
+    words in the library's static scratch array), B > 1 -> split + merge over caller-owned
+    partials of S = 8 segments (inference_gpt2_opt.cu:711-716).  Called twice per dtype, so
+    that the second call finds the first one's words in the array."""
     import torch
     kvattn = _kv()
     NH, maxT, S = 12, 1024, 8
