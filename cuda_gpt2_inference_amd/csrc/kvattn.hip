@@ -65,6 +65,10 @@ constexpr int kMaxDesignatedSegments = 64;  // the designated merger follows one
 // Workspace status words (the first 256 bytes of a kvattn_decode workspace).
 constexpr int kWsStatusMergeTimeouts = 0;   // merges that stopped waiting (a sticky count)
 constexpr int kWsStatusBarrier = 2;         // u64 {generation, count} of the cooperative grid barrier
+// Designated producers of an XCD-local grid that published write-through because their
+// merger's XCD word named another XCD (a count), or was not there yet when they looked.
+constexpr int kWsStatusXcdRemote = 4;
+constexpr int kWsStatusXcdUnseen = 5;
 constexpr size_t kWsStatusBytes = 256;
 
 // ------------------------------------------------------------------------------------
@@ -170,6 +174,18 @@ __device__ __forceinline__ float dot_chunk(const float (&q)[Row<DT>::kElems], co
 // Attended positions of sequence b: device length clamped to [0, maxT-1], plus one.
 __device__ __forceinline__ int seq_total(const int* cur_len, int lens_per_seq, int b, int maxT) {
     int cl = cur_len[lens_per_seq ? b : 0];
+    cl = cl < 0 ? 0 : (cl > maxT - 1 ? maxT - 1 : cl);
+    return cl + 1;
+}
+
+// seq_total for a wave-uniform b, read with a scalar load: the lengths are written by earlier
+// dispatches or the host, never during a launch, so the constant address space applies.  A
+// scalar load is waited for on its own counter, so waiting for the length does not wait for
+// the vector loads (K/V tiles, q) or stores issued before it, as it would on the in-order
+// vector memory counter.
+typedef const __attribute__((address_space(4))) int* ConstIntPtr;
+__device__ __forceinline__ int seq_total_uniform(const int* cur_len, int lens_per_seq, int b, int maxT) {
+    int cl = ((ConstIntPtr)cur_len)[lens_per_seq ? b : 0];
     cl = cl < 0 ? 0 : (cl > maxT - 1 ? maxT - 1 : cl);
     return cl + 1;
 }
@@ -841,6 +857,7 @@ constexpr int kXcdLocalBit = 1 << 30;
 constexpr int kSlotMask = (1 << 17) - 1;
 constexpr int kHintSegShift = 17;
 constexpr int kLensBit = 1 << 24;
+constexpr int kXcdRotShift = 25;   // bits 25-27: the test rotation of xcd_slot_rotated
 inline int split_spec(const SplitArgs& a) { return a.lens_per_seq ? -1 : (a.spec_rows > 0 ? a.spec_rows : 0); }
 #define SPLIT_PARAMS(x) {&(x).kv, &(x).qkv, &(x).cur_len, &pnh, &(x).maxT, &pks, &(x).seg_rows, &bnh, \
                          &spec, &(x).B, &(x)}
@@ -907,7 +924,7 @@ __device__ __forceinline__ int seg_count(int seg_rows, int total, int heads, int
 __device__ __forceinline__ bool locate(const SplitArgs& a, int BNH, int x, Item& it, bool dense) {
     if (dense || !a.lens_per_seq || a.seg_rows == 0) {
         if (!dense_slot(x, a.S, BNH, a.NH, it.b, it.h, it.s)) return false;
-        it.total = seq_total(a.cur_len, a.lens_per_seq, it.b, a.maxT);
+        it.total = seq_total_uniform(a.cur_len, a.lens_per_seq, it.b, a.maxT);
         it.rows = 0;
         it.n_seg = a.seg_rows != 0 ? seg_count(a.seg_rows, it.total, a.B * a.NH, it.rows) : a.S;
         return it.s < it.n_seg;
@@ -997,13 +1014,18 @@ __host__ __device__ __forceinline__ long long designated_grid(int B, int NH, int
     return xcd_local_layout(B, NH) ? 8ll * ((B * NH + 7) / 8) * S : (long long)B * NH * S;
 }
 
+// Rotation of the designated grid's producers against their merger's XCD
+// (kvattn_set_xcd_layout_offset, a test setting; 0 in use).
+std::atomic<int> g_xcd_rot{0};
+
 // pk_S of a split launch: the slot count and, for the designated instances, the XCD-local
-// layout bit and the length hint in the form their first requests use (the segments the hint
-// puts in use, per-sequence lengths).
+// layout bit (and its test rotation) and the length hint in the form their first requests use
+// (the segments the hint puts in use, per-sequence lengths).
 inline int split_pks(const SplitArgs& a, bool des) {
     int pks = a.S;
     if (des) {
-        if (xcd_local_layout(a.B, a.NH)) pks |= kXcdLocalBit;
+        if (xcd_local_layout(a.B, a.NH))
+            pks |= kXcdLocalBit | (g_xcd_rot.load(std::memory_order_relaxed) & 7) << kXcdRotShift;
         if (a.lens_per_seq) pks |= kLensBit;
         else if (a.seg_rows > 0 && a.spec_rows > 0)
             pks |= std::min(ceil_div_i(a.spec_rows, a.seg_rows), kMaxDesignatedSegments) << kHintSegShift;
@@ -1107,7 +1129,7 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
     // Designated grids of the XCD-local layout: the slot this workgroup works on (every segment
     // of a head on one XCD).
     const bool xl = kDesMode && (pk_S & kXcdLocalBit) != 0;
-    const int vbx = xl ? xcd_slot(blockIdx.x, a.S) : (int)blockIdx.x;
+    const int vbx = xl ? xcd_slot_rotated(blockIdx.x, a.S, (pk_S >> kXcdRotShift) & 7) : (int)blockIdx.x;
 
     // Uniform lengths with fixed-size segments: (b, h, s) and the segment's nominal rows
     // [j0, min(j0 + seg_rows, maxT)) follow from blockIdx alone, and the nominal range
@@ -1165,6 +1187,20 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
         }
     }
 
+    // Designated grids: the call's tag, and in the XCD-local layout this wave's XCD.  Every
+    // segment of a head is laid out on the merger's XCD (xcd_slot), where the producers' plain
+    // stores stay in the L2 the merger polls.  That rests on how the hardware hands workgroups
+    // to XCDs; a producer whose stores the merger would not see holds it for its whole poll
+    // bound.  So each merger (segment 0 of a real head) publishes the XCD it runs on,
+    // write-through, once it knows the length (below, after locate); each producer reads that
+    // word once its own tiles are consumed and publishes with plain stores only when it names
+    // its own XCD, write-through otherwise (counted in the workspace's status words).
+    uint32_t des_tag = 0, my_xcc = 0;
+    if constexpr (kDesMode) {
+        des_tag = call_tag();
+        if (xl) my_xcc = xcc_id();
+    }
+
     // The work of one segment `it` (active: the workgroup has one; the cooperative launch
     // also runs it without, for the grid barrier).  The guess comes in through the
     // parameters (spec: made; spec_tile: holds this wave's tile; [spec_j0, spec_end): its
@@ -1211,6 +1247,7 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                 Slot sl{};
                 FreshDst fd{};
                 PagedView pv{};
+                unsigned long long mword = 0;   // designated producer: the merger's XCD word
                 if constexpr (kPaged) {
                     q0 = load_q<DT>(a.qkv, it.b, it.h, a.NH, slice);
                     if constexpr (kFresh) fr = load_fresh<DT>(a.qkv, it.b, it.h, a.NH, slice);
@@ -1249,6 +1286,13 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                         online_rows_from<DT, kU, kFresh, kHwDot>(tx, q0, sl, x0, x1, slot_row, a.qscale, fr, fd, cur, m,
                                                                  l, acc);
                 }
+                // A producer's look at its merger's XCD word: requested once its tiles are consumed,
+                // needed only when it publishes.  (Requested before the tiles are consumed, it
+                // found the word not yet written for a fifth of the producers, which then published
+                // write-through: +0.2 us per call.)
+                if constexpr (kDes) {
+                    if (xl && it.s != 0 && wave == 0) mword = get_word(a.tag_ml + (size_t)kMlStride * bh * a.S);
+                }
 
                 // Combine the row slots of this wave, then the 4 waves.
                 const float mw = slot_reduce<R::kLanes, true>(m);
@@ -1274,13 +1318,19 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                         // The only segment of its (b,h): the result needs no merge.
                         store_out<DT>(a.out, (size_t)bh * kHeadDim + lane, A / L);
                     } else if constexpr (kDes) {
-                        const uint32_t tag = call_tag();
+                        const uint32_t tag = des_tag;
                         if (it.s != 0) {
-                            // Producer: publish the tagged partial and finish; nothing waits.
-                            publish_word(a.tag_out + pidx * kHeadDim + lane, tagged_word(A, tag), xl);
+                            // Producer: publish the tagged partial and finish; nothing waits.  Plain
+                            // stores only when the merger's word names this XCD.
+                            const bool seen = xl && word_is(mword, tag);
+                            const bool local = seen && (uint32_t)mword == my_xcc;
+                            publish_word(a.tag_out + pidx * kHeadDim + lane, tagged_word(A, tag), local);
                             if (lane == 0) {
-                                publish_word(a.tag_ml + kMlStride * pidx, tagged_word(Mb * kLn2, tag), xl);
-                                publish_word(a.tag_ml + kMlStride * pidx + 1, tagged_word(L, tag), xl);
+                                publish_word(a.tag_ml + kMlStride * pidx, tagged_word(Mb * kLn2, tag), local);
+                                publish_word(a.tag_ml + kMlStride * pidx + 1, tagged_word(L, tag), local);
+                                if (xl && !local)
+                                    __hip_atomic_fetch_add(a.status + (seen ? kWsStatusXcdRemote : kWsStatusXcdUnseen),
+                                                           1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                             }
                         } else {
                             // Designated merger (segment 0): lane u follows segment u.  A head's
@@ -1577,6 +1627,12 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
         const bool active = locate(a, BNH, vbx, it, kDesMode);
         if constexpr (kMode != kCoopMerge) {
             if (!active) return;
+        }
+        // The merger's XCD word (segment 0 of a real head, whose slot is vbx).
+        if constexpr (kDesMode) {
+            if (xl && it.s == 0 && threadIdx.x == 0)
+                __hip_atomic_store(a.tag_ml + (size_t)kMlStride * vbx, ((unsigned long long)des_tag << 32) | my_xcc,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         segment(it, active, g_tile, g_q, g_fresh, g_on, g_has_tile, g_w0, g_w1, g_j0, g_end);
     }
@@ -2636,6 +2692,8 @@ int kvattn_scratch_status(int clear, void* stream_v, int* merge_timeouts) {
     KV_TRY(scratch_base(stream, base));
     return read_status((unsigned*)base, clear, stream, merge_timeouts);
 }
+
+int kvattn_set_xcd_layout_offset(int rot) { return g_xcd_rot.exchange(rot & 7); }
 
 int kvattn_set_merge_poll_limit(int polls) {
     return g_merge_polls.exchange(polls < 0 ? kDefaultMergePolls : polls);

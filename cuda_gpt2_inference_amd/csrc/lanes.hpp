@@ -256,6 +256,13 @@ __device__ __forceinline__ uint32_t queue_salt() {
 __device__ __forceinline__ uint32_t call_tag() {
     return ((uint32_t)kvattn_dispatch_id() + queue_salt()) | 0x80000000u;
 }
+
+// The XCD (accelerator complex die) this wave runs on: HW_REG_XCC_ID bits 3:0.
+__device__ __forceinline__ uint32_t xcc_id() {
+    uint32_t v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+    return v & 0xFu;
+}
 __device__ __forceinline__ void publish_word(unsigned long long* p, unsigned long long w, bool xcd_local) {
     if (xcd_local) *p = w;
     else __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -274,6 +281,7 @@ using kvattn_layout::div_uniform;
 using kvattn_layout::guess_rows;
 using kvattn_layout::guess_slot_live;
 using kvattn_layout::xcd_slot;
+using kvattn_layout::xcd_slot_rotated;
 
 // s_waitcnt vmcnt(0) (GFX9 encoding: expcnt and lgkmcnt fields left at their maximum),
 // fenced against compiler reordering on both sides.

@@ -29,6 +29,18 @@ KVATTN_LAYOUT_FN int xcd_slot(int x, int S) {
     return ((k << 3) + r) * S + s;
 }
 
+// xcd_slot with the non-first members of each group moved `rot` XCDs on (mod 8): member
+// s > 0 of group 8k + r is workgroup 8 (S k + s) + (r + rot) % 8, member 0 stays at
+// 8 S k + r.  Still a bijection, and member 0 of a group still comes before its other
+// members in dispatch order; with rot != 0 those members run on another XCD than member 0.
+// A test setting: it puts a designated merger and its producers on different XCDs on purpose.
+KVATTN_LAYOUT_FN int xcd_slot_rotated(int x, int S, int rot) {
+    const int r = x & 7, j = x >> 3;
+    const int k = div_uniform(j, S), s = j - k * S;
+    const int rr = s == 0 ? r : ((r - rot) & 7);
+    return ((k << 3) + rr) * S + s;
+}
+
 // Slot v of a dense grid of S slots per (b,h) (head bh = v / S, segment s = v % S, sequence
 // b = bh / NH) of BNH = B * NH heads: false for the slots beyond the last head (b >= B),
 // which a designated grid padded to whole rounds of 8 heads holds and whose workgroups must

@@ -91,6 +91,7 @@ SIGNATURES = {
     "kvattn_set_merge_poll_limit": (_i, [_i]),
     "kvattn_scratch_status": (_i, [_i, _vp, ctypes.POINTER(_i)]),
     "kvattn_call_identity": (_i, [_vp, _vp]),
+    "kvattn_set_xcd_layout_offset": (_i, [_i]),
     "kvattn_plan": (_i, [_i, _i, _i, _i, _i, _i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i),
                          ctypes.POINTER(_i)]),
     "kvattn_decode": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp, _sz, _i, _i, _i, _vp]),
@@ -268,6 +269,12 @@ def call_identity(out, stream=None) -> None:
     """Enqueue one dispatch that writes {dispatch id, queue address, tag} into out (3 int64
     words on the device): the identity a tagged partial word of that stream carries."""
     _check(lib().kvattn_call_identity(_ptr(out), _stream(stream)), "kvattn_call_identity")
+
+
+def set_xcd_layout_offset(rot: int) -> int:
+    """Test setting: designated producers `rot` XCDs away from their merger (0: the layout in
+    use).  Returns the previous setting."""
+    return int(lib().kvattn_set_xcd_layout_offset(int(rot)))
 
 
 def set_merge_poll_limit(polls: int) -> int:

@@ -215,6 +215,17 @@ int kvattn_scratch_status(int clear, void* stream, int* merge_timeouts);
  * dispatch ids coincide, never share a tag. */
 int kvattn_call_identity(unsigned long long* out, void* stream);
 
+/* Moves every designated producer of an XCD-local grid (8 or more (b,h) rows) `rot` XCDs
+ * (mod 8) away from its merger, for launches (and captures) from this call on, process-wide;
+ * 0 (the default) keeps each head's segments on one XCD.  Returns the previous setting.
+ * Each designated merger publishes the XCD it runs on and each producer publishes its partial
+ * with plain stores (which stay in its XCD's L2) only when that XCD is its own, else
+ * write-through, so a producer placed elsewhere, by this setting or by a dispatcher that hands
+ * workgroups to XCDs otherwise than the layout expects, costs the merger no wait: the output
+ * and the merge-timeout count stay as they are.
+ * No reference counterpart: a testing hook for the layout the designated merger relies on. */
+int kvattn_set_xcd_layout_offset(int rot);
+
 /* Bound on the polls of a designated merger waiting for its producers' partials (and of a
  * cooperative merger at the grid barrier), for launches (and captures) from this call on,
  * process-wide: polls > 0 sets it, polls == 0 makes every merger of a multi-segment (b,h)

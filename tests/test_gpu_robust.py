@@ -273,3 +273,56 @@ def test_cooperative_barrier_give_up_is_reported(dev):
         torch.cuda.synchronize()
         assert_close(out2.float().cpu().numpy(), second.reference(), "bf16", f"coop S={S} after the give-up")
     assert ws.status() == 0
+
+
+def _xcd_words(ws):
+    """The workspace's status words 4 and 5: designated producers of XCD-local grids that
+    published write-through because their merger's XCD word named another XCD (4) or was not
+    there yet when they looked (5)."""
+    w = ws.buf[:256].cpu().numpy().view(np.uint32)
+    return int(w[4]), int(w[5])
+
+
+@pytest.mark.parametrize("rot", [0, 1, 3, 7])
+def test_designated_producers_on_other_xcds(dev, rot):
+    """kvattn_set_xcd_layout_offset(rot) moves every producer of an XCD-local designated grid
+    rot XCDs away from its merger, where its plain stores would stay in an L2 the merger does
+    not poll.  Each producer reads the XCD its merger publishes and then stores write-through,
+    so every output still matches the oracle and no merger stops waiting (a plain-store
+    producer elsewhere would hold its merger for the whole poll bound and count a timeout).
+    With rot != 0 every producer counts itself as remote (or as having not seen the merger's
+    word yet); with rot = 0 none finds its merger elsewhere.  Every kernel exits normally:
+    the setting only rotates the host's grid layout."""
+    import torch
+    kvattn = _kv()
+    calls = [("bf16", 1, 12, 1024, [1023], True), ("bf16", 1, 12, 1024, [1023], False),
+             ("int8", 1, 12, 1024, [1023], True), ("f32", 1, 8, 1024, [700], True),
+             ("fp8", 2, 12, 700, [699, 299], True), ("bf16", 3, 4, 2048, [2047, 1500, 900], False)]
+    prev = kvattn.set_xcd_layout_offset(rot)
+    try:
+        for i, (dtype, B, NH, maxT, cur, hinted) in enumerate(calls):
+            case = make_case(dtype, B, NH, maxT, cur, seed=1200 + 10 * rot + i)
+            qkv, cache, scale, curd = to_device(case, dev)
+            out = out_tensor(case, dev)
+            ws = kvattn.Workspace(B, NH, maxT, 0)
+            hint = int(case.cur_lens.max()) if hinted else -1
+            st, slots, rows = kvattn.plan(B, NH, HS, maxT, kv_dtype=dtype, len_hint=hint)
+            assert st == kvattn.SPLIT_DESIGNATED and B * NH >= 8, (dtype, B, NH, st)
+            rows = rows if rows > 0 else 128
+            producers = sum(NH * (-(-int(t) // rows) - 1) for t in case.totals)
+            before = _xcd_words(ws)
+            kvattn.decode(out, qkv, cache, B, NH, HS, maxT, kv_dtype=dtype, kv_scale=scale, cur_len=curd,
+                          lens_per_seq=B > 1, len_hint=hint, **ws.kwargs())
+            torch.cuda.synchronize()
+            what = f"rot {rot} call {i} {dtype} B={B} NH={NH}"
+            assert_close(out.float().cpu().numpy(), case.reference(), dtype, what)
+            assert ws.status() == 0, f"{what}: a merger stopped waiting"
+            after = _xcd_words(ws)
+            remote, unseen = after[0] - before[0], after[1] - before[1]
+            if rot:
+                assert remote + unseen == producers and remote > 0, f"{what}: remote {remote} unseen {unseen} " \
+                                                                     f"of {producers} producers"
+            else:
+                assert remote == 0, f"{what}: {remote} producers found their merger on another XCD"
+    finally:
+        kvattn.set_xcd_layout_offset(prev)
