@@ -355,3 +355,40 @@ def test_paged_seeded_shape_sweep(dev):
             kvattn.paged_decode(out, qkv, pg.cache, B, NH, HS, strategy="lastblock", **kw)
         torch.cuda.synchronize()
         assert_close(out.float().cpu().numpy(), case.reference(), dtype, name)
+
+
+@pytest.mark.parametrize("rot", [0, 2])
+@pytest.mark.parametrize("dtype", ["bf16", "int8"])
+def test_paged_designated_producers_on_other_xcds(dev, dtype, rot):
+    """The run-time XCD check on a paged cache: 12 (b,h) rows (an XCD-local designated grid),
+    64-row segments, producers rotated `rot` XCDs away from their merger
+    (kvattn_set_xcd_layout_offset).  Outputs against the oracle, no merge timeout; at rot 0 no
+    producer finds its merger elsewhere, otherwise every producer (76 here) publishes
+    write-through, counted in status words 4 (merger elsewhere) and 5 (its word not there yet)."""
+    import torch
+    kvattn = _kv()
+    B, NH, maxT, P = 3, 4, 1024, 64
+    lens = [1024, 300, 64]
+    case = make_case(dtype, B, NH, maxT, np.array(lens, np.int32) - 1, seed=83 + rot)
+    cur = torch.from_numpy(case.cur_lens.copy()).to(dev)
+    qkv = torch.from_numpy(case.qkv_raw.view(np.int16)).to(dev).view(torch.bfloat16)
+    producers = NH * sum(-(-L // 64) - 1 for L in lens)
+    prev = kvattn.set_xcd_layout_offset(rot)
+    try:
+        pg = Paged(case, P, dev, seed=5)
+        ws = kvattn.Workspace(B, NH, maxT, -64)
+        out = out_tensor(case, dev)
+        kvattn.paged_decode(out, qkv, pg.cache, B, NH, HS, kv_dtype=dtype, cur_len=cur, lens_per_seq=True,
+                            len_hint=max(lens) - 1, S=-64, strategy="designated", **ws.kwargs())
+        torch.cuda.synchronize()
+    finally:
+        kvattn.set_xcd_layout_offset(prev)
+    what = f"paged designated {dtype} rot {rot}"
+    assert_close(out.float().cpu().numpy(), case.reference(), dtype, what)
+    assert ws.status() == 0, f"{what}: a merger stopped waiting"
+    words = ws.buf[:256].cpu().numpy().view(np.uint32)
+    remote, unseen = int(words[4]), int(words[5])
+    if rot:
+        assert remote + unseen == producers and remote > 0, f"{what}: remote {remote} unseen {unseen} of {producers}"
+    else:
+        assert remote == 0, f"{what}: {remote} producers found their merger on another XCD"
