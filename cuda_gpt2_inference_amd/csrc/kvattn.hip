@@ -1806,8 +1806,6 @@ std::atomic<int> g_merge_polls{kDefaultMergePolls};
         if (st_ != KVATTN_OK) return st_; \
     } while (0)
 
-size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
-
 bool is_8bit(int dt) { return dt == KVATTN_KV_INT8 || dt == KVATTN_KV_FP8_E4M3; }
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
@@ -2194,16 +2192,83 @@ constexpr long long kStreamRows = 1 << 19; // AUTO: split + merge kernel from th
 // planned on the device from the device length when there is no hint (len_hint == -1).
 struct Plan {
     int strategy, slots, seg_rows;
-    bool lat;   // latency-bound call: 16-wave workgroups with short tiles
+    bool lat;   // the latency shape: tiles of KVATTN_SPLIT_LAT_ROWS rows (else the streaming shape's)
 };
 
 // A call is latency bound while it streams fewer rows than kStreamRows.
 bool latency_bound(int B, int NH, int total_rows) { return (long long)B * NH * total_rows < kStreamRows; }
 
+// AUTO with a length hint, one cache per call (contiguous), beyond fused_single: the plan
+// measured fastest across B = 1..64, contexts 512..8192 and the four cache types (12-layer
+// graphs on MI355X, 13 plans per shape).
+// - One segment per (b,h) (last-block instance, which then stores without a merge) when the
+//   heads alone give 192 or more workgroups and no head is longer than 512 rows; FP8 takes the
+//   streaming shape's 64-row tiles there.  (INT8 goes on to the designated merger, which
+//   measured faster at these shapes.)
+// - The designated merger while its grid stays within kAutoDesignatedMaxGrid workgroups and
+//   the call streams at most kAutoDesignatedMaxBytes: segments of max(128, maxT / 16) rows
+//   (a power of two, so at most 16 per head; up to 64 per head when fewer than 12 heads
+//   share the GPU), doubled up to 512 rows while the grid is too large; not when the
+//   doubling left 8 or more segments per head of a call above kAutoDoubledMaxBytes (96 heads
+//   x 8 segments of 256 or 512 rows: measured slower than the split + merge kernel).  8-bit
+//   caches take the streaming shape for segments of 256 rows or more on grids of up to 384
+//   workgroups (one 64-row tile per wave).
+// - Beyond that the call is bandwidth bound: with one length for every sequence, BF16 streams
+//   256-row segments with the latency shape's tiles and INT8 256-row segments with the
+//   streaming shape's (512 rows and the latency shape from contexts of 8192), through the
+//   split + merge kernels; FP32 and FP8, and per-sequence lengths (whose streaming kernel
+//   packs two segments per workgroup on the general plan: 64 sequences of up to 8192
+//   positions ran 9 % slower on 256-row segments), keep the general plan (false).
+// Returns false to leave the plan to the general rules below.
+constexpr long long kAutoDesignatedMaxGrid = 768;
+constexpr long long kAutoDesignatedMaxBytes = 64ll << 20;
+constexpr long long kAutoDoubledMaxBytes = 40ll << 20;
+bool tuned_auto(int B, int NH, int maxT, int total_hint, int kv_dtype, bool ragged, Plan& p) {
+    const long long heads = (long long)B * NH;
+    const bool k8 = is_8bit(kv_dtype);
+    const long long row_bytes = kv_dtype == KVATTN_KV_F32 ? 512 : (kv_dtype == KVATTN_KV_BF16 ? 256 : 136);
+    const long long bytes = heads * total_hint * row_bytes;
+    if (maxT <= 512 && heads >= 192 && kv_dtype != KVATTN_KV_INT8) {
+        p.strategy = KVATTN_SPLIT_LASTBLOCK;
+        p.seg_rows = 512;
+        p.slots = 1;
+        p.lat = kv_dtype != KVATTN_KV_FP8_E4M3;
+        return true;
+    }
+    // At most 16 segments per head once the heads give 192 workgroups with them; fewer heads
+    // take up to 64 (the merger's limit).
+    const int target = (int)std::min<long long>(kMaxDesignatedSegments, std::max<long long>(16, 192 / heads));
+    const int r0 = std::max(128, ceil_pow2(ceil_div_i(maxT, target)));
+    int r = r0;
+    while (heads * ceil_div_i(maxT, r) > kAutoDesignatedMaxGrid && r < 512) r <<= 1;
+    const int segs = ceil_div_i(maxT, r);
+    const long long grid = heads * segs;
+    if (grid <= kAutoDesignatedMaxGrid && bytes <= kAutoDesignatedMaxBytes &&
+        !(r > r0 && segs >= 8 && bytes > kAutoDoubledMaxBytes)) {
+        p.strategy = KVATTN_SPLIT_DESIGNATED;
+        p.seg_rows = r;
+        p.slots = segs;
+        p.lat = !(k8 && r >= 256 && grid <= 384);
+        return true;
+    }
+    if (!ragged && (kv_dtype == KVATTN_KV_BF16 || kv_dtype == KVATTN_KV_INT8)) {
+        const bool long_int8 = kv_dtype == KVATTN_KV_INT8 && maxT >= 8192;
+        p.strategy = KVATTN_SPLIT_MERGE;
+        p.seg_rows = long_int8 ? 512 : 256;
+        p.slots = ceil_div_i(maxT, p.seg_rows);
+        p.lat = kv_dtype == KVATTN_KV_BF16 || long_int8;
+        return true;
+    }
+    return false;
+}
+
 // paged: a paged cache, which has no fused_single or cooperative instance and whose
 // segments start at multiples of 64 rows (the tile), so rows per segment are planned on
 // the device unless S < 0 gives a multiple of 64.
-int make_plan(int B, int NH, int maxT, int len_hint, int S, int strategy, Plan& p, bool paged = false) {
+// ragged: per-sequence lengths.  tuned: AUTO may take tuned_auto's plan (off: the general
+// rules alone).
+int make_plan(int B, int NH, int maxT, int len_hint, int S, int strategy, int kv_dtype, Plan& p,
+              bool paged = false, bool ragged = false, bool tuned = true) {
     if (strategy < KVATTN_AUTO || strategy > KVATTN_SPLIT_DESIGNATED) return KVATTN_ERR_STRATEGY;
     if (len_hint >= maxT || len_hint < -1) return KVATTN_ERR_LENGTH;
     if (paged) {
@@ -2217,7 +2282,14 @@ int make_plan(int B, int NH, int maxT, int len_hint, int S, int strategy, Plan& 
         // the in-kernel merge while the whole call is latency bound, and split + merge
         // kernel once the call streams enough rows to be bandwidth bound.
         const bool fits = (size_t)maxT * sizeof(float) <= kFusedMaxLds;
-        if (!paged && fits && total_hint <= kFusedMaxRows) strategy = KVATTN_FUSED_SINGLE;
+        const bool fused = !paged && fits && total_hint <= kFusedMaxRows;
+        if (tuned && !fused && !paged && len_hint >= 0 && S == 0) {
+            int slots_bound = 0, rows_bound = 0;   // the workspace bound of S == 0, checked as below
+            KV_TRY(segment_slots(maxT, S, slots_bound, rows_bound));
+            if (tuned_auto(B, NH, maxT, total_hint, kv_dtype, ragged, p))
+                return (long long)B * NH * p.slots >= (1ll << 31) ? KVATTN_ERR_SHAPE : KVATTN_OK;
+        }
+        if (fused) strategy = KVATTN_FUSED_SINGLE;
         else if ((long long)B * NH * total_hint >= kStreamRows) strategy = KVATTN_SPLIT_MERGE;
         else if ((long long)B * NH * ceil_div_i(total_hint, designated_rows(total_hint, B * NH)) <= kDesignatedMaxGrid)
             strategy = KVATTN_SPLIT_DESIGNATED;
@@ -2249,7 +2321,7 @@ int make_plan(int B, int NH, int maxT, int len_hint, int S, int strategy, Plan& 
         // More segments per (b,h) than the merger follows (or longer paged segments than a
         // wave walks): AUTO takes the last-block merge with its own segmentation.
         if (!auto_strategy) return KVATTN_ERR_SPLIT;
-        return make_plan(B, NH, maxT, len_hint, S, KVATTN_SPLIT_LASTBLOCK, p, paged);
+        return make_plan(B, NH, maxT, len_hint, S, KVATTN_SPLIT_LASTBLOCK, kv_dtype, p, paged, ragged);
     }
     return KVATTN_OK;
 }
@@ -2268,7 +2340,7 @@ int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scal
     if (!out) return KVATTN_ERR_NULL_POINTER;
     if (!aligned16(out)) return KVATTN_ERR_MISALIGNED;
     Plan plan{};
-    KV_TRY(make_plan(B, NH, maxT, len_hint, S, strategy, plan, pm != nullptr));
+    KV_TRY(make_plan(B, NH, maxT, len_hint, S, strategy, kv_dtype, plan, pm != nullptr, lens_per_seq != 0));
     hipStream_t stream = (hipStream_t)stream_v;
 
     if (plan.strategy == KVATTN_FUSED_SINGLE) {
@@ -2287,7 +2359,14 @@ int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scal
             return KVATTN_ERR_STRATEGY;
         uint8_t* base = nullptr;
         KV_TRY(scratch_base(stream, base));
-        if (!carve_scratch(base, B, NH, plan.slots, w)) return KVATTN_ERR_WORKSPACE;
+        if (!carve_scratch(base, B, NH, plan.slots, w)) {
+            // A tuned AUTO plan may hold more segments than the array has room for where the
+            // general plan's fit: AUTO then takes the general plan.
+            if (strategy != KVATTN_AUTO) return KVATTN_ERR_WORKSPACE;
+            KV_TRY(make_plan(B, NH, maxT, len_hint, S, strategy, kv_dtype, plan, pm != nullptr, lens_per_seq != 0,
+                             false));
+            if (!carve_scratch(base, B, NH, plan.slots, w)) return KVATTN_ERR_WORKSPACE;
+        }
     } else {
         if (!workspace) return KVATTN_ERR_WORKSPACE;
         if (!aligned16(workspace)) return KVATTN_ERR_MISALIGNED;
@@ -2336,15 +2415,19 @@ int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scal
         case KVATTN_SPLIT_DESIGNATED: {
             const int mode = plan.seg_rows == kDevicePlanDes && !pm ? kDesignatedDev : kDesignated;
             // The mergers wait for their producers, so the whole grid must fit on the GPU at once
-            // (AUTO plans at most kDesignatedMaxGrid segments, one per CU; the workgroups an
-            // XCD-local grid adds exit at once and do not count).
+            // (AUTO plans at most kAutoDesignatedMaxGrid segments; the workgroups an XCD-local
+            // grid adds exit at once and do not count).  An AUTO plan whose grid this GPU does
+            // not hold takes the last-block merge instead.
             const long long grid = (long long)B * NH * plan.slots;
             if (grid > kDesignatedMaxGrid) {
                 const void* fn = split_ptr_for(a, kv_dtype, mode, plan.lat);
                 if (!fn) return KVATTN_ERR_DTYPE;
                 long long cap = 0;
                 KV_TRY(resident_capacity(fn, split_threads(plan.lat), cap));
-                if (grid > cap) return KVATTN_ERR_GRID_TOO_LARGE;
+                if (grid > cap) {
+                    if (strategy != KVATTN_AUTO) return KVATTN_ERR_GRID_TOO_LARGE;
+                    return launch_split(a, kv_dtype, kLastBlockMerge, plan.lat, stream);
+                }
             }
             return launch_split(a, kv_dtype, mode, plan.lat, stream);
         }
@@ -2706,7 +2789,7 @@ int kvattn_plan(int B, int NH, int hs, int maxT, int len_hint, int S, int strate
     if (kv_dtype < KVATTN_KV_F32 || kv_dtype > KVATTN_KV_FP8_E4M3) return KVATTN_ERR_DTYPE;
     if (!strategy_out || !segments_out || !seg_rows_out) return KVATTN_ERR_NULL_POINTER;
     Plan p{};
-    KV_TRY(make_plan(B, NH, maxT, len_hint, S, strategy, p));
+    KV_TRY(make_plan(B, NH, maxT, len_hint, S, strategy, kv_dtype, p));
     *strategy_out = p.strategy;
     *segments_out = p.slots;
     *seg_rows_out = p.seg_rows < 0 ? -1 : p.seg_rows;

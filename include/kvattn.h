@@ -68,8 +68,11 @@ typedef enum kvattn_dtype {
 } kvattn_dtype;
 
 typedef enum kvattn_strategy {
-    KVATTN_AUTO = 0,                /* fused_single for short contexts, else split with
-                                       in-kernel merge; chosen from len_hint */
+    KVATTN_AUTO = 0,                /* fused_single for short contexts, else a split plan
+                                       chosen from len_hint, the shape and the cache type:
+                                       the designated merger while its grid is small, one
+                                       segment per (b,h) for many short heads, split +
+                                       merge kernels once the call is bandwidth bound */
     KVATTN_FUSED_SINGLE = 1,        /* one workgroup per (b,h), scores staged in LDS */
     KVATTN_SPLIT_MERGE = 2,         /* flash-decoding: split kernel + merge kernel */
     KVATTN_SINGLE_LAUNCH_COOP = 3,  /* split + grid barrier + merge, cooperative launch */
@@ -80,7 +83,8 @@ typedef enum kvattn_strategy {
                                        the other segments publish tagged partials and finish,
                                        segment 0 polls for them; one ordinary launch,
                                        capturable; at most 64 segments per (b,h).  AUTO's
-                                       choice for latency-bound calls. */
+                                       choice for latency-bound calls (with a length hint:
+                                       grids of up to 768 workgroups and 64 MiB of cache). */
 } kvattn_strategy;
 
 /* Human-readable text of a status code. */
@@ -238,9 +242,13 @@ int kvattn_set_merge_poll_limit(int polls);
  * *strategy_out = the resolved kvattn_strategy (AUTO resolved), *segments_out = segment
  * slots per (b,h) (1 for FUSED_SINGLE), *seg_rows_out = rows per segment (0 when the
  * reference partition ceil(total/S) is used, -1 when the kernels plan the rows from the
- * device length).  No reference counterpart: it exposes the
- * AUTO choice, which the reference makes inline in its caller (inference_gpt2_opt.cu:247,
- * 304,331: fused_single below a length threshold, split + merge above it). */
+ * device length).  The plan is that of a call with one length for the batch
+ * (lens_per_seq == 0).  A call with per-sequence lengths takes the same plan, except where
+ * this one streams a BF16 or INT8 cache through the split + merge kernels: there AUTO keeps
+ * its general plan (the last-block merge, or split + merge over segments of up to 512
+ * rows).  No reference counterpart: it exposes the AUTO choice, which the reference makes
+ * inline in its caller (inference_gpt2_opt.cu:247,304,331: fused_single below a length
+ * threshold, split + merge above it). */
 int kvattn_plan(int B, int NH, int hs, int maxT, int len_hint, int S, int strategy, int kv_dtype,
                 int* strategy_out, int* segments_out, int* seg_rows_out);
 

@@ -28,10 +28,10 @@ def test_auto_gpt2_layer_is_single_launch_split():
     assert kvattn.plan(1, 12, 64, 1024, kv_dtype="bf16", len_hint=1023) == (kvattn.SPLIT_DESIGNATED, 8, 128)
     # 257 positions: three 128-row segments used; the grid covers every length up to maxT.
     assert kvattn.plan(1, 12, 64, 1024, kv_dtype="int8", len_hint=256) == (kvattn.SPLIT_DESIGNATED, 8, 128)
-    # More heads: 256-row segments while heads x segments stays within 256 workgroups; a
-    # larger grid takes the last-block merge.
-    assert kvattn.plan(2, 12, 64, 1024, kv_dtype="bf16", len_hint=1023) == (kvattn.SPLIT_DESIGNATED, 4, 256)
-    assert kvattn.plan(16, 12, 64, 1024, kv_dtype="bf16", len_hint=1023) == (kvattn.SPLIT_LASTBLOCK, 4, 256)
+    # More heads: 128-row segments while heads x segments stays within 768 workgroups, then
+    # 256 rows.
+    assert kvattn.plan(2, 12, 64, 1024, kv_dtype="bf16", len_hint=1023) == (kvattn.SPLIT_DESIGNATED, 8, 128)
+    assert kvattn.plan(16, 12, 64, 1024, kv_dtype="bf16", len_hint=1023) == (kvattn.SPLIT_DESIGNATED, 4, 256)
     # The lastblock strategy keeps its own segmentation (about four segments).
     assert kvattn.plan(1, 12, 64, 1024, kv_dtype="bf16", len_hint=1023, strategy="lastblock") == \
         (kvattn.SPLIT_LASTBLOCK, 4, 256)
@@ -52,7 +52,64 @@ def test_designated_follows_at_most_64_segments():
 
 def test_auto_large_batch_streams_with_split_merge():
     st, slots, rows = kvattn.plan(64, 12, 64, 8192, kv_dtype="bf16", len_hint=8191)
-    assert (st, slots, rows) == (kvattn.SPLIT_MERGE, 16, 512)
+    assert (st, slots, rows) == (kvattn.SPLIT_MERGE, 32, 256)
+    # FP32 and FP8 keep the general streaming plan (512-row segments).
+    assert kvattn.plan(64, 12, 64, 8192, kv_dtype="fp8", len_hint=8191) == (kvattn.SPLIT_MERGE, 16, 512)
+    assert kvattn.plan(64, 12, 64, 8192, kv_dtype="int8", len_hint=8191) == (kvattn.SPLIT_MERGE, 16, 512)
+    assert kvattn.plan(64, 12, 64, 4096, kv_dtype="int8", len_hint=4095) == (kvattn.SPLIT_MERGE, 16, 256)
+
+
+# (B, NH, maxT, hint, dtype) -> AUTO's plan, one shape per branch of the tuned choice.
+TUNED = [
+    # one segment per head: >= 192 heads of at most 512 rows (INT8 excepted)
+    ((16, 12, 512, 511, "fp8"), (kvattn.SPLIT_LASTBLOCK, 1, 512)),
+    ((64, 12, 512, 299, "f32"), (kvattn.SPLIT_LASTBLOCK, 1, 512)),
+    ((15, 12, 512, 511, "bf16"), (kvattn.SPLIT_DESIGNATED, 4, 128)),     # 180 heads: designated
+    ((64, 12, 512, 511, "int8"), (kvattn.SPLIT_DESIGNATED, 1, 512)),     # INT8: designated
+    # designated: rows max(128, maxT / 16) (a power of two), doubled while the grid exceeds 768
+    ((8, 12, 1024, 1023, "bf16"), (kvattn.SPLIT_DESIGNATED, 8, 128)),    # 96 x 8 = 768
+    ((1, 12, 4096, 4095, "int8"), (kvattn.SPLIT_DESIGNATED, 16, 256)),
+    ((1, 12, 8192, 8191, "bf16"), (kvattn.SPLIT_DESIGNATED, 16, 512)),
+    ((32, 12, 1024, 1023, "fp8"), (kvattn.SPLIT_DESIGNATED, 2, 512)),    # doubled twice, 53.6 MB
+    ((8, 12, 2048, 2047, "int8"), (kvattn.SPLIT_DESIGNATED, 8, 256)),    # doubled, 8 segments, 26.8 MB
+    ((1, 2, 8192, 8191, "bf16"), (kvattn.SPLIT_DESIGNATED, 64, 128)),    # 2 heads: up to 64 segments
+    # not designated: doubled to 8 segments above 40 MB, or above 64 MB, or a grid beyond 768
+    ((8, 12, 2048, 2047, "bf16"), (kvattn.SPLIT_MERGE, 8, 256)),
+    ((8, 12, 4096, 4095, "fp8"), (kvattn.SPLIT_LASTBLOCK, 8, 512)),      # FP8: the general plan
+    ((32, 12, 1024, 1023, "bf16"), (kvattn.SPLIT_MERGE, 4, 256)),
+    ((16, 12, 1024, 1023, "f32"), (kvattn.SPLIT_LASTBLOCK, 4, 256)),
+    ((2, 32, 8192, 8191, "int8"), (kvattn.SPLIT_MERGE, 16, 512)),
+]
+
+
+@pytest.mark.parametrize("args,plan", TUNED, ids=[f"B{a[0]}-NH{a[1]}-maxT{a[2]}-{a[4]}" for a, _ in TUNED])
+def test_auto_with_hint_takes_the_measured_plan(args, plan):
+    B, NH, maxT, hint, dt = args
+    assert kvattn.plan(B, NH, 64, maxT, kv_dtype=dt, len_hint=hint) == plan
+
+
+def test_auto_tuned_plans_stay_within_their_bounds():
+    """Every hinted AUTO plan over a grid of shapes: a designated grid of at most 768
+    workgroups and 64 segments per head, at most 16 once there are 12 or more heads; the
+    one-segment plan only for 192+ heads of at most 512 rows; and the GPT-2 layer (B = 1,
+    NH = 12, maxT = 1024) unchanged at every length past fused_single."""
+    for dt in ("f32", "bf16", "int8", "fp8"):
+        for B in (1, 2, 3, 5, 8, 16, 33, 64, 200):
+            for NH in (1, 4, 12, 25):
+                for maxT in (300, 512, 1000, 1024, 2048, 5000, 8192, 20000):
+                    for hint in {maxT // 3, maxT - 1}:
+                        st, slots, rows = kvattn.plan(B, NH, 64, maxT, kv_dtype=dt, len_hint=hint)
+                        heads = B * NH
+                        if st == kvattn.SPLIT_DESIGNATED:
+                            assert heads * slots <= 768 and slots <= 64, (dt, B, NH, maxT, hint)
+                            if heads >= 12:
+                                assert slots <= 16, (dt, B, NH, maxT, hint)
+                        if st == kvattn.SPLIT_LASTBLOCK and slots == 1 and rows == 512:
+                            assert heads >= 192 and maxT <= 512
+                        if st != kvattn.FUSED_SINGLE:
+                            assert slots * rows >= maxT
+    for hint in range(256, 1024, 37):
+        assert kvattn.plan(1, 12, 64, 1024, kv_dtype="bf16", len_hint=hint) == (kvattn.SPLIT_DESIGNATED, 8, 128)
 
 
 def test_auto_without_hint_plans_on_the_device():

@@ -86,3 +86,44 @@ def test_static_rejects_what_it_cannot_serve(dev):
                                            torch.cuda.current_stream().cuda_stream)
     assert st == kvattn.ERR_WORKSPACE
     torch.cuda.synchronize()
+
+
+def test_static_auto_takes_the_general_plan_when_the_tuned_one_does_not_fit(dev):
+    """B=64, NH=12, maxT=4096, BF16, one length with a hint: AUTO's tuned plan streams 256-row
+    segments (16 per head, 12,288 slots, ~11 MB of partials and tags: more than the 8 MiB
+    array holds), so kvattn_decode_static takes the general plan, 512-row segments through
+    the same split + merge kernels (8 per head).  Its output must equal, bit for bit,
+    kvattn_decode's with that plan asked for explicitly (split_merge, S = -512) on a
+    workspace of the caller's; 8 sampled heads are also checked against the oracle."""
+    import torch
+    from oracle import oracle
+    kvattn = _kv()
+    B, NH, maxT, T = 64, 12, 4096, 4096
+    assert kvattn.plan(B, NH, HS, maxT, kv_dtype="bf16", len_hint=T - 1) == (kvattn.SPLIT_MERGE, 16, 256)
+    g = torch.Generator(device=dev)
+    g.manual_seed(77)
+    cache = torch.randn(2 * B * NH * maxT * HS, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    qkv = torch.randn(B * 3 * NH * HS, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    cur = torch.tensor([T - 1], dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    a = torch.full((B * NH * HS,), float("nan"), dtype=torch.bfloat16, device=dev)
+    st = kvattn.lib().kvattn_decode_static(a.data_ptr(), qkv.data_ptr(), cache.data_ptr(), None, B, NH, HS, maxT,
+                                           cur.data_ptr(), 0, T - 1, 0, kvattn.AUTO, kvattn.KV_BF16, stream)
+    assert st == 0, kvattn.strerror(st)
+    b = torch.full_like(a, float("nan"))
+    ws = kvattn.Workspace(B, NH, maxT, -512)
+    kvattn.decode(b, qkv, cache, B, NH, HS, maxT, kv_dtype="bf16", cur_len=cur, len_hint=T - 1, S=-512,
+                  strategy="split_merge", **ws.kwargs())
+    torch.cuda.synchronize()
+    ga, gb = a.float().cpu().numpy(), b.float().cpu().numpy()
+    assert np.array_equal(ga.view(np.uint32), gb.view(np.uint32)), "static AUTO differs from split_merge S=-512"
+    kv5 = cache.view(2, B, NH, maxT, HS)
+    q = qkv.float().view(B, 3, NH, HS)
+    rng = np.random.RandomState(78)
+    for bb, h in zip(rng.randint(0, B, 8), rng.randint(0, NH, 8)):
+        k = kv5[0, bb, h].float().cpu().numpy()
+        v = kv5[1, bb, h].float().cpu().numpy()
+        q1 = np.zeros((1, 3, 1, HS), np.float32)
+        q1[0, 0, 0] = q[bb, 0, h].cpu().numpy()
+        ref = oracle.attention_f32(q1.reshape(-1), np.stack([k, v]).reshape(-1), T, 1, 1, HS, T)
+        assert_close(ga.reshape(B, NH, HS)[bb, h], ref, "bf16", f"static AUTO b={bb} h={h}")
