@@ -24,11 +24,13 @@ Also in the same JSON line:
                 sequences x NH=12, BF16, lengths ~ U[1, 8192] (~0.8 GB of KV per call),
                 which streams from HBM and carries the >=70 % of peak target.  The 8-bit
                 configurations (C3 INT8 with 1 % outliers x8, C4 FP8) time caches filled by
-                the library's own append from seeded bf16 values.
+                the library's own append from seeded bf16 values.  batch_auto: AUTO's plan
+                and time per call for B = 1-32 sequences of 512-4096 positions in each cache
+                type (batch_configs).
 
 Inputs are synthetic (seeded N(0,1)) and resident in HBM before any timed region.
 
-`--only c2|c5|configs|gemv|qkv_append` runs one workload and prints its record alone: one
+`--only c2|c5|configs|gemv|qkv_append|batch` runs one workload and prints its record alone: one
 `rocprofv3 --kernel-trace --stats` process per workload attributes the kernel dispatches.
 These runs make no cooperative launch (a rocprofv3 process that made one ends in a
 segmentation fault at exit): the cooperative rows are timed by the full run only.
@@ -73,7 +75,7 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=6.0, help="CPU baseline budget of the headline call")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-configs", action="store_true", help="skip the other GPT-2-shaped configurations")
-    p.add_argument("--only", choices=["c2", "c5", "configs", "gemv", "qkv_append"], default=None,
+    p.add_argument("--only", choices=["c2", "c5", "configs", "gemv", "qkv_append", "batch"], default=None,
                    help="run one workload and print its record alone (one rocprofv3 process per workload "
                         "attributes kernel dispatches to it)")
     return p.parse_args()
@@ -915,6 +917,64 @@ def pmc_pass(args, torch, kvattn, dev):
     print("pmc pass done")
 
 
+BATCH_SHAPES = (("bf16", 8, 1024), ("bf16", 16, 1024), ("bf16", 32, 1024), ("bf16", 4, 4096), ("bf16", 16, 4096),
+                ("int8", 8, 2048), ("int8", 1, 4096), ("int8", 16, 4096), ("fp8", 16, 512), ("f32", 8, 1024))
+
+
+def batch_configs(torch, kvattn, dev, layers=12, reps=20):
+    """AUTO beyond GPT-2's one-sequence layer: NH = 12, B sequences of one length T = maxT with
+    the length hint, per cache type.  One graph of `layers` calls over distinct caches (as a
+    decode step walks its layers), replayed: µs per call, GB/s against the algorithmic bytes
+    (K and V rows, 8-bit row scales, q and out) and the fraction of peak, with the plan AUTO
+    took.  8-bit caches hold random finite codes and row scales."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(21)
+    res = {}
+    for dtype, B, T in BATCH_SHAPES:
+        NH, maxT = 12, T
+        act = torch.float32 if dtype == "f32" else torch.bfloat16
+        n = 2 * B * NH * maxT * HD
+        caches, scales = [], []
+        for _ in range(layers):
+            if dtype in ("f32", "bf16"):
+                caches.append(torch.randn(n, generator=g, device=dev, dtype=torch.float32).to(act))
+                scales.append(None)
+            else:
+                c = torch.randint(0, 256, (n,), generator=g, device=dev, dtype=torch.int32)
+                caches.append((c & 0x77 if dtype == "fp8" else c).to(torch.uint8))
+                scales.append(torch.rand(2 * B * NH * maxT, generator=g, device=dev) * 0.05 + 1e-3)
+        qkvs = [torch.randn(B * 3 * NH * HD, generator=g, device=dev).to(act) for _ in range(layers)]
+        outs = [torch.empty(B * NH * HD, device=dev, dtype=act) for _ in range(layers)]
+        cur = torch.tensor([T - 1], dtype=torch.int32, device=dev)
+        ws = kvattn.Workspace(B, NH, maxT, 0)
+
+        def step():
+            for l in range(layers):
+                kvattn.decode(outs[l], qkvs[l], caches[l], B, NH, HD, maxT, kv_dtype=dtype, kv_scale=scales[l],
+                              cur_len=cur, len_hint=T - 1, **ws.kwargs())
+        step()
+        s = torch.cuda.Stream()
+        graph = torch.cuda.CUDAGraph()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(graph, stream=s):
+                step()
+        for _ in range(3):
+            graph.replay()
+        with phase(f"batch_{dtype}_B{B}_T{T}"):
+            us = timed(torch, graph.replay, reps) * 1000.0 / layers
+        kv_bytes = {"f32": 4, "bf16": 2, "int8": 1, "fp8": 1}[dtype]
+        nbytes = bytes_per_call([T] * B, NH, kv_bytes, act.itemsize, B) + (2 * B * NH * T * 4 if kv_bytes == 1 else 0)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        plan = kvattn.plan(B, NH, HD, maxT, kv_dtype=dtype, len_hint=T - 1)
+        res[f"{dtype}_B{B}_T{T}"] = {"us_per_call": round(us, 3), "bytes_per_call": nbytes, "GBps": round(gbs, 1),
+                                     "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                                     "strategy": kvattn.STRATEGY_NAMES[plan[0]], "segments_per_head": plan[1],
+                                     "rows_per_segment": plan[2]}
+        del caches, scales, graph
+    return res
+
+
 def cache_sweep(torch, kvattn, dev, reps=40):
     """Infinity Cache regime, from timing: MI355X exposes no MALL counter to rocprofv3 here,
     so the same calls are replayed over N distinct copies of their KV caches and the bytes
@@ -1063,6 +1123,8 @@ def main():
         elif args.only == "gemv":
             part = gemv_configs(torch, kvattn, dev)
             part["tall"] = gemv_tall_configs(torch, kvattn, dev)
+        elif args.only == "batch":
+            part = batch_configs(torch, kvattn, dev)
         else:
             part = qkv_append_configs(torch, kvattn, dev)
         print(json.dumps({"only": args.only, "result": part, "gpu": torch.cuda.get_device_name(dev)}))
@@ -1102,6 +1164,7 @@ def main():
     gemv = None if args.no_configs else gemv_configs(torch, kvattn, dev)
     gemv_tall = None if args.no_configs else gemv_tall_configs(torch, kvattn, dev)
     qkv_append = None if args.no_configs else qkv_append_configs(torch, kvattn, dev)
+    batch = None if args.no_configs else batch_configs(torch, kvattn, dev)
     gemv_cpu = None if (args.no_configs or args.no_cpu) else gemv_cpu_baseline()
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds, c2)
     if cpu is not None:
@@ -1139,7 +1202,7 @@ def main():
                   "gemv_cpu_baseline": gemv_cpu,
                   "rel_err_vs_f64": rel,
                   "gpu_vs_cpu_speedup": (round(cpu["value"] / us_call, 1) if cpu else None),
-                  "c5": c5, "configs": configs, "gpu": torch.cuda.get_device_name(dev),
+                  "c5": c5, "configs": configs, "batch_auto": batch, "gpu": torch.cuda.get_device_name(dev),
                   "host": platform.node()},
     }
     print(json.dumps(line))
