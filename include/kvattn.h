@@ -260,7 +260,10 @@ int kvattn_plan(int B, int NH, int hs, int maxT, int len_hint, int S, int strate
  *              replayed token after token: with S == 0 the kernels then plan the
  *              segmentation from the device length (one segment up to 256 positions,
  *              about four beyond), where the reference captures a small and a large
- *              graph and picks one per token (inference_gpt2_opt.cu:420-449,556).
+ *              graph and picks one per token (inference_gpt2_opt.cu:420-449,556).  AUTO
+ *              with more than 16 heads (B*NH), or a longer maxT, takes fixed rows sized
+ *              for maxT instead while its designated grid stays small (kvattn_plan
+ *              reports them); segments past a call's length exit at once.
  *   S          segments per (b,h) for the split strategies: S > 0 uses the reference
  *              partition chunk = ceil(total/S); S < 0 uses -S rows per segment; S == 0
  *              lets the library pick the rows per segment (from len_hint, or on the

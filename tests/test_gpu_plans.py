@@ -1,5 +1,6 @@
-"""AUTO's plans for batches and long contexts (a length hint, one length for the batch) on an
-MI355X: one shape per branch of the plan choice, checked against the oracle.
+"""AUTO's plans for batches and long contexts on an MI355X: one shape per branch of the plan
+choice, with a length hint (one length for the batch) and without one (the plan a captured
+graph replays at every length), checked against the oracle.
 
 Each case first asserts, through kvattn_plan, that AUTO takes the branch it is there for
 (the one-segment-per-head last-block plan, the designated merger on grids of up to 768
@@ -127,3 +128,51 @@ def test_auto_plan_branches(dev, dtype, B, NH, maxT, T, expect):
     ref2 = outs["reference partition"]
     d = (got - ref2).norm(dim=2) / ref2.norm(dim=2).clamp_min(1e-30)
     assert float(d.max()) <= TOL[dtype], f"AUTO and the reference partition differ ({float(d.max()):.3e})"
+
+
+# Without a length hint (a graph captured once and replayed at every length): beyond the
+# device-planned grid of a few heads, AUTO takes the hinted plan's designated window (or one
+# segment per head) at maxT with fixed rows, and the same launch serves every length.
+# dtype, B, NH, maxT, attended lengths (one per call; per sequence when ragged), plan, ragged
+NO_HINT = [
+    ("int8", 2, 12, 1024, [300, 1024], ("designated", 8, 128), False),
+    ("bf16", 1, 12, 4096, [1000, 4096], ("designated", 16, 256), False),
+    ("fp8", 32, 12, 1024, [300, 1024], ("designated", 2, 512), False),
+    ("bf16", 16, 12, 512, [300, 512], ("lastblock", 1, 512), False),
+    ("int8", 8, 12, 1024, [1024, 77, 512, 1000, 129, 300, 1024, 1], ("designated", 8, 128), True),
+]
+
+
+@pytest.mark.parametrize("dtype,B,NH,maxT,Ts,expect,ragged", NO_HINT,
+                         ids=[f"{c[0]}-B{c[1]}-maxT{c[3]}-{c[5][0]}{'-ragged' if c[6] else ''}" for c in NO_HINT])
+def test_auto_without_hint_plan_branches(dev, dtype, B, NH, maxT, Ts, expect, ragged):
+    import torch
+    kvattn = _kv()
+    plan = kvattn.plan(B, NH, HS, maxT, kv_dtype=dtype)
+    assert (kvattn.STRATEGY_NAMES[plan[0]], plan[1], plan[2]) == expect, plan
+    qkv, cache, scale = _inputs(torch, dev, dtype, B, NH, maxT, seed=B * 100 + maxT)
+    act = torch.float32 if dtype == "f32" else torch.bfloat16
+    ws = kvattn.Workspace(B, NH, maxT, 0)
+    q = qkv.float().view(B, 3, NH, HS)
+    calls = [Ts] if ragged else [[T] * B for T in Ts]
+    for lens in calls:
+        print(f"{dtype} B={B} maxT={maxT} lengths {lens} plan {expect}", flush=True)
+        cur = torch.tensor([t - 1 for t in lens], dtype=torch.int32, device=dev)
+        if not ragged:
+            cur = cur[:1].contiguous()
+        out = torch.full((B * NH * HS,), float("nan"), dtype=act, device=dev)
+        kvattn.decode(out, qkv, cache, B, NH, HS, maxT, kv_dtype=dtype, kv_scale=scale, cur_len=cur,
+                      lens_per_seq=ragged, **ws.kwargs())
+        torch.cuda.synchronize()
+        assert ws.status() == 0
+        got = out.float().view(B, NH, HS)
+        rng = np.random.RandomState(sum(lens))
+        picks = {(int(b), int(h)) for b, h in zip(rng.randint(0, B, 12), rng.randint(0, NH, 12))}
+        picks |= {(0, 0), (B - 1, NH - 1)}
+        for b, h in sorted(picks):
+            T = lens[b]
+            k, v = _rows_f32(cache, scale, dtype, B, NH, maxT, b, h, T)
+            q1 = np.zeros((1, 3, 1, HS), np.float32)
+            q1[0, 0, 0] = q[b, 0, h].cpu().numpy()
+            ref = oracle.attention_f32(q1.reshape(-1), np.stack([k, v]).reshape(-1), T, 1, 1, HS, T)
+            assert_close(got[b, h].cpu().numpy(), ref, dtype, f"{dtype} lengths {lens} b={b} h={h}")

@@ -128,6 +128,21 @@ def test_auto_without_hint_plans_on_the_device():
         (kvattn.SPLIT_LASTBLOCK, 8, 128)
 
 
+def test_auto_without_hint_beyond_a_few_heads_takes_fixed_rows():
+    # More than 16 heads, or a device-planned designated grid beyond 256 workgroups: the
+    # hinted plan's designated window (or one segment per head) at maxT, fixed rows.
+    assert kvattn.plan(2, 12, 64, 1024, kv_dtype="int8") == (kvattn.SPLIT_DESIGNATED, 8, 128)
+    assert kvattn.plan(1, 12, 64, 4096, kv_dtype="bf16") == (kvattn.SPLIT_DESIGNATED, 16, 256)
+    assert kvattn.plan(32, 12, 64, 1024, kv_dtype="fp8") == (kvattn.SPLIT_DESIGNATED, 2, 512)
+    assert kvattn.plan(16, 12, 64, 512, kv_dtype="bf16") == (kvattn.SPLIT_LASTBLOCK, 1, 512)
+    # ... but never its split + merge streaming plans: those stay planned on the device.
+    assert kvattn.plan(32, 12, 64, 1024, kv_dtype="bf16") == (kvattn.SPLIT_LASTBLOCK, 4, -1)
+    assert kvattn.plan(16, 12, 64, 4096, kv_dtype="int8") == (kvattn.SPLIT_MERGE, 8, -1)
+    # A few heads whose device-planned designated grid fits keep it (GPT-2's layer).
+    assert kvattn.plan(1, 12, 64, 2048, kv_dtype="bf16") == (kvattn.SPLIT_DESIGNATED, 16, -1)
+    assert kvattn.plan(1, 16, 64, 1024, kv_dtype="fp8") == (kvattn.SPLIT_DESIGNATED, 8, -1)
+
+
 def test_auto_skips_fused_single_when_scores_exceed_lds():
     # 64 KB of LDS holds 16384 scores; maxT beyond that rules fused_single out.
     st, _, _ = kvattn.plan(1, 12, 64, 20000, kv_dtype="bf16", len_hint=10)
