@@ -2283,19 +2283,20 @@ int make_plan(int B, int NH, int maxT, int len_hint, int S, int strategy, int kv
         // kernel once the call streams enough rows to be bandwidth bound.
         const bool fits = (size_t)maxT * sizeof(float) <= kFusedMaxLds;
         const bool fused = !paged && fits && total_hint <= kFusedMaxRows;
-        if (tuned && !fused && !paged && S == 0) {
+        const bool hinted = len_hint >= 0;
+        if (tuned && !fused && S == 0 && !(paged && hinted && total_hint <= kFusedMaxRows)) {
             int slots_bound = 0, rows_bound = 0;   // the workspace bound of S == 0, checked as below
             KV_TRY(segment_slots(maxT, S, slots_bound, rows_bound));
             const long long heads = (long long)B * NH;
-            if (len_hint >= 0) {
-                if (tuned_auto(B, NH, maxT, total_hint, kv_dtype, ragged, p))
-                    return heads * p.slots >= (1ll << 31) ? KVATTN_ERR_SHAPE : KVATTN_OK;
-            } else if (heads > 16 || heads * designated_slots(maxT, B * NH) > kDesignatedMaxGrid) {
-                // No hint, beyond the device-planned designated grid of a few heads: the
-                // designated window (or one segment per head) of the hinted plan at maxT, with
-                // fixed rows, whose grid serves every length up to maxT.
+            // Without a hint: beyond the device-planned designated grid of a few heads, the
+            // designated window (or one segment per head) of the hinted plan at maxT, with fixed
+            // rows, whose grid serves every length up to maxT.  Without a hint and on a paged
+            // cache, the split + merge plans stay planned on the device (a paged cache's short
+            // hinted lengths too).
+            if (hinted || heads > 16 || heads * designated_slots(maxT, B * NH) > kDesignatedMaxGrid) {
                 Plan q{};
-                if (tuned_auto(B, NH, maxT, maxT, kv_dtype, ragged, q) && q.strategy != KVATTN_SPLIT_MERGE) {
+                if (tuned_auto(B, NH, maxT, hinted ? total_hint : maxT, kv_dtype, ragged, q) &&
+                    (q.strategy != KVATTN_SPLIT_MERGE || (hinted && !paged))) {
                     p = q;
                     return heads * p.slots >= (1ll << 31) ? KVATTN_ERR_SHAPE : KVATTN_OK;
                 }

@@ -342,10 +342,13 @@ int kvattn_paged_cache_write(void* pages, float* page_scales, const int* block_t
                              const int* d_cur_len, int lens_per_seq, int kv_dtype, void* stream);
 
 /* kvattn_decode (append == 0) or kvattn_append_decode (append != 0) on a paged cache.
- * Strategies: AUTO, SPLIT_MERGE, SPLIT_LASTBLOCK, SINGLE_LAUNCH_GRAPH (no FUSED_SINGLE or
- * cooperative launch: short contexts take a single segment of the split kernel).  S == 0
- * plans the segments on the device; S < 0 gives -S rows per segment, a multiple of 64 and
- * at most 4096.  Workspace: kvattn_workspace_bytes(B, NH, hs, max_pages*page_rows, S). */
+ * Strategies: AUTO, SPLIT_MERGE, SPLIT_LASTBLOCK, SPLIT_DESIGNATED, SINGLE_LAUNCH_GRAPH (no
+ * FUSED_SINGLE or cooperative launch: short contexts take a single segment of the split
+ * kernel).  S == 0 plans the segments on the device, except where AUTO takes the designated
+ * merger or one segment per (b,h) with fixed rows (128, 256 or 512: the choice kvattn_decode's
+ * AUTO makes for a contiguous cache, hinted lengths of up to 256 positions excepted); S < 0
+ * gives -S rows per segment, a multiple of 64 and at most 4096.  Workspace:
+ * kvattn_workspace_bytes(B, NH, hs, max_pages*page_rows, S). */
 int kvattn_paged_decode(void* out, const void* qkv, void* pages, float* page_scales,
                         const int* block_table, int max_pages, int page_rows, int num_pages,
                         int B, int NH, int hs,

@@ -176,3 +176,70 @@ def test_auto_without_hint_plan_branches(dev, dtype, B, NH, maxT, Ts, expect, ra
             q1[0, 0, 0] = q[b, 0, h].cpu().numpy()
             ref = oracle.attention_f32(q1.reshape(-1), np.stack([k, v]).reshape(-1), T, 1, 1, HS, T)
             assert_close(got[b, h].cpu().numpy(), ref, dtype, f"{dtype} lengths {lens} b={b} h={h}")
+
+
+# A paged cache (page pool [num_pages][2][NH][P][hs], shuffled block table) takes the same
+# designated window and one-segment plan, with and without a hint; its split + merge plans
+# stay planned on the device.  dtype, B, NH, P, maxT, lengths per sequence
+PAGED = [
+    ("bf16", 16, 12, 256, 512, [512] * 16),                 # 192 heads of 512 rows: one segment per head
+    ("int8", 1, 12, 256, 4096, [4096]),                     # designated 16 x 256, 8-bit streaming tiles
+    ("fp8", 8, 12, 64, 1024, [1024, 1, 300, 64, 65, 1000, 777, 129]),   # designated 8 x 128, ragged
+]
+
+
+@pytest.mark.parametrize("dtype,B,NH,P,maxT,lens", PAGED,
+                         ids=[f"{c[0]}-B{c[1]}-P{c[3]}-maxT{c[4]}" for c in PAGED])
+def test_auto_paged_plan_branches(dev, dtype, B, NH, P, maxT, lens):
+    import torch
+    kvattn = _kv()
+    rs = np.random.RandomState(B * 7 + maxT)
+    need = [(t + P - 1) // P for t in lens]
+    npg = sum(need) + 2
+    perm = rs.permutation(npg)
+    table = np.full((B, maxT // P), -1, np.int32)
+    k = 0
+    for b in range(B):
+        table[b, :need[b]] = perm[k:k + need[b]]
+        k += need[b]
+    qkv, pool, scale = _inputs(torch, dev, dtype, npg, NH, P, seed=B + maxT + P)   # [npg][2][NH][P][hs]
+    qkv = qkv[: B * 3 * NH * HS].contiguous()    # npg >= B, so the generated q/k/v cover B sequences
+    d_table = torch.from_numpy(table).to(dev)
+    cache = kvattn.PagedCache(pool, d_table, maxT // P, P, npg, page_scales=scale)
+    ragged = len(set(lens)) > 1
+    cur = torch.tensor([t - 1 for t in lens], dtype=torch.int32, device=dev)
+    if not ragged:
+        cur = cur[:1].contiguous()
+    act = torch.float32 if dtype == "f32" else torch.bfloat16
+    q = qkv.float().view(B, 3, NH, HS)
+    pool5 = pool.view(npg, 2, NH, P, HS)
+    sc4 = scale.view(npg, 2, NH, P) if scale is not None else None
+    for hint in (max(lens) - 1, -1):
+        print(f"paged {dtype} B={B} P={P} maxT={maxT} hint={hint}", flush=True)
+        ws = kvattn.Workspace(B, NH, maxT, 0)
+        out = torch.full((B * NH * HS,), float("nan"), dtype=act, device=dev)
+        kvattn.paged_decode(out, qkv, cache, B, NH, HS, kv_dtype=dtype, cur_len=cur, lens_per_seq=ragged,
+                            len_hint=hint, **ws.kwargs())
+        torch.cuda.synchronize()
+        assert ws.status() == 0
+        got = out.float().view(B, NH, HS)
+        rng = np.random.RandomState(hint + 5)
+        picks = {(int(b), int(h)) for b, h in zip(rng.randint(0, B, 10), rng.randint(0, NH, 10))}
+        picks |= {(0, 0), (B - 1, NH - 1)}
+        for b, h in sorted(picks):
+            T = lens[b]
+            pages = [int(table[b, i]) for i in range((T + P - 1) // P)]
+            if dtype in ("f32", "bf16"):
+                k_rows = torch.cat([pool5[p, 0, h] for p in pages])[:T].float().cpu().numpy()
+                v_rows = torch.cat([pool5[p, 1, h] for p in pages])[:T].float().cpu().numpy()
+            else:
+                codes = np.stack([torch.cat([pool5[p, kv, h] for p in pages])[:T].cpu().numpy() for kv in (0, 1)])
+                scs = np.stack([torch.cat([sc4[p, kv, h] for p in pages])[:T].cpu().numpy() for kv in (0, 1)])
+                fmt = oracle.W8_INT8 if dtype == "int8" else oracle.W8_FP8_E4M3
+                deq = oracle.dequant_w8(codes.reshape(-1), scs.reshape(-1).astype(np.float32), 1, 1, HS, T,
+                                        fmt).reshape(2, T, HS)
+                k_rows, v_rows = deq[0], deq[1]
+            q1 = np.zeros((1, 3, 1, HS), np.float32)
+            q1[0, 0, 0] = q[b, 0, h].cpu().numpy()
+            ref = oracle.attention_f32(q1.reshape(-1), np.stack([k_rows, v_rows]).reshape(-1), T, 1, 1, HS, T)
+            assert_close(got[b, h].cpu().numpy(), ref, dtype, f"paged {dtype} hint={hint} b={b} h={h} T={T}")
