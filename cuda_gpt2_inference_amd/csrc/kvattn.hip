@@ -2298,11 +2298,12 @@ int make_plan(int B, int NH, int maxT, int len_hint, int S, int strategy, int kv
             // designated window (or one segment per head) of the hinted plan at maxT, with fixed
             // rows, whose grid serves every length up to maxT.  Without a hint and on a paged
             // cache, the split + merge plans stay planned on the device (a paged cache's short
-            // hinted lengths too).
+            // hinted lengths too, and segments longer than a paged wave walks).
             if (hinted || heads > 16 || heads * designated_slots(maxT, B * NH) > kDesignatedMaxGrid) {
                 Plan q{};
                 if (tuned_auto(B, NH, maxT, hinted ? total_hint : maxT, kv_dtype, ragged, q) &&
-                    (q.strategy != KVATTN_SPLIT_MERGE || (hinted && !paged))) {
+                    (q.strategy != KVATTN_SPLIT_MERGE || (hinted && !paged)) &&
+                    !(paged && q.seg_rows > kMaxPagedSegRows)) {
                     p = q;
                     return heads * p.slots >= (1ll << 31) ? KVATTN_ERR_SHAPE : KVATTN_OK;
                 }

@@ -243,3 +243,40 @@ def test_auto_paged_plan_branches(dev, dtype, B, NH, P, maxT, lens):
             q1[0, 0, 0] = q[b, 0, h].cpu().numpy()
             ref = oracle.attention_f32(q1.reshape(-1), np.stack([k_rows, v_rows]).reshape(-1), T, 1, 1, HS, T)
             assert_close(got[b, h].cpu().numpy(), ref, dtype, f"paged {dtype} hint={hint} b={b} h={h} T={T}")
+
+
+def test_auto_paged_long_max_context_keeps_segments_a_wave_walks(dev):
+    """A paged cache of maxT = 2^20 positions over 2 heads: the hinted rule would plan
+    16,384-row segments, longer than a paged wave walks (it follows at most 64 tiles, one page
+    id per lane), so AUTO keeps the general plan.  20,000 attended positions, both heads
+    against the oracle, with and without the hint."""
+    import torch
+    kvattn = _kv()
+    B, NH, P, maxT, T = 1, 2, 256, 1 << 20, 20000
+    need = (T + P - 1) // P
+    npg = need + 3
+    rs = np.random.RandomState(11)
+    table = np.full((B, maxT // P), -1, np.int32)
+    table[0, :need] = rs.permutation(npg)[:need]
+    g = torch.Generator(device=dev)
+    g.manual_seed(12)
+    pool = torch.randn(npg * 2 * NH * P * HS, generator=g, device=dev).to(torch.bfloat16)
+    qkv = torch.randn(B * 3 * NH * HS, generator=g, device=dev).to(torch.bfloat16)
+    cache = kvattn.PagedCache(pool, torch.from_numpy(table).to(dev), maxT // P, P, npg)
+    cur = torch.tensor([T - 1], dtype=torch.int32, device=dev)
+    pool5 = pool.view(npg, 2, NH, P, HS)
+    q = qkv.float().view(B, 3, NH, HS)
+    for hint in (T - 1, -1):
+        ws = kvattn.Workspace(B, NH, maxT, 0)
+        out = torch.full((B * NH * HS,), float("nan"), dtype=torch.bfloat16, device=dev)
+        kvattn.paged_decode(out, qkv, cache, B, NH, HS, kv_dtype="bf16", cur_len=cur, len_hint=hint, **ws.kwargs())
+        torch.cuda.synchronize()
+        got = out.float().view(B, NH, HS)
+        for h in range(NH):
+            pages = [int(table[0, i]) for i in range(need)]
+            k_rows = torch.cat([pool5[p, 0, h] for p in pages])[:T].float().cpu().numpy()
+            v_rows = torch.cat([pool5[p, 1, h] for p in pages])[:T].float().cpu().numpy()
+            q1 = np.zeros((1, 3, 1, HS), np.float32)
+            q1[0, 0, 0] = q[0, 0, h].cpu().numpy()
+            ref = oracle.attention_f32(q1.reshape(-1), np.stack([k_rows, v_rows]).reshape(-1), T, 1, 1, HS, T)
+            assert_close(got[0, h].cpu().numpy(), ref, "bf16", f"paged maxT=2^20 hint={hint} h={h}")
