@@ -2204,9 +2204,11 @@ struct Plan {
 // A call is latency bound while it streams fewer rows than kStreamRows.
 bool latency_bound(int B, int NH, int total_rows) { return (long long)B * NH * total_rows < kStreamRows; }
 
-// AUTO with a length hint, one cache per call (contiguous), beyond fused_single: the plan
-// measured fastest across B = 1..64, contexts 512..8192 and the four cache types (12-layer
-// graphs on MI355X, 13 plans per shape).
+// AUTO's tuned plan for an attended length of total_hint (the host's hint, or maxT for a call
+// that must serve every length), beyond fused_single: the plan measured fastest across
+// B = 1..64, contexts 512..8192 and the four cache types (12-layer graphs on MI355X, 13 plans
+// per shape).  make_plan decides where it applies (paged caches and calls without a hint take
+// only its first two cases).
 // - One segment per (b,h) (last-block instance, which then stores without a merge) when the
 //   heads alone give 192 or more workgroups and no head is longer than 512 rows; FP8 takes the
 //   streaming shape's 64-row tiles there.  (INT8 goes on to the designated merger, which
