@@ -2210,9 +2210,8 @@ bool latency_bound(int B, int NH, int total_rows) { return (long long)B * NH * t
 // per shape).  make_plan decides where it applies (paged caches and calls without a hint take
 // only its first two cases).
 // - One segment per (b,h) (last-block instance, which then stores without a merge) when the
-//   heads alone give 192 or more workgroups and no head is longer than 512 rows; FP8 takes the
-//   streaming shape's 64-row tiles there.  (INT8 goes on to the designated merger, which
-//   measured faster at these shapes.)
+//   heads alone give 192 or more workgroups and no head is longer than 512 rows; 8-bit caches
+//   take the streaming shape's 64-row tiles there.
 // - The designated merger while its grid stays within kAutoDesignatedMaxGrid workgroups and
 //   the call streams at most kAutoDesignatedMaxBytes: segments of max(128, maxT / 16) rows
 //   (a power of two, so at most 16 per head; up to 64 per head when fewer than 12 heads
@@ -2236,11 +2235,11 @@ bool tuned_auto(int B, int NH, int maxT, int total_hint, int kv_dtype, bool ragg
     const bool k8 = is_8bit(kv_dtype);
     const long long row_bytes = kv_dtype == KVATTN_KV_F32 ? 512 : (kv_dtype == KVATTN_KV_BF16 ? 256 : 136);
     const long long bytes = heads * total_hint * row_bytes;
-    if (maxT <= 512 && heads >= 192 && kv_dtype != KVATTN_KV_INT8) {
+    if (maxT <= 512 && heads >= 192) {
         p.strategy = KVATTN_SPLIT_LASTBLOCK;
         p.seg_rows = 512;
         p.slots = 1;
-        p.lat = kv_dtype != KVATTN_KV_FP8_E4M3;
+        p.lat = !k8;
         return true;
     }
     // At most 16 segments per head once the heads give 192 workgroups with them; fewer heads

@@ -36,6 +36,7 @@ CASES = [
     ("int8", 2, 32, 8192, 8192, ("split_merge", 16, 512)),
     # 192 heads of at most 512 rows: one segment per head, no merge
     ("fp8", 16, 12, 512, 512, ("lastblock", 1, 512)),
+    ("int8", 32, 12, 512, 480, ("lastblock", 1, 512)),
     ("bf16", 16, 12, 512, 400, ("lastblock", 1, 512)),
     # designated merger on 768 workgroups
     ("bf16", 8, 12, 1024, 1024, ("designated", 8, 128)),

@@ -61,11 +61,11 @@ def test_auto_large_batch_streams_with_split_merge():
 
 # (B, NH, maxT, hint, dtype) -> AUTO's plan, one shape per branch of the tuned choice.
 TUNED = [
-    # one segment per head: >= 192 heads of at most 512 rows (INT8 excepted)
+    # one segment per head: >= 192 heads of at most 512 rows
     ((16, 12, 512, 511, "fp8"), (kvattn.SPLIT_LASTBLOCK, 1, 512)),
     ((64, 12, 512, 299, "f32"), (kvattn.SPLIT_LASTBLOCK, 1, 512)),
     ((15, 12, 512, 511, "bf16"), (kvattn.SPLIT_DESIGNATED, 4, 128)),     # 180 heads: designated
-    ((64, 12, 512, 511, "int8"), (kvattn.SPLIT_DESIGNATED, 1, 512)),     # INT8: designated
+    ((64, 12, 512, 511, "int8"), (kvattn.SPLIT_LASTBLOCK, 1, 512)),
     # designated: rows max(128, maxT / 16) (a power of two), doubled while the grid exceeds 768
     ((8, 12, 1024, 1023, "bf16"), (kvattn.SPLIT_DESIGNATED, 8, 128)),    # 96 x 8 = 768
     ((1, 12, 4096, 4095, "int8"), (kvattn.SPLIT_DESIGNATED, 16, 256)),
