@@ -110,14 +110,26 @@ template <int DT> constexpr int kUnroll = Row<DT>::k8bit ? KVATTN_UNROLL_BYTE : 
 #endif
 template <int DT> constexpr int kUnrollLat = KVATTN_LAT_ROWS / kRowsPerLoad<DT> > 0 ? KVATTN_LAT_ROWS / kRowsPerLoad<DT> : 1;
 constexpr int kWavesLat = KVATTN_LAT_WAVES;
-// fused_single: a head of up to kFusedMaxRows positions is one tile per wave.  FP32 rows are
-// the widest (four lanes' arithmetic per row of bf16), so FP32 takes 8 waves of 32-row tiles
-// and the others 4 waves of KVATTN_LAT_ROWS-row tiles.  Measured (12-layer graphs, A/B both
-// orders): FP32 at 256 positions −0.15 µs with 8 × 32; BF16 within ±0.04; INT8 +0.23.
+// fused_single: a head of up to kFusedMaxRows positions is one tile per wave.  A wave's
+// arithmetic over its tile is the call's critical path while the heads leave CUs idle, and a
+// 4-wave workgroup puts one wave on each SIMD of its CU.  So:
+// - Hinted lengths up to 128 take 4 waves of 32-row tiles (every wave holds rows).  Measured
+//   (12 calls per graph, B·NH from 12 to 768): 10-17 % faster than 4 waves of 64-row tiles at
+//   12-96 heads, 10-33 % at 384-768 heads.
+// - Otherwise FP32 rows, the widest (four lanes' arithmetic per row of bf16), take 8 waves of
+//   32-row tiles up to 256 heads (12-layer graphs, A/B both orders: -0.15 us at 256 positions
+//   against 4 × 64; INT8 +0.23 and BF16 within ±0.04 with 8 × 32), and 4 waves of 64-row tiles
+//   beyond: once the heads outnumber the CUs, the 8-wave workgroups lose 9-21 % (B·NH from 288
+//   to 768, 160-256 positions).  The other caches take 4 waves of KVATTN_LAT_ROWS-row tiles.
 template <int DT> constexpr int kFusedWaves = DT == KVATTN_KV_F32 ? 8 : KVATTN_LAT_WAVES;
 template <int DT> constexpr int kFusedRows = DT == KVATTN_KV_F32 ? 32 : KVATTN_LAT_ROWS;
-template <int DT> constexpr int kUnrollFused =
-    kFusedRows<DT> / kRowsPerLoad<DT> > 0 ? kFusedRows<DT> / kRowsPerLoad<DT> : 1;
+constexpr int kFusedShortWaves = 4;
+constexpr int kFusedShortRows = 32;
+constexpr int kFusedF32WideRows = 64;
+constexpr long long kFusedF32WideHeads = 256;   // B * NH beyond which FP32 takes 4 waves of 64-row tiles
+template <int DT> constexpr int unroll_for(int rows) {
+    return rows / kRowsPerLoad<DT> > 0 ? rows / kRowsPerLoad<DT> : 1;
+}
 // The split kernels' latency shape takes KVATTN_SPLIT_LAT_ROWS rows per wave per tile: a
 // 128-row designated segment is then one full tile per wave of a 4-wave workgroup.  Each
 // tile's arithmetic runs over all its row slots, valid or masked, and at GPT-2's sizes it is
@@ -1866,17 +1878,31 @@ int launch_fused_single(void* out, const void* qkv, const void* kv, const float*
     const size_t lds = (size_t)maxT * sizeof(float);
     if (lds > kFusedMaxLds) return KVATTN_ERR_LDS;
     const float qs = qscale_for(kHeadDim);
+    const bool short_tiles = spec_rows > 0 && spec_rows <= kFusedShortWaves * kFusedShortRows;
+    const bool wide_f32 = kv_dtype == KVATTN_KV_F32 && (long long)B * NH > kFusedF32WideHeads;
     return dispatch_dtype(kv_dtype, [&](auto dtc) -> int {
         constexpr int DT = decltype(dtc)::value;
-        constexpr int kThreads = kFusedWaves<DT> * kWave;
-        if (kv_out)
-            hipLaunchKernelGGL((fused_single_kernel<DT, kThreads, kUnrollFused<DT>, true>), dim3(B * NH),
-                               dim3(kThreads), lds, stream, qkv, (const uint8_t*)kv, cur_len, lens_per_seq, B, NH,
-                               maxT, spec_rows, qs, kv_scale, out, (uint8_t*)kv_out, kv_scale_out);
+        auto launch = [&](auto threads_c, auto unroll_c) {
+            constexpr int kThreads = decltype(threads_c)::value;
+            constexpr int kU = decltype(unroll_c)::value;
+            if (kv_out)
+                hipLaunchKernelGGL((fused_single_kernel<DT, kThreads, kU, true>), dim3(B * NH), dim3(kThreads), lds,
+                                   stream, qkv, (const uint8_t*)kv, cur_len, lens_per_seq, B, NH, maxT, spec_rows, qs,
+                                   kv_scale, out, (uint8_t*)kv_out, kv_scale_out);
+            else
+                hipLaunchKernelGGL((fused_single_kernel<DT, kThreads, kU, false>), dim3(B * NH), dim3(kThreads), lds,
+                                   stream, qkv, (const uint8_t*)kv, cur_len, lens_per_seq, B, NH, maxT, spec_rows, qs,
+                                   kv_scale, out, (uint8_t*)nullptr, (float*)nullptr);
+        };
+        if (short_tiles)
+            launch(std::integral_constant<int, kFusedShortWaves * kWave>{},
+                   std::integral_constant<int, unroll_for<DT>(kFusedShortRows)>{});
+        else if (DT == KVATTN_KV_F32 && wide_f32)
+            launch(std::integral_constant<int, kWavesLat * kWave>{},
+                   std::integral_constant<int, unroll_for<DT>(kFusedF32WideRows)>{});
         else
-            hipLaunchKernelGGL((fused_single_kernel<DT, kThreads, kUnrollFused<DT>, false>), dim3(B * NH),
-                               dim3(kThreads), lds, stream, qkv, (const uint8_t*)kv, cur_len, lens_per_seq, B, NH,
-                               maxT, spec_rows, qs, kv_scale, out, (uint8_t*)nullptr, (float*)nullptr);
+            launch(std::integral_constant<int, kFusedWaves<DT> * kWave>{},
+                   std::integral_constant<int, unroll_for<DT>(kFusedRows<DT>)>{});
         KV_HIP(hipGetLastError());
         return KVATTN_OK;
     });

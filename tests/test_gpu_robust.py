@@ -88,6 +88,36 @@ def test_fused_single_stale_hint_ignores_rows_past_length(dev, dtype):
 
 
 @pytest.mark.parametrize("dtype", ALL_DT)
+def test_fused_single_short_tiles(dev, dtype):
+    """Hinted lengths up to 128 take fused_single's 4 waves of 32-row tiles: exact hints at
+    and around the tile edges, a stale hint longer than the device length (rows past it are
+    poisoned), and hints shorter than it, whose device length leaves the one-tile-per-wave
+    shape for the scores staged in LDS (up to 700 positions)."""
+    for maxT, hint_total, total in ((256, 1, 1), (256, 32, 32), (256, 33, 33), (1024, 100, 100), (256, 128, 128),
+                                    (256, 128, 60), (1024, 100, 230), (1024, 64, 700)):
+        case = _uniform(dtype, 12, maxT, total, seed=400 + total + maxT)
+        for strategy in ("fused_single", "auto"):
+            got, _, _ = _decode(case, dev, strategy, len_hint=hint_total - 1)
+            assert_close(got, case.reference(), dtype, f"{strategy} hint {hint_total} T={total} maxT={maxT}")
+    case = poison_past_length(make_case(dtype, 8, 12, 512, [96] * 8, seed=470))
+    got, _, _ = _decode(case, dev, "auto", len_hint=96)
+    assert_close(got, case.reference(), dtype, "auto B=8 hint 97 T=97")
+
+
+@pytest.mark.parametrize("B,NH", [(24, 12), (21, 12), (16, 17)])
+def test_fused_single_fp32_across_the_head_count_switch(dev, B, NH):
+    """FP32 fused_single takes 4 waves of 64-row tiles beyond 256 heads (B * NH = 288 and
+    272 here) and 8 waves of 32-row tiles up to it (252): exact hints from 129 to 256
+    positions, a stale hint longer than the device length, and one shorter than it whose
+    device length needs the scores staged in LDS."""
+    for maxT, hint_total, total in ((256, 129, 129), (256, 200, 200), (256, 256, 256), (256, 256, 150),
+                                    (1024, 150, 600)):
+        case = poison_past_length(make_case("f32", B, NH, maxT, [total - 1] * B, seed=480 + total))
+        got, _, _ = _decode(case, dev, "fused_single", len_hint=hint_total - 1)
+        assert_close(got, case.reference(), "f32", f"B={B} NH={NH} hint {hint_total} T={total} maxT={maxT}")
+
+
+@pytest.mark.parametrize("dtype", ALL_DT)
 def test_device_planned_designated_ignores_rows_past_length(dev, dtype):
     """AUTO without a hint plans on the device; the designated instance requests its
     nominal first tile (segment 0: up to 256 rows) before the length: T below and above 256."""
@@ -115,7 +145,8 @@ def test_append_decode_ignores_rows_past_length(dev, dtype):
     """Append and attend in one launch over a poisoned cache: the fresh row replaces the
     garbage at position cur_len, every row after it stays out of the result."""
     for strategy, len_hint, total, maxT in (("auto", -1, 500, 1024), ("auto", 1023, 500, 1024),
-                                            ("fused_single", 255, 150, 256)):
+                                            ("fused_single", 255, 150, 256), ("fused_single", 99, 100, 256),
+                                            ("fused_single", 63, 150, 256)):
         case = _uniform(dtype, 12, maxT, total, seed=360 + total)
         got, cache, scale = _decode(case, dev, strategy, len_hint=len_hint, append=True)
         # The reference: the oracle's append into the host copy, then attention over it.
