@@ -944,7 +944,7 @@ __device__ __forceinline__ bool locate(const SplitArgs& a, int BNH, int x, Item&
         if (!dense_slot(x, a.S, BNH, a.NH, it.b, it.h, it.s)) return false;
         it.total = seq_total_uniform(a.cur_len, a.lens_per_seq, it.b, a.maxT);
         it.rows = 0;
-        it.n_seg = a.seg_rows != 0 ? seg_count(a.seg_rows, it.total, a.B * a.NH, it.rows) : a.S;
+        it.n_seg = a.seg_rows != 0 ? seg_count(a.seg_rows, it.total, BNH, it.rows) : a.S;
         return it.s < it.n_seg;
     }
     const int lane = threadIdx.x & (kWave - 1);
@@ -1274,7 +1274,7 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                                                                    a.qscale, fr, a.kv_out, a.kv_scale_out, cur, m, l,
                                                                    acc, pid_in, have_pid);
                 } else {
-                    sl = make_slot<DT>(a.kv, a.kv_scale, a.B, a.NH, a.maxT, bh, slice);
+                    sl = make_slot<DT>(a.kv, a.kv_scale, 1, BNH, a.maxT, bh, slice);   // B * NH: preloaded
                     // Device-planned segment 0 beyond its first kW tiles (128 < length <= 256): this
                     // wave's second tile, kW tiles further on, requested before the first is consumed.
                     constexpr int kTileRows = kRowsPerLoad<DT> * kU;
@@ -1297,7 +1297,7 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                         if constexpr (kFresh) fr = load_fresh<DT>(a.qkv, it.b, it.h, a.NH, slice);
                     }
                     if constexpr (kFresh)
-                        fd = fresh_dst(a.kv_out, a.kv_scale_out, a.B, a.NH, a.maxT, bh, slice, cur);
+                        fd = fresh_dst(a.kv_out, a.kv_scale_out, 1, BNH, a.maxT, bh, slice, cur);
                     online_rows_from<DT, kU, kFresh, kHwDot>(t0, q0, sl, w0, w1, slot_row, a.qscale, fr, fd, cur, m, l,
                                                              acc);
                     if (kDev && x0 < x1)
@@ -1646,9 +1646,10 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
         if constexpr (kMode != kCoopMerge) {
             if (!active) return;
         }
-        // The merger's XCD word (segment 0 of a real head, whose slot is vbx).
+        // The merger's XCD word (segment 0 of a real head, whose slot is vbx), which a head of
+        // one segment, with no producer to read it, does without.
         if constexpr (kDesMode) {
-            if (xl && it.s == 0 && threadIdx.x == 0)
+            if (xl && it.s == 0 && it.n_seg > 1 && threadIdx.x == 0)
                 __hip_atomic_store(a.tag_ml + (size_t)kMlStride * vbx, ((unsigned long long)des_tag << 32) | my_xcc,
                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
