@@ -551,6 +551,28 @@ def test_designated_merger_workspace_reuse(dev):
         assert_close(out.float().cpu().numpy(), case.reference(), "bf16", f"call {i} {strategy} S={S}")
 
 
+@pytest.mark.parametrize("dtype", ALL_DT)
+@pytest.mark.parametrize("NH", [16, 20, 25])
+def test_gpt2_family_head_counts(dev, dtype, NH):
+    """GPT-2 medium, large and XL head counts (hd = 64), one length for a batch of 2, maxT = 1024:
+    AUTO with the length hint (fused_single's 32- and 64-row tiles, the designated merger) and
+    without it (the segmentation planned on the device), against the oracle."""
+    import torch
+    kvattn = _kv()
+    B, maxT = 2, 1024
+    for T in (100, 200, 700, 1024):
+        case = make_case(dtype, B, NH, maxT, [T - 1] * B, seed=600 + NH + T)
+        qkv, cache, scale, _ = to_device(case, dev)
+        cur = torch.tensor([T - 1], dtype=torch.int32, device=dev)
+        for hint in (T - 1, -1):
+            out = out_tensor(case, dev)
+            ws = kvattn.Workspace(B, NH, maxT, 0)
+            kvattn.decode(out, qkv, cache, B, NH, HS, maxT, kv_dtype=dtype, kv_scale=scale, cur_len=cur,
+                          len_hint=hint, strategy="auto", **ws.kwargs())
+            torch.cuda.synchronize()
+            assert_close(out.float().cpu().numpy(), case.reference(), dtype, f"NH={NH} T={T} hint={hint}")
+
+
 @pytest.mark.parametrize("dtype", ["bf16", "int8"])
 @pytest.mark.parametrize("B,NH", [(1, 7), (1, 8), (3, 3), (1, 12), (17, 1), (2, 12), (5, 8)])
 def test_designated_head_counts_around_the_xcd_layout(dev, dtype, B, NH):
