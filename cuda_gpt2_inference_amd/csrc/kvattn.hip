@@ -113,7 +113,8 @@ constexpr int kWavesLat = KVATTN_LAT_WAVES;
 // fused_single: a head of up to kFusedMaxRows positions is one tile per wave.  A wave's
 // arithmetic over its tile is the call's critical path while the heads leave CUs idle, and a
 // 4-wave workgroup puts one wave on each SIMD of its CU.  So:
-// - Hinted lengths up to 128 take 4 waves of 32-row tiles (every wave holds rows).  Measured
+// - Hinted lengths up to 128 (the longest, with per-sequence lengths) take 4 waves of 32-row
+//   tiles (every wave holds rows).  Measured
 //   (12 calls per graph, B·NH from 12 to 768): 10-17 % faster than 4 waves of 64-row tiles at
 //   12-96 heads, 10-33 % at 384-768 heads.
 // - Otherwise FP32 rows, the widest (four lanes' arithmetic per row of bf16), take 8 waves of
@@ -1873,13 +1874,16 @@ int dispatch_dtype(int dt, F&& f) {
 
 // kv_out == nullptr: attention only.  Otherwise the kernel also appends the current
 // token's row into kv_out / kv_scale_out (the same cache as kv / kv_scale).
+// spec_rows: the hinted length the kernel may request tiles for before it reads the device
+// length (one length for the batch), else 0.  hint_rows: the host's hinted (longest) length,
+// which picks the tile shape only, else 0.
 int launch_fused_single(void* out, const void* qkv, const void* kv, const float* kv_scale, void* kv_out,
                         float* kv_scale_out, int B, int NH, int maxT, const int* cur_len, int lens_per_seq,
-                        int spec_rows, int kv_dtype, hipStream_t stream) {
+                        int spec_rows, int hint_rows, int kv_dtype, hipStream_t stream) {
     const size_t lds = (size_t)maxT * sizeof(float);
     if (lds > kFusedMaxLds) return KVATTN_ERR_LDS;
     const float qs = qscale_for(kHeadDim);
-    const bool short_tiles = spec_rows > 0 && spec_rows <= kFusedShortWaves * kFusedShortRows;
+    const bool short_tiles = hint_rows > 0 && hint_rows <= kFusedShortWaves * kFusedShortRows;
     const bool wide_f32 = kv_dtype == KVATTN_KV_F32 && (long long)B * NH > kFusedF32WideHeads;
     return dispatch_dtype(kv_dtype, [&](auto dtc) -> int {
         constexpr int DT = decltype(dtc)::value;
@@ -2395,8 +2399,8 @@ int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scal
         KV_TRY(resolve_len(d_cur_len));
         return launch_fused_single(out, qkv, kv, kv_scale, append ? const_cast<void*>(kv) : nullptr,
                                    append ? const_cast<float*>(kv_scale) : nullptr, B, NH, maxT, d_cur_len,
-                                   lens_per_seq, (lens_per_seq || len_hint < 0) ? 0 : len_hint + 1, kv_dtype,
-                                   stream);
+                                   lens_per_seq, (lens_per_seq || len_hint < 0) ? 0 : len_hint + 1,
+                                   len_hint < 0 ? 0 : len_hint + 1, kv_dtype, stream);
     }
 
     Workspace w{};
@@ -2709,7 +2713,7 @@ int kvattn_forward_small(void* out, const void* qkv, const void* kv_cache, const
     if (!aligned16(out)) return KVATTN_ERR_MISALIGNED;
     KV_TRY(resolve_len(d_cur_len));
     return launch_fused_single(out, qkv, kv_cache, kv_scale, nullptr, nullptr, B, NH, maxT, d_cur_len,
-                               lens_per_seq, 0, kv_dtype, (hipStream_t)stream);
+                               lens_per_seq, 0, 0, kv_dtype, (hipStream_t)stream);
 }
 
 int kvattn_forward_large(void* out, const void* qkv, const void* kv_cache, const float* kv_scale, int B, int NH,

@@ -104,6 +104,26 @@ def test_fused_single_short_tiles(dev, dtype):
     assert_close(got, case.reference(), dtype, "auto B=8 hint 97 T=97")
 
 
+@pytest.mark.parametrize("dtype", ALL_DT)
+def test_fused_single_short_tiles_per_sequence_lengths(dev, dtype):
+    """Per-sequence lengths with a hinted longest length up to 128 take the 32-row tiles too
+    (the hint picks the shape; no tile is requested before the lengths): rows past each
+    sequence's length are poisoned, and a stale hint shorter than some lengths sends those
+    sequences to the scores staged in LDS."""
+    import torch
+    kvattn = _kv()
+    for maxT, lens, hint in ((256, [1, 37, 64, 128, 100, 5], 128), (1024, [90, 300, 17, 128, 700, 64], 100)):
+        B = len(lens)
+        case = poison_past_length(make_case(dtype, B, 12, maxT, np.array(lens) - 1, seed=490 + maxT))
+        qkv, cache, scale, cur = to_device(case, dev)
+        out = out_tensor(case, dev)
+        ws = kvattn.Workspace(B, 12, maxT, 0)
+        kvattn.decode(out, qkv, cache, B, 12, HS, maxT, kv_dtype=dtype, kv_scale=scale, cur_len=cur,
+                      lens_per_seq=True, len_hint=hint - 1, strategy="auto", **ws.kwargs())
+        torch.cuda.synchronize()
+        assert_close(out.float().cpu().numpy(), case.reference(), dtype, f"lens {lens} hint {hint}")
+
+
 @pytest.mark.parametrize("B,NH", [(24, 12), (21, 12), (16, 17)])
 def test_fused_single_fp32_across_the_head_count_switch(dev, B, NH):
     """FP32 fused_single takes 4 waves of 64-row tiles beyond 256 heads (B * NH = 288 and
