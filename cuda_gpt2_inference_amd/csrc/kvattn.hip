@@ -1876,7 +1876,7 @@ int dispatch_dtype(int dt, F&& f) {
 // token's row into kv_out / kv_scale_out (the same cache as kv / kv_scale).
 // spec_rows: the hinted length the kernel may request tiles for before it reads the device
 // length (one length for the batch), else 0.  hint_rows: the host's hinted (longest) length,
-// which picks the tile shape only, else 0.
+// or maxT when any length may come, which picks the tile shape only; 0: the general shape.
 int launch_fused_single(void* out, const void* qkv, const void* kv, const float* kv_scale, void* kv_out,
                         float* kv_scale_out, int B, int NH, int maxT, const int* cur_len, int lens_per_seq,
                         int spec_rows, int hint_rows, int kv_dtype, hipStream_t stream) {
@@ -2400,7 +2400,7 @@ int decode_impl(void* out, const void* qkv, const void* kv, const float* kv_scal
         return launch_fused_single(out, qkv, kv, kv_scale, append ? const_cast<void*>(kv) : nullptr,
                                    append ? const_cast<float*>(kv_scale) : nullptr, B, NH, maxT, d_cur_len,
                                    lens_per_seq, (lens_per_seq || len_hint < 0) ? 0 : len_hint + 1,
-                                   len_hint < 0 ? 0 : len_hint + 1, kv_dtype, stream);
+                                   len_hint < 0 ? maxT : len_hint + 1, kv_dtype, stream);
     }
 
     Workspace w{};
