@@ -20,7 +20,9 @@ Also in the same JSON line:
                 built, else the oracle's restatement (kind "port"); a reported baseline, not
                 the target.  Every configuration in extra.configs (C1, C3, C4) and extra.c5
                 carries its own (C5: the whole 64-sequence call, median of three).
-  extra         eager and cold-cache per-call times, and the scaled-up ragged configuration: 64
+  extra         eager and cold-cache per-call times (eager_us_per_call through Python's ctypes;
+                eager_cpp the same 12-layer step called from C++, tests/cpp/eager_timing), and
+                the scaled-up ragged configuration: 64
                 sequences x NH=12, BF16, lengths ~ U[1, 8192] (~0.8 GB of KV per call),
                 which streams from HBM and carries the >=70 % of peak target.  The 8-bit
                 configurations (C3 INT8 with 1 % outliers x8, C4 FP8) time caches filled by
@@ -1077,6 +1079,21 @@ def cache_sweep(torch, kvattn, dev, reps=40):
     return out
 
 
+def eager_cpp(dtype="bf16", B=1, NH=12, maxT=1024, cur_len=1023, layers=12, steps=200):
+    """The C2 stack called eagerly from C++ (tests/cpp/eager_timing, a child process): the
+    reference engine's per-layer call without --graph, free of the Python ctypes overhead that
+    `eager_us_per_call` carries.  None when the tool is not built."""
+    import subprocess
+    exe = os.path.join(ROOT, "tests", "cpp", "eager_timing")
+    if not os.path.exists(exe):
+        return None
+    r = subprocess.run([exe, dtype, str(B), str(NH), str(maxT), str(cur_len), str(layers), str(steps)],
+                       capture_output=True, text=True, timeout=120)
+    if r.returncode != 0:
+        raise RuntimeError(f"eager_timing failed ({r.returncode}): {r.stderr.strip()[-300:]}")
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -1135,6 +1152,9 @@ def main():
     coop = None if args.no_configs else coop_configs(torch, kvattn, dev, cpu_seconds=cpu_s)
     c2 = C2(args, torch, kvattn, dev)
     graph_ms, eager_ms = c2.measure()
+    torch.cuda.synchronize()
+    with phase("c2_eager_cpp"):
+        eager_c = eager_cpp()
     rel = c2.check()
     long_graph = c2.measure_long()
     cold_us = c2.cold()
@@ -1194,6 +1214,7 @@ def main():
                      "kernel": key2, "bytes_per_launch": nbytes, "us_per_launch": round(us_call, 4)},
         "cpu_baseline": cpu,
         "extra": {"eager_us_per_call": round(eager_ms * 1000.0 / c2.L, 4),
+                  "eager_cpp": eager_c,
                   "c2_long_graph": long_graph,
                   "cold_us_per_call": round(cold_us, 3),
                   "c2_context_sweep": t_sweep,
