@@ -759,3 +759,42 @@ def test_seeded_shape_sweep(dev):
             print(f"  refused ({e}); last-block instead", flush=True)
             got = _run(case, dev, "lastblock", S=S, len_hint=len_hint)
         assert_close(got, case.reference(), dtype, name)
+
+
+def test_seeded_auto_sweep(dev):
+    """40 AUTO calls drawn from a fixed seed across the plan space AUTO chooses from: GPT-2's
+    head counts (12, 16, 20, 25), B up to 40, maxT from 64 to 2048 (at most 256K cache rows),
+    one length for the batch or per-sequence lengths, a length hint that is exact, stale
+    (any value below maxT) or absent.  That reaches fused_single's three tile shapes, the
+    designated merger (host- and device-planned), one segment per head and the split + merge
+    plans; each call against the oracle."""
+    import torch
+    kvattn = _kv()
+    rng = np.random.RandomState(4242)
+    for i in range(40):
+        dtype = ALL_DT[rng.randint(len(ALL_DT))]
+        NH = int(rng.choice([12, 16, 20, 25]))
+        maxT = int(rng.choice([64, 128, 256, 512, 1024, 2048]))
+        B = int(rng.randint(1, max(2, min(40, (1 << 18) // (NH * maxT)) + 1)))
+        ragged = bool(rng.randint(2))
+        if ragged:
+            lens = rng.randint(1, maxT + 1, B).astype(np.int32)
+        else:
+            lens = np.full(B, int(rng.randint(1, maxT + 1)), np.int32)
+        hint_kind = rng.randint(3)
+        len_hint = -1 if hint_kind == 0 else (int(lens.max()) - 1 if hint_kind == 1 else int(rng.randint(0, maxT)))
+        plan = kvattn.plan(B, NH, HS, maxT, kv_dtype=dtype, len_hint=len_hint)
+        name = (f"case {i}: {dtype} B={B} NH={NH} maxT={maxT} {'ragged' if ragged else 'uniform'} "
+                f"hint={len_hint} plan={plan} lens={lens.tolist()[:8]}")
+        print(name, flush=True)
+        case = make_case(dtype, B, NH, maxT, lens - 1, seed=9500 + i)
+        qkv, cache, scale, cur = to_device(case, dev)
+        if not ragged:
+            cur = cur[:1].contiguous()
+        out = out_tensor(case, dev)
+        ws = kvattn.Workspace(B, NH, maxT, 0)
+        kvattn.decode(out, qkv, cache, B, NH, HS, maxT, kv_dtype=dtype, kv_scale=scale, cur_len=cur,
+                      lens_per_seq=ragged, len_hint=len_hint, strategy="auto", **ws.kwargs())
+        torch.cuda.synchronize()
+        assert ws.status() == 0, name
+        assert_close(out.float().cpu().numpy(), case.reference(), dtype, name)
