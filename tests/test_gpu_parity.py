@@ -766,8 +766,8 @@ def test_seeded_auto_sweep(dev):
     head counts (12, 16, 20, 25), B up to 40, maxT from 64 to 2048 (at most 256K cache rows),
     one length for the batch or per-sequence lengths, a length hint that is exact, stale
     (any value below maxT) or absent.  That reaches fused_single's three tile shapes, the
-    designated merger (host- and device-planned), one segment per head and the split + merge
-    plans; each call against the oracle."""
+    designated merger (host- and device-planned) and the last-block plans (the split + merge
+    plans need more cache than this bound: test_gpu_plans); each call against the oracle."""
     import torch
     kvattn = _kv()
     rng = np.random.RandomState(4242)
