@@ -2248,7 +2248,11 @@ bool latency_bound(int B, int NH, int total_rows) { return (long long)B * NH * t
 //   (a power of two, so at most 16 per head; up to 64 per head when fewer than 12 heads
 //   share the GPU), doubled up to 512 rows while the grid is too large; not when the
 //   doubling left 8 or more segments per head of a call above kAutoDoubledMaxBytes (96 heads
-//   x 8 segments of 256 or 512 rows: measured slower than the split + merge kernel).  8-bit
+//   x 8 segments of 256 or 512 rows: measured slower than the split + merge kernel).  Up to
+//   64 heads whose segments are long (256 rows or more, 512 for 8-bit caches) the grid may
+//   reach 1024 workgroups (49-64 heads x 16 segments; measured, A/B over NH = 12-64: BF16 at
+//   4096 positions -7 % to +1 %, INT8 and FP8 at 8192 -1 % to -16 %, with or without a
+//   hint; with 128-row segments the wider grid lost 4-17 %).  8-bit
 //   caches take the streaming shape for segments of 256 rows or more on grids of up to 384
 //   workgroups (one 64-row tile per wave).
 // - Beyond that the call is bandwidth bound: with one length for every sequence, BF16 streams
@@ -2278,10 +2282,11 @@ bool tuned_auto(int B, int NH, int maxT, int total_hint, int kv_dtype, bool ragg
     const int target = (int)std::min<long long>(kMaxDesignatedSegments, std::max<long long>(16, 192 / heads));
     const int r0 = std::max(128, ceil_pow2(ceil_div_i(maxT, target)));
     int r = r0;
-    while (heads * ceil_div_i(maxT, r) > kAutoDesignatedMaxGrid && r < 512) r <<= 1;
+    const long long max_grid = heads <= 64 && r0 >= (k8 ? 512 : 256) ? 1024 : kAutoDesignatedMaxGrid;
+    while (heads * ceil_div_i(maxT, r) > max_grid && r < 512) r <<= 1;
     const int segs = ceil_div_i(maxT, r);
     const long long grid = heads * segs;
-    if (grid <= kAutoDesignatedMaxGrid && bytes <= kAutoDesignatedMaxBytes &&
+    if (grid <= max_grid && bytes <= kAutoDesignatedMaxBytes &&
         !(r > r0 && segs >= 8 && bytes > kAutoDoubledMaxBytes)) {
         p.strategy = KVATTN_SPLIT_DESIGNATED;
         p.seg_rows = r;

@@ -43,6 +43,9 @@ CASES = [
     ("fp8", 4, 12, 2048, 2000, ("designated", 16, 128)),
     # designated merger, 8-bit streaming tiles (256-row segments, 192 workgroups)
     ("int8", 1, 12, 4096, 4096, ("designated", 16, 256)),
+    # up to 64 heads with long segments: designated grids past 768 workgroups
+    ("bf16", 2, 25, 4096, 4096, ("designated", 16, 256)),
+    ("fp8", 1, 49, 8192, 8000, ("designated", 16, 512)),
     # FP32 beyond the designated window keeps the general plan (last-block merge)
     ("f32", 16, 12, 1024, 1024, ("lastblock", 4, 256)),
 ]
@@ -140,6 +143,7 @@ NO_HINT = [
     ("bf16", 1, 12, 4096, [1000, 4096], ("designated", 16, 256), False),
     ("fp8", 32, 12, 1024, [300, 1024], ("designated", 2, 512), False),
     ("bf16", 16, 12, 512, [300, 512], ("lastblock", 1, 512), False),
+    ("int8", 5, 12, 8192, [700, 8192], ("designated", 16, 512), False),
     ("int8", 8, 12, 1024, [1024, 77, 512, 1000, 129, 300, 1024, 1], ("designated", 8, 128), True),
 ]
 

@@ -73,6 +73,12 @@ TUNED = [
     ((32, 12, 1024, 1023, "fp8"), (kvattn.SPLIT_DESIGNATED, 2, 512)),    # doubled twice, 53.6 MB
     ((8, 12, 2048, 2047, "int8"), (kvattn.SPLIT_DESIGNATED, 8, 256)),    # doubled, 8 segments, 26.8 MB
     ((1, 2, 8192, 8191, "bf16"), (kvattn.SPLIT_DESIGNATED, 64, 128)),    # 2 heads: up to 64 segments
+    # up to 64 heads with long segments (256 rows, 512 for 8-bit): grids of up to 1024
+    ((2, 25, 4096, 4095, "bf16"), (kvattn.SPLIT_DESIGNATED, 16, 256)),   # 50 x 16 = 800
+    ((1, 64, 4096, 4095, "bf16"), (kvattn.SPLIT_DESIGNATED, 16, 256)),   # 64 x 16 = 1024, 64 MiB
+    ((5, 12, 8192, 8191, "fp8"), (kvattn.SPLIT_DESIGNATED, 16, 512)),    # 60 x 16 = 960
+    ((5, 12, 2048, 2047, "bf16"), (kvattn.SPLIT_DESIGNATED, 8, 256)),    # 128-row segments: 768 still
+    ((5, 12, 4096, 4095, "int8"), (kvattn.SPLIT_DESIGNATED, 8, 512)),    # 8-bit 256-row segments: 768 still
     # not designated: doubled to 8 segments above 40 MB, or above 64 MB, or a grid beyond 768
     ((8, 12, 2048, 2047, "bf16"), (kvattn.SPLIT_MERGE, 8, 256)),
     ((8, 12, 4096, 4095, "fp8"), (kvattn.SPLIT_LASTBLOCK, 8, 512)),      # FP8: the general plan
@@ -90,7 +96,8 @@ def test_auto_with_hint_takes_the_measured_plan(args, plan):
 
 def test_auto_tuned_plans_stay_within_their_bounds():
     """Every hinted AUTO plan over a grid of shapes: a designated grid of at most 768
-    workgroups and 64 segments per head, at most 16 once there are 12 or more heads; the
+    workgroups (1024 for up to 64 heads with segments of 256 rows or more, 512 for 8-bit
+    caches) and 64 segments per head, at most 16 once there are 12 or more heads; the
     one-segment plan only for 192+ heads of at most 512 rows; and the GPT-2 layer (B = 1,
     NH = 12, maxT = 1024) unchanged at every length past fused_single."""
     for dt in ("f32", "bf16", "int8", "fp8"):
@@ -101,7 +108,8 @@ def test_auto_tuned_plans_stay_within_their_bounds():
                         st, slots, rows = kvattn.plan(B, NH, 64, maxT, kv_dtype=dt, len_hint=hint)
                         heads = B * NH
                         if st == kvattn.SPLIT_DESIGNATED:
-                            assert heads * slots <= 768 and slots <= 64, (dt, B, NH, maxT, hint)
+                            wide = heads <= 64 and rows >= (512 if dt in ("int8", "fp8") else 256)
+                            assert heads * slots <= (1024 if wide else 768) and slots <= 64, (dt, B, NH, maxT, hint)
                             if heads >= 12:
                                 assert slots <= 16, (dt, B, NH, maxT, hint)
                         if st == kvattn.SPLIT_LASTBLOCK and slots == 1 and rows == 512:
