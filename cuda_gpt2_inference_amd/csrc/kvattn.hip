@@ -2258,13 +2258,16 @@ bool latency_bound(int B, int NH, int total_rows) { return (long long)B * NH * t
 // - Beyond that the call is bandwidth bound: with one length for every sequence, BF16 streams
 //   256-row segments with the latency shape's tiles and INT8 256-row segments with the
 //   streaming shape's (512 rows and the latency shape from contexts of 8192), through the
-//   split + merge kernels; FP32 and FP8, and per-sequence lengths (whose streaming kernel
+//   split + merge kernels, at most 64 segments per head (longer rows, in the streaming shape,
+//   from contexts of 16384 (BF16) or 32768 (INT8) on: measured 1-12 % faster at 32768-131072
+//   positions than 128-512 segments per head); FP32 and FP8, and per-sequence lengths (whose streaming kernel
 //   packs two segments per workgroup on the general plan: 64 sequences of up to 8192
 //   positions ran 9 % slower on 256-row segments), keep the general plan (false).
 // Returns false to leave the plan to the general rules below.
 constexpr long long kAutoDesignatedMaxGrid = 768;
 constexpr long long kAutoDesignatedMaxBytes = 64ll << 20;
 constexpr long long kAutoDoubledMaxBytes = 40ll << 20;
+constexpr int kMaxMergeSegments = 64;   // segments per head of the bandwidth-bound split + merge plan
 bool tuned_auto(int B, int NH, int maxT, int total_hint, int kv_dtype, bool ragged, Plan& p) {
     const long long heads = (long long)B * NH;
     const bool k8 = is_8bit(kv_dtype);
@@ -2298,8 +2301,15 @@ bool tuned_auto(int B, int NH, int maxT, int total_hint, int kv_dtype, bool ragg
         const bool long_int8 = kv_dtype == KVATTN_KV_INT8 && maxT >= 8192;
         p.strategy = KVATTN_SPLIT_MERGE;
         p.seg_rows = long_int8 ? 512 : 256;
-        p.slots = ceil_div_i(maxT, p.seg_rows);
         p.lat = kv_dtype == KVATTN_KV_BF16 || long_int8;
+        // At most kMaxMergeSegments segments per head: longer rows, in the streaming shape,
+        // once the context passes that many segments.
+        const int capped = ceil_pow2(ceil_div_i(maxT, kMaxMergeSegments));
+        if (capped > p.seg_rows) {
+            p.seg_rows = capped;
+            p.lat = false;
+        }
+        p.slots = ceil_div_i(maxT, p.seg_rows);
         return true;
     }
     return false;

@@ -34,6 +34,9 @@ CASES = [
     ("int8", 12, 12, 4096, 4096, ("split_merge", 16, 256)),
     # bandwidth bound INT8 at a context of 8192 (71 MB): 512-row segments
     ("int8", 2, 32, 8192, 8192, ("split_merge", 16, 512)),
+    # long contexts: at most 64 segments per head, longer rows in the streaming shape
+    ("bf16", 1, 12, 32768, 32000, ("split_merge", 64, 512)),
+    ("int8", 1, 12, 65536, 65536, ("split_merge", 64, 1024)),
     # 192 heads of at most 512 rows: one segment per head, no merge
     ("fp8", 16, 12, 512, 512, ("lastblock", 1, 512)),
     ("int8", 32, 12, 512, 480, ("lastblock", 1, 512)),

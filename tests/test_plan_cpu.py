@@ -85,6 +85,11 @@ TUNED = [
     ((32, 12, 1024, 1023, "bf16"), (kvattn.SPLIT_MERGE, 4, 256)),
     ((16, 12, 1024, 1023, "f32"), (kvattn.SPLIT_LASTBLOCK, 4, 256)),
     ((2, 32, 8192, 8191, "int8"), (kvattn.SPLIT_MERGE, 16, 512)),
+    # split + merge: at most 64 segments per head, longer rows past that
+    ((2, 12, 16384, 16383, "bf16"), (kvattn.SPLIT_MERGE, 64, 256)),
+    ((1, 12, 32768, 32767, "bf16"), (kvattn.SPLIT_MERGE, 64, 512)),
+    ((1, 12, 65536, 65535, "int8"), (kvattn.SPLIT_MERGE, 64, 1024)),
+    ((16, 12, 20000, 19999, "bf16"), (kvattn.SPLIT_MERGE, 40, 512)),
 ]
 
 
