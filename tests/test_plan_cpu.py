@@ -238,3 +238,17 @@ def test_designated_rows_closed_form_matches_the_rule(heads):
                                      strategy="designated")
         assert (st, got) == (kvattn.SPLIT_DESIGNATED, rows if total > 256 else total), (total, heads)
         assert slots == -(-total // got)
+
+
+def test_auto_caps_hinted_split_segments_at_64_per_head():
+    """AUTO with one length for the batch grows the rows instead of passing 64 segments per
+    head of the hinted length (general plan: FP8 / FP32; tuned plan: BF16 / INT8, sized from
+    the hint, not maxT); explicit strategies keep 512-row segments."""
+    assert kvattn.plan(1, 12, 64, 65536, kv_dtype="fp8", len_hint=65535) == (kvattn.SPLIT_MERGE, 64, 1024)
+    assert kvattn.plan(1, 12, 64, 65536, kv_dtype="f32", len_hint=65535) == (kvattn.SPLIT_MERGE, 64, 1024)
+    assert kvattn.plan(1, 12, 64, 65536, kv_dtype="fp8", len_hint=65535, strategy="lastblock") == \
+        (kvattn.SPLIT_LASTBLOCK, 128, 512)
+    # a hint of 16384 in a 65536-row cache: 256-row segments for the hinted length, the grid
+    # covering maxT
+    assert kvattn.plan(8, 12, 64, 65536, kv_dtype="bf16", len_hint=16383) == (kvattn.SPLIT_MERGE, 256, 256)
+    assert kvattn.plan(1, 12, 64, 32768, kv_dtype="fp8", len_hint=32767)[2] == 512
