@@ -251,4 +251,4 @@ def test_auto_caps_hinted_split_segments_at_64_per_head():
     # a hint of 16384 in a 65536-row cache: 256-row segments for the hinted length, the grid
     # covering maxT
     assert kvattn.plan(8, 12, 64, 65536, kv_dtype="bf16", len_hint=16383) == (kvattn.SPLIT_MERGE, 256, 256)
-    assert kvattn.plan(1, 12, 64, 32768, kv_dtype="fp8", len_hint=32767)[2] == 512
+    assert kvattn.plan(4, 12, 64, 32768, kv_dtype="fp8", len_hint=32767) == (kvattn.SPLIT_MERGE, 64, 512)
