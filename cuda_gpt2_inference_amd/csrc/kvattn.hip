@@ -54,7 +54,7 @@ constexpr float kEmptyMax = -FLT_MAX;   // max of an empty segment (reference se
 constexpr float kStartMax = -1.0e30f;   // finite start value of every running max
 constexpr int kMinSegRows = 64;         // smallest automatic segment length
 constexpr int kMaxSegRows = 512;        // largest automatic segment length up to kMaxMergeSegments segments
-constexpr int kMaxMergeSegments = 64;   // AUTO: beyond that many segments of a hinted length, rows grow instead
+constexpr int kMaxMergeSegments = 64;   // beyond that many 512-row segments (AUTO's hinted and device plans), rows grow
 constexpr int kFusedMaxRows = 256;      // automatic plans keep up to this many positions in one workgroup
 constexpr int kStridedMaxSeqs = 256;    // ragged batches up to this size take the strided grid
 constexpr int kStridedFactor = 2;       // segments per workgroup bound of the strided grid
@@ -912,7 +912,10 @@ __host__ __device__ __forceinline__ int ceil_pow2(int x) {
 
 __host__ __device__ __forceinline__ int planned_rows(int total) {
     const int want = ceil_div_i(total, 4);
-    const int r = min(max(kMinSegRows, ceil_pow2(max(want, 1))), kMaxSegRows);
+    int r = min(max(kMinSegRows, ceil_pow2(max(want, 1))), kMaxSegRows);
+    // Past kMaxMergeSegments segments of kMaxSegRows rows the rows grow instead, up to what a
+    // paged wave walks.
+    r = max(r, min(ceil_pow2(max(ceil_div_i(total, kMaxMergeSegments), 1)), kMaxPagedSegRows));
     return total <= kFusedMaxRows ? (total > 0 ? total : 1) : r;
 }
 
@@ -2209,8 +2212,9 @@ int auto_seg_rows(int total_hint) {
 }
 
 // Segment slots that cover planned_rows() at every length up to maxT: one segment up to
-// kFusedMaxRows positions, at most four while planned_rows(total) >= total / 4, and
-// ceil(total / kMaxSegRows) beyond.
+// kFusedMaxRows positions, at most four while planned_rows(total) >= total / 4,
+// ceil(total / kMaxSegRows) beyond, at most kMaxMergeSegments from there until the rows
+// reach kMaxPagedSegRows, and ceil(total / kMaxPagedSegRows) past that.
 // Segment slots covering designated_rows() at every length up to maxT.
 int designated_slots(int maxT, int heads) {
     if (maxT <= kFusedMaxRows) return 1;
@@ -2219,7 +2223,9 @@ int designated_slots(int maxT, int heads) {
 
 int planned_slots(int maxT) {
     if (maxT <= kFusedMaxRows) return 1;
-    const int s = ceil_div_i(maxT, kMaxSegRows);
+    const int s = maxT <= kMaxSegRows * kMaxMergeSegments
+                      ? ceil_div_i(maxT, kMaxSegRows)
+                      : std::max(kMaxMergeSegments, ceil_div_i(maxT, kMaxPagedSegRows));
     return s > 4 ? s : 4;
 }
 

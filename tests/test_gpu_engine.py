@@ -53,6 +53,31 @@ def test_device_plan_uniform_length(dev, dtype):
             assert_close(out.float().cpu().numpy(), case.reference(), dtype, f"{strategy} T={total}")
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "int8"])
+def test_device_plan_past_64_segments(dev, dtype):
+    """Past 64 segments of 512 rows (32768 positions) the device plan grows the rows instead
+    (1024 from 32769, 2048 from 65537): split strategies with no hint, one length for the
+    batch and per-sequence lengths, at and around those edges, against the oracle."""
+    import torch
+    kvattn = _kv()
+    B, NH, maxT = 2, 2, 70000
+    ws = kvattn.Workspace(B, NH, maxT, 0)
+    for strategy in ("split_merge", "lastblock", "graph"):
+        assert kvattn.plan(B, NH, HS, maxT, kv_dtype=dtype, strategy=strategy)[1:] == (64, -1)
+    for lens in ([32768, 32768], [32769, 32769], [65536, 65536], [65537, 70000], [70000, 300], [40000, 33000]):
+        case = make_case(dtype, B, NH, maxT, np.array(lens) - 1, seed=37 + lens[0] % 97)
+        qkv, cache, scale, cur = to_device(case, dev)
+        uniform = lens[0] == lens[1]
+        if uniform:
+            cur = cur[:1].contiguous()
+        for strategy in ("split_merge", "lastblock", "graph"):
+            out = out_tensor(case, dev)
+            kvattn.decode(out, qkv, cache, B, NH, HS, maxT, kv_dtype=dtype, kv_scale=scale, cur_len=cur,
+                          lens_per_seq=not uniform, strategy=strategy, **ws.kwargs())
+            torch.cuda.synchronize()
+            assert_close(out.float().cpu().numpy(), case.reference(), dtype, f"{strategy} lens={lens}")
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16", "fp8"])
 def test_designated_device_plan_doubled_rows(dev, dtype):
     """The designated merger planned on the device beyond 64 segments of the base length:
