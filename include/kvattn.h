@@ -259,7 +259,8 @@ int kvattn_plan(int B, int NH, int hs, int maxT, int len_hint, int S, int strate
  *   len_hint   -1 when the call must serve any length, as a graph captured once and
  *              replayed token after token: with S == 0 the kernels then plan the
  *              segmentation from the device length (one segment up to 256 positions,
- *              about four beyond), where the reference captures a small and a large
+ *              about four beyond, segments of at most 512 rows up to 64 of them, longer
+ *              rows past 32768 positions), where the reference captures a small and a large
  *              graph and picks one per token (inference_gpt2_opt.cu:420-449,556).  AUTO
  *              with more than 16 heads (B*NH), or a longer maxT, takes fixed rows sized
  *              for maxT instead while its designated grid stays small (kvattn_plan
