@@ -84,7 +84,8 @@ typedef enum kvattn_strategy {
                                        segment 0 polls for them; one ordinary launch,
                                        capturable; at most 64 segments per (b,h).  AUTO's
                                        choice for latency-bound calls (with a length hint:
-                                       grids of up to 768 workgroups and 64 MiB of cache). */
+                                       grids of up to 768 workgroups, 1024 for up to 64
+                                       heads with long segments, and 64 MiB of cache). */
 } kvattn_strategy;
 
 /* Human-readable text of a status code. */
