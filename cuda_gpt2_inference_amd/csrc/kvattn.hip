@@ -562,7 +562,9 @@ __device__ __forceinline__ int paged_tile_ids(const PagedView& pv, int b, int j0
 
 // Online softmax over rows [j0, j1) of (b, h) (j0 a multiple of kTile) by one wave of kW.
 // kFresh: the row `cur` is taken from fr and written through the table.
-template <int DT, int kU, int kW, bool kFresh, bool kHw = false>
+// kAhead: the wave's first two tiles are both requested before the first is consumed (the
+// paged latency shape of the 8-bit caches, whose waves walk one or a few tiles).
+template <int DT, int kU, int kW, bool kFresh, bool kHw = false, bool kAhead = false>
 __device__ __forceinline__ void online_tiles_paged(const PagedView& pv, int b, int h, int j0, int j1, int wave,
                                                    int slot_row, int slice, const QRaw<DT>& qr, float qscale,
                                                    const FreshRaw<DT>& fr, uint8_t* kv_out, float* kv_scale_out,
@@ -577,7 +579,32 @@ __device__ __forceinline__ void online_tiles_paged(const PagedView& pv, int b, i
     convert_q<DT, kHw>(qr, qscale, q);
     Tile<DT, kU> t;
     int i = 0;
-    for (int r = j0 + wave * kTile; r < j1; r += kW * kTile, ++i) {
+    int r = j0 + wave * kTile;
+    if constexpr (kAhead) {
+        // Tiles 0 and 1 of the wave (rows ra and rb), each from its own page, both checked
+        // against j1 as the walk's last tile is.
+        Tile<DT, kU> t1;
+        const int ra = r, rb = r + kW * kTile;
+        const int pa = __shfl(pid, 0), pb = __shfl(pid, 1);
+        const bool va = ra < j1 && pa >= 0 && pa < pv.num_pages;
+        const bool vb = rb < j1 && pb >= 0 && pb < pv.num_pages;
+        const int a0 = ra / P * P, b0 = rb / P * P;
+        if (va) load_tile<DT, kU, true>(t, page_slot<DT>(pv, pa, h, slice), ra - a0, j1 - a0, slot_row);
+        if (vb) load_tile<DT, kU, true>(t1, page_slot<DT>(pv, pb, h, slice), rb - b0, j1 - b0, slot_row);
+        auto take = [&](Tile<DT, kU>& tt, int page, int rr, int p0) {
+            if (kFresh && cur >= rr && cur < min(rr + kTile, j1)) {
+                const size_t rk = ((size_t)page * 2 * pv.NH + h) * P + (cur - p0);
+                const FreshDst fd{kv_out, kv_scale_out, rk, rk + (size_t)pv.NH * P, slice};
+                patch_tile<DT, kU>(tt, fr, fd, rr - p0, slot_row, cur - p0);
+            }
+            consume_tile<DT, kU, true, kHw>(tt, rr - p0, j1 - p0, slot_row, q, m, l, acc);
+        };
+        if (va) take(t, pa, ra, a0);
+        if (vb) take(t1, pb, rb, b0);
+        r = rb + kW * kTile;
+        i = 2;
+    }
+    for (; r < j1; r += kW * kTile, ++i) {
         const int page = __shfl(pid, i);
         if (page < 0 || page >= pv.num_pages) continue;
         const int pr0 = r / P * P;
@@ -1143,6 +1170,10 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
     using R = Row<DT>;
     // The latency shape (tiles of KVATTN_SPLIT_LAT_ROWS rows) takes the hardware bf16 dot.
     constexpr bool kHwDot = kU == kUnrollSplitLat<DT>;
+    // Paged 8-bit caches in the latency shape request each wave's second tile with its first
+    // (measured on 12-layer graphs, 64- and 256-row pages: INT8 and FP8 3-17 % faster at
+    // 64-4096 positions; BF16 3-6 % slower, so it keeps the plain walk).
+    constexpr bool kPagedAhead = kPaged && kHwDot && R::k8bit;
     __shared__ float s_m[kW];
     __shared__ float s_l[kW];
     __shared__ float s_acc[kW][kHeadDim];
@@ -1275,9 +1306,9 @@ __global__ __launch_bounds__(kW * kWave, kW == kWaves ? KVATTN_STREAM_MIN_BLOCKS
                     q0 = load_q<DT>(a.qkv, it.b, it.h, a.NH, slice);
                     if constexpr (kFresh) fr = load_fresh<DT>(a.qkv, it.b, it.h, a.NH, slice);
                     pv = PagedView{a.kv, a.kv_scale, a.table, a.max_pages, a.page_rows, a.num_pages, a.NH};
-                    online_tiles_paged<DT, kU, kW, kFresh, kHwDot>(pv, it.b, it.h, j0, j1, wave, slot_row, slice, q0,
-                                                                   a.qscale, fr, a.kv_out, a.kv_scale_out, cur, m, l,
-                                                                   acc, pid_in, have_pid);
+                    online_tiles_paged<DT, kU, kW, kFresh, kHwDot, kPagedAhead>(
+                        pv, it.b, it.h, j0, j1, wave, slot_row, slice, q0, a.qscale, fr, a.kv_out, a.kv_scale_out,
+                        cur, m, l, acc, pid_in, have_pid);
                 } else {
                     sl = make_slot<DT>(a.kv, a.kv_scale, 1, BNH, a.maxT, bh, slice);   // B * NH: preloaded
                     // Device-planned segment 0 beyond its first kW tiles (128 < length <= 256): this
