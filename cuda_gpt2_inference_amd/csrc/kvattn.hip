@@ -581,23 +581,29 @@ __device__ __forceinline__ void online_tiles_paged(const PagedView& pv, int b, i
     int i = 0;
     int r = j0 + wave * kTile;
     if constexpr (kAhead) {
-        // Tiles 0 and 1 of the wave (rows ra and rb), each from its own page, both checked
-        // against j1 as the walk's last tile is.
+        // Tiles 0 and 1 of the wave (rows ra and rb), each from its own page; a tile that
+        // reaches j1 takes the checked loads and scores, as the walk's last tile does.
         Tile<DT, kU> t1;
         const int ra = r, rb = r + kW * kTile;
         const int pa = __shfl(pid, 0), pb = __shfl(pid, 1);
         const bool va = ra < j1 && pa >= 0 && pa < pv.num_pages;
         const bool vb = rb < j1 && pb >= 0 && pb < pv.num_pages;
         const int a0 = ra / P * P, b0 = rb / P * P;
-        if (va) load_tile<DT, kU, true>(t, page_slot<DT>(pv, pa, h, slice), ra - a0, j1 - a0, slot_row);
-        if (vb) load_tile<DT, kU, true>(t1, page_slot<DT>(pv, pb, h, slice), rb - b0, j1 - b0, slot_row);
+        auto ld = [&](Tile<DT, kU>& tt, int page, int rr, int p0) {
+            const Slot sp = page_slot<DT>(pv, page, h, slice);
+            if (rr + kTile <= j1) load_tile<DT, kU, false>(tt, sp, rr - p0, j1 - p0, slot_row);
+            else load_tile<DT, kU, true>(tt, sp, rr - p0, j1 - p0, slot_row);
+        };
+        if (va) ld(t, pa, ra, a0);
+        if (vb) ld(t1, pb, rb, b0);
         auto take = [&](Tile<DT, kU>& tt, int page, int rr, int p0) {
             if (kFresh && cur >= rr && cur < min(rr + kTile, j1)) {
                 const size_t rk = ((size_t)page * 2 * pv.NH + h) * P + (cur - p0);
                 const FreshDst fd{kv_out, kv_scale_out, rk, rk + (size_t)pv.NH * P, slice};
                 patch_tile<DT, kU>(tt, fr, fd, rr - p0, slot_row, cur - p0);
             }
-            consume_tile<DT, kU, true, kHw>(tt, rr - p0, j1 - p0, slot_row, q, m, l, acc);
+            if (rr + kTile <= j1) consume_tile<DT, kU, false, kHw>(tt, rr - p0, j1 - p0, slot_row, q, m, l, acc);
+            else consume_tile<DT, kU, true, kHw>(tt, rr - p0, j1 - p0, slot_row, q, m, l, acc);
         };
         if (va) take(t, pa, ra, a0);
         if (vb) take(t1, pb, rb, b0);
