@@ -215,18 +215,22 @@ class C2:
                         (kvattn_append_decode);
           graph_pair    the reference's pair: append + fused_single below 150 positions,
                         append + split + merge with S = 8 from 150 on (host switch per token);
+          graph_trio    three append + attention graphs picked per token by the host, as the
+                        reference picks its pair: hints of 127 and 255 positions (fused_single,
+                        32- and 64-row tiles) up to 128 and 256 positions, no hint beyond;
           attn_only     AUTO attention with no hint, without the append.
         Mean microseconds per token (whole 12-layer graph) and per layer."""
         torch, kvattn = self.torch, self.kvattn
         ws = kvattn.Workspace(self.B, self.NH, self.maxT, 0)
         ws8 = kvattn.Workspace(self.B, self.NH, self.maxT, 8)
 
-        def capture(strategy, S, append, w, fused=False):
+        def capture(strategy, S, append, w, fused=False, hint=-1):
             def step():
                 for l in range(self.L):
                     if fused:
                         kvattn.append_decode(self.outs[l], self.qkvs[l], self.caches[l], self.B, self.NH, HD,
-                                             self.maxT, kv_dtype="bf16", cur_len=self.cur, **w.kwargs())
+                                             self.maxT, kv_dtype="bf16", cur_len=self.cur, len_hint=hint,
+                                             **w.kwargs())
                         continue
                     if append:
                         kvattn.kv_cache_write(self.caches[l], self.qkvs[l], self.B, self.NH, HD, self.maxT,
@@ -245,8 +249,11 @@ class C2:
         fused = capture("auto", 0, True, ws, fused=True)
         small, large = capture("fused_single", 0, True, ws), capture("split_merge", 8, True, ws8)
         attn = capture("auto", 0, False, ws)
+        trio = [capture("auto", 0, True, ws, fused=True, hint=127), capture("auto", 0, True, ws, fused=True, hint=255),
+                fused]
         modes = {"one_graph": lambda t: one, "fused": lambda t: fused,
                  "graph_pair": lambda t: small if t < 150 else large,
+                 "graph_trio": lambda t: trio[0] if t < 128 else (trio[1] if t < 256 else trio[2]),
                  "attn_only": lambda t: attn}
         res = {"tokens": self.maxT}
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

@@ -240,12 +240,12 @@ class Engine:
         n = 2 * self.B * self.NH * self.maxT
         return None if self.scale is None else self.scale[l * n:(l + 1) * n]
 
-    def step(self, strategy="auto", S=0, fused=False):
+    def step(self, strategy="auto", S=0, fused=False, hint=-1):
         k = self.kvattn
         for l in range(self.L):
             args = (self.out[l], self.qkv[l], self.layer_cache(l), self.B, self.NH, HS, self.maxT)
             kw = dict(kv_dtype=self.dtype, kv_scale=self.layer_scale(l), cur_len=self.cur, S=S, strategy=strategy,
-                      **self.ws.kwargs())
+                      len_hint=hint, **self.ws.kwargs())
             if fused:
                 k.append_decode(*args, **kw)
                 continue
@@ -253,14 +253,14 @@ class Engine:
                              kv_scale=self.layer_scale(l), cur_len=self.cur)
             k.decode(*args, **kw)
 
-    def capture(self, strategy="auto", S=0, fused=False):
+    def capture(self, strategy="auto", S=0, fused=False, hint=-1):
         import torch
         torch.cuda.synchronize()
         s = torch.cuda.Stream()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.stream(s):
             with torch.cuda.graph(g, stream=s):
-                self.step(strategy, S, fused)
+                self.step(strategy, S, fused, hint)
         torch.cuda.synchronize()
         return g
 
@@ -273,14 +273,17 @@ def _host_values(t, dtype):
 
 
 @pytest.mark.parametrize("dtype,mode", [("bf16", "one_graph"), ("bf16", "graph_pair"), ("fp8", "one_graph"),
-                                        ("bf16", "fused"), ("int8", "fused")])
+                                        ("bf16", "fused"), ("int8", "fused"), ("bf16", "graph_trio"),
+                                        ("int8", "graph_trio")])
 def test_decode_step_token_by_token(dev, dtype, mode):
     """GPT-2 shape, 12 layers, B=1, NH=12, maxT=1024: the step graph is replayed for every
     token 1..1024 with fresh qkv and the device length advanced by set_cur_len_async.
     one_graph: one capture, AUTO with no hint.  fused: the same with kvattn_append_decode
     (append and attention in one launch per layer).  graph_pair: the reference's two graphs,
     fused_single below 150 positions and split + merge with S = 8 above (selection on the
-    host per token, as inference_gpt2_opt.cu:556).  Checked: every appended row bit for bit
+    host per token, as inference_gpt2_opt.cu:556).  graph_trio: three fused append + attention
+    graphs picked the same way, with length hints of 127 and 255 positions up to 128 and 256
+    positions and no hint beyond.  Checked: every appended row bit for bit
     (8-bit: codes and scales against the oracle's quantiser) and the outputs of all layers
     at 40 tokens (every plan edge and a stride) against the oracle."""
     import torch
@@ -290,6 +293,10 @@ def test_decode_step_token_by_token(dev, dtype, mode):
     if mode in ("one_graph", "fused"):
         graphs = [eng.capture("auto", fused=(mode == "fused"))]
         pick = lambda cur_len: graphs[0]
+    elif mode == "graph_trio":
+        graphs = [eng.capture("auto", fused=True, hint=127), eng.capture("auto", fused=True, hint=255),
+                  eng.capture("auto", fused=True)]
+        pick = lambda cur_len: graphs[0] if cur_len < 128 else (graphs[1] if cur_len < 256 else graphs[2])
     else:
         graphs = [eng.capture("fused_single"), eng.capture("split_merge", S=8)]
         pick = lambda cur_len: graphs[0] if cur_len < 150 else graphs[1]
