@@ -254,6 +254,45 @@ def test_paged_invalid_table_entries_are_skipped(dev):
             assert np.linalg.norm(got[b, h] - ref) / np.linalg.norm(ref) <= 1e-2, (b, h)
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "int8", "fp8"])
+@pytest.mark.parametrize("hint", [-1, 249])
+def test_paged_invalid_entries_in_either_tile(dev, dtype, hint):
+    """One segment per (b,h) of up to 256 positions in 64-row pages: each wave walks two
+    32-row tiles, rows [32w, 32w + 32) and [32w + 128, 32w + 160) (the 8-bit caches request
+    the second with the first).  Page 0 of sequence 0 is invalid (the first tile of waves 0
+    and 1), page 3 of sequence 1 too (the second tile of waves 2 and 3, at the sequence's
+    end): those positions are skipped, never read, and the rest attended as usual."""
+    import torch
+    kvattn = _kv()
+    B, NH, maxT, P = 2, 3, 256, 64
+    case = make_case(dtype, B, NH, maxT, [249, 199], seed=83)
+    pg = Paged(case, P, dev, seed=4)
+    table = pg.table.copy()
+    table[0, 0] = -1                  # positions 0..63 of sequence 0
+    table[1, 3] = pg.num_pages + 7    # positions 192..199 of sequence 1
+    pg.d_table.copy_(torch.from_numpy(table))
+    qkv = torch.from_numpy(case.qkv_raw.view(np.int16)).to(dev).view(torch.bfloat16)
+    cur = torch.from_numpy(case.cur_lens.copy()).to(dev)
+    ws = kvattn.Workspace(B, NH, maxT, 0)
+    out = out_tensor(case, dev)
+    kvattn.paged_decode(out, qkv, pg.cache, B, NH, HS, kv_dtype=dtype, cur_len=cur, lens_per_seq=True,
+                        len_hint=hint, **ws.kwargs())
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    c = case.cache_host.reshape(2, B, NH, maxT, HS)
+    q = case.qkv_host.reshape(B, 3, NH, HS)
+    ref = np.zeros((B, NH, HS), np.float64)
+    for b, (lo, hi) in ((0, (0, 64)), (1, (192, 256))):
+        keep = [j for j in range(int(case.totals[b])) if not lo <= j < hi]
+        for h in range(NH):
+            k = c[0, b, h, keep].astype(np.float64)
+            v = c[1, b, h, keep].astype(np.float64)
+            sc = k @ q[b, 0, h].astype(np.float64) / 8.0
+            p_ = np.exp(sc - sc.max())
+            ref[b, h] = (p_ @ v) / p_.sum()
+    assert_close(got, ref.reshape(-1).astype(np.float32), dtype, f"{dtype} hint={hint}")
+
+
 def test_paged_c5_shape_matches_contiguous(dev):
     """64 sequences x NH=12, lengths U[1, 8192], 256-row pages shuffled in a pool holding
     only the pages in use (~0.82 GB instead of 1.6 GB): every (b,h) agrees with the
