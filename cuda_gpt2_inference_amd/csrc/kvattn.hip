@@ -2267,6 +2267,14 @@ int planned_slots(int maxT) {
 }
 
 constexpr long long kStreamRows = 1 << 19; // AUTO: split + merge kernel from this many rows
+// ... and with per-sequence lengths of up to kRaggedLatMaxRows positions from this many (the
+// longest length counted for every sequence): between the two, the last-block merge on the
+// latency shape measured 1-18 % faster than split + merge (BF16, INT8, FP8, B = 6-64,
+// 589,824-786,432 rows, contiguous and paged), while longer contexts (8-bit 17-25 % slower at
+// 16384-32768 positions) and one length for the batch (FP8 and FP32 up to 26 % slower) keep
+// the lower bound.
+constexpr long long kStreamRowsRagged = 1 << 20;
+constexpr int kRaggedLatMaxRows = 8192;
 
 // Resolve AUTO and the segmentation.  S > 0: reference partition with S slots; S < 0:
 // -S rows per segment; S == 0: automatic rows per segment, from the length hint, or
@@ -2276,8 +2284,12 @@ struct Plan {
     bool lat;   // the latency shape: tiles of KVATTN_SPLIT_LAT_ROWS rows (else the streaming shape's)
 };
 
-// A call is latency bound while it streams fewer rows than kStreamRows.
-bool latency_bound(int B, int NH, int total_rows) { return (long long)B * NH * total_rows < kStreamRows; }
+// A call is latency bound while it streams fewer rows than kStreamRows (kStreamRowsRagged for
+// per-sequence lengths of up to kRaggedLatMaxRows).
+bool latency_bound(int B, int NH, int total_rows, bool ragged = false) {
+    const bool wide = ragged && total_rows <= kRaggedLatMaxRows;
+    return (long long)B * NH * total_rows < (wide ? kStreamRowsRagged : kStreamRows);
+}
 
 // AUTO's tuned plan for an attended length of total_hint (the host's hint, or maxT for a call
 // that must serve every length), beyond fused_single: the plan measured fastest across
@@ -2400,13 +2412,13 @@ int make_plan(int B, int NH, int maxT, int len_hint, int S, int strategy, int kv
             }
         }
         if (fused) strategy = KVATTN_FUSED_SINGLE;
-        else if ((long long)B * NH * total_hint >= kStreamRows) strategy = KVATTN_SPLIT_MERGE;
+        else if (!latency_bound(B, NH, total_hint, ragged)) strategy = KVATTN_SPLIT_MERGE;
         else if ((long long)B * NH * ceil_div_i(total_hint, designated_rows(total_hint, B * NH)) <= kDesignatedMaxGrid)
             strategy = KVATTN_SPLIT_DESIGNATED;
         else strategy = KVATTN_SPLIT_LASTBLOCK;
     }
     p.strategy = strategy;
-    p.lat = latency_bound(B, NH, total_hint);
+    p.lat = latency_bound(B, NH, total_hint, ragged && auto_strategy);
     if (strategy == KVATTN_FUSED_SINGLE) {
         p.slots = 1;
         p.seg_rows = 0;

@@ -431,3 +431,26 @@ def test_paged_designated_producers_on_other_xcds(dev, dtype, rot):
         assert remote + unseen == producers and remote > 0, f"{what}: remote {remote} unseen {unseen} of {producers}"
     else:
         assert remote == 0, f"{what}: {remote} producers found their merger on another XCD"
+
+
+def test_paged_auto_ragged_between_the_stream_bounds(dev):
+    """The same band in a paged cache (64 sequences x 12 heads x up to 1024 positions, 256-row
+    pages, INT8): AUTO's last-block merge on the latency shape through the table, against the
+    oracle."""
+    import torch
+    kvattn = _kv()
+    B, NH, maxT, P = 64, 12, 1024, 256
+    rng = np.random.RandomState(517)
+    lens = rng.randint(1, maxT + 1, B).astype(np.int32)
+    lens[3] = maxT
+    case = make_case("int8", B, NH, maxT, lens - 1, seed=518)
+    pg = Paged(case, P, dev, seed=6)
+    qkv = torch.from_numpy(case.qkv_raw.view(np.int16)).to(dev).view(torch.bfloat16)
+    cur = torch.from_numpy(case.cur_lens.copy()).to(dev)
+    ws = kvattn.Workspace(B, NH, maxT, 0)
+    out = out_tensor(case, dev)
+    kvattn.paged_decode(out, qkv, pg.cache, B, NH, HS, kv_dtype="int8", cur_len=cur, lens_per_seq=True,
+                        len_hint=maxT - 1, **ws.kwargs())
+    torch.cuda.synchronize()
+    assert ws.status() == 0
+    assert_close(out.float().cpu().numpy(), case.reference(), "int8", "paged int8 ragged band")

@@ -798,3 +798,26 @@ def test_seeded_auto_sweep(dev):
         torch.cuda.synchronize()
         assert ws.status() == 0, name
         assert_close(out.float().cpu().numpy(), case.reference(), dtype, name)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "int8"])
+@pytest.mark.parametrize("hinted", [True, False])
+def test_auto_ragged_between_the_stream_bounds(dev, dtype, hinted):
+    """Per-sequence lengths, 64 sequences x 12 heads x up to 1024 positions (786,432 rows, between
+    the split + merge bounds of one length for the batch and of per-sequence lengths): AUTO
+    takes the last-block merge on the latency shape there; the call against the oracle."""
+    import torch
+    kvattn = _kv()
+    B, NH, maxT = 64, 12, 1024
+    rng = np.random.RandomState(515)
+    lens = rng.randint(1, maxT + 1, B).astype(np.int32)
+    lens[7] = maxT
+    case = make_case(dtype, B, NH, maxT, lens - 1, seed=516)
+    qkv, cache, scale, cur = to_device(case, dev)
+    out = out_tensor(case, dev)
+    ws = kvattn.Workspace(B, NH, maxT, 0)
+    kvattn.decode(out, qkv, cache, B, NH, HS, maxT, kv_dtype=dtype, kv_scale=scale, cur_len=cur,
+                  lens_per_seq=True, len_hint=maxT - 1 if hinted else -1, strategy="auto", **ws.kwargs())
+    torch.cuda.synchronize()
+    assert ws.status() == 0
+    assert_close(out.float().cpu().numpy(), case.reference(), dtype, f"{dtype} hinted={hinted}")
