@@ -2275,6 +2275,11 @@ constexpr long long kStreamRows = 1 << 19; // AUTO: split + merge kernel from th
 // the lower bound.
 constexpr long long kStreamRowsRagged = 1 << 20;
 constexpr int kRaggedLatMaxRows = 8192;
+// ... and from this many with per-sequence lengths of up to kRaggedShortRows positions (96-128
+// sequences of up to 1024 positions: the last-block merge 7-11 % faster than split + merge;
+// at 2048-8192 positions the same bound was mixed, BF16 +2 to +3 %, 8-bit -1 to -5 %).
+constexpr long long kStreamRowsRaggedShort = 1 << 21;
+constexpr int kRaggedShortRows = 1024;
 
 // Resolve AUTO and the segmentation.  S > 0: reference partition with S slots; S < 0:
 // -S rows per segment; S == 0: automatic rows per segment, from the length hint, or
@@ -2284,11 +2289,14 @@ struct Plan {
     bool lat;   // the latency shape: tiles of KVATTN_SPLIT_LAT_ROWS rows (else the streaming shape's)
 };
 
-// A call is latency bound while it streams fewer rows than kStreamRows (kStreamRowsRagged for
-// per-sequence lengths of up to kRaggedLatMaxRows).
+// A call is latency bound while it streams fewer rows than kStreamRows (with per-sequence
+// lengths: kStreamRowsRaggedShort up to kRaggedShortRows positions, kStreamRowsRagged up to
+// kRaggedLatMaxRows).
 bool latency_bound(int B, int NH, int total_rows, bool ragged = false) {
-    const bool wide = ragged && total_rows <= kRaggedLatMaxRows;
-    return (long long)B * NH * total_rows < (wide ? kStreamRowsRagged : kStreamRows);
+    long long bound = kStreamRows;
+    if (ragged && total_rows <= kRaggedShortRows) bound = kStreamRowsRaggedShort;
+    else if (ragged && total_rows <= kRaggedLatMaxRows) bound = kStreamRowsRagged;
+    return (long long)B * NH * total_rows < bound;
 }
 
 // AUTO's tuned plan for an attended length of total_hint (the host's hint, or maxT for a call

@@ -800,15 +800,16 @@ def test_seeded_auto_sweep(dev):
         assert_close(out.float().cpu().numpy(), case.reference(), dtype, name)
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "int8"])
+@pytest.mark.parametrize("dtype,B", [("bf16", 64), ("int8", 64), ("bf16", 128)])
 @pytest.mark.parametrize("hinted", [True, False])
-def test_auto_ragged_between_the_stream_bounds(dev, dtype, hinted):
-    """Per-sequence lengths, 64 sequences x 12 heads x up to 1024 positions (786,432 rows, between
-    the split + merge bounds of one length for the batch and of per-sequence lengths): AUTO
-    takes the last-block merge on the latency shape there; the call against the oracle."""
+def test_auto_ragged_between_the_stream_bounds(dev, dtype, B, hinted):
+    """Per-sequence lengths, 64 or 128 sequences x 12 heads x up to 1024 positions (786,432 and
+    1,572,864 rows, between the split + merge bound of one length for the batch and those of
+    per-sequence lengths): AUTO takes the last-block merge on the latency shape there; the
+    call against the oracle."""
     import torch
     kvattn = _kv()
-    B, NH, maxT = 64, 12, 1024
+    NH, maxT = 12, 1024
     rng = np.random.RandomState(515)
     lens = rng.randint(1, maxT + 1, B).astype(np.int32)
     lens[7] = maxT
