@@ -28,6 +28,9 @@ def _identity(kvattn, stream, dev):
     """(dispatch id, queue address, tag) of one dispatch on `stream`."""
     import torch
     buf = torch.zeros(3, dtype=torch.int64, device=dev)
+    # The zero fill runs on the current stream: order `stream` after it, or the fill can land
+    # after the identity dispatch's store.
+    stream.wait_stream(torch.cuda.current_stream())
     kvattn.call_identity(buf, stream=stream)
     stream.synchronize()
     return [int(v) & (2**64 - 1) for v in buf.cpu().numpy().view(np.uint64)]
