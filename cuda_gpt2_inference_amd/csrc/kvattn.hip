@@ -2275,10 +2275,11 @@ constexpr long long kStreamRows = 1 << 19; // AUTO: split + merge kernel from th
 // the lower bound.
 constexpr long long kStreamRowsRagged = 1 << 20;
 constexpr int kRaggedLatMaxRows = 8192;
-// ... and from this many with per-sequence lengths of up to kRaggedShortRows positions (96-128
-// sequences of up to 1024 positions: the last-block merge 7-11 % faster than split + merge;
-// at 2048-8192 positions the same bound was mixed, BF16 +2 to +3 %, 8-bit -1 to -5 %).
-constexpr long long kStreamRowsRaggedShort = 1 << 21;
+// ... and from this many with per-sequence lengths of up to kRaggedShortRows positions (96-320
+// sequences of up to 1024 positions: the last-block merge up to 11 % faster than split + merge,
+// one shape of twelve 2 % slower; at 2048-8192 positions a bound of 2^21 was already mixed,
+// BF16 +2 to +3 %, 8-bit -1 to -5 %).
+constexpr long long kStreamRowsRaggedShort = 1 << 22;
 constexpr int kRaggedShortRows = 1024;
 
 // Resolve AUTO and the segmentation.  S > 0: reference partition with S slots; S < 0:
