@@ -2281,6 +2281,11 @@ constexpr int kRaggedLatMaxRows = 8192;
 // BF16 +2 to +3 %, 8-bit -1 to -5 %).
 constexpr long long kStreamRowsRaggedShort = 1 << 22;
 constexpr int kRaggedShortRows = 1024;
+// ... and for contiguous 8-bit caches from this many up to kRagged8MidRows positions (INT8
+// and FP8, 24-64 sequences of 2048-4096 positions: 1-8 % faster than from 2^20; BF16 2-3 %
+// slower there, a paged INT8 cache +5 % to -3 %).
+constexpr long long kStreamRowsRagged8Mid = 1 << 21;
+constexpr int kRagged8MidRows = 4096;
 
 // Resolve AUTO and the segmentation.  S > 0: reference partition with S slots; S < 0:
 // -S rows per segment; S == 0: automatic rows per segment, from the length hint, or
@@ -2291,11 +2296,13 @@ struct Plan {
 };
 
 // A call is latency bound while it streams fewer rows than kStreamRows (with per-sequence
-// lengths: kStreamRowsRaggedShort up to kRaggedShortRows positions, kStreamRowsRagged up to
+// lengths: kStreamRowsRaggedShort up to kRaggedShortRows positions, for contiguous 8-bit
+// caches (k8) kStreamRowsRagged8Mid up to kRagged8MidRows, kStreamRowsRagged up to
 // kRaggedLatMaxRows).
-bool latency_bound(int B, int NH, int total_rows, bool ragged = false) {
+bool latency_bound(int B, int NH, int total_rows, bool ragged = false, bool k8 = false) {
     long long bound = kStreamRows;
     if (ragged && total_rows <= kRaggedShortRows) bound = kStreamRowsRaggedShort;
+    else if (ragged && k8 && total_rows <= kRagged8MidRows) bound = kStreamRowsRagged8Mid;
     else if (ragged && total_rows <= kRaggedLatMaxRows) bound = kStreamRowsRagged;
     return (long long)B * NH * total_rows < bound;
 }
@@ -2421,13 +2428,13 @@ int make_plan(int B, int NH, int maxT, int len_hint, int S, int strategy, int kv
             }
         }
         if (fused) strategy = KVATTN_FUSED_SINGLE;
-        else if (!latency_bound(B, NH, total_hint, ragged)) strategy = KVATTN_SPLIT_MERGE;
+        else if (!latency_bound(B, NH, total_hint, ragged, is_8bit(kv_dtype) && !paged)) strategy = KVATTN_SPLIT_MERGE;
         else if ((long long)B * NH * ceil_div_i(total_hint, designated_rows(total_hint, B * NH)) <= kDesignatedMaxGrid)
             strategy = KVATTN_SPLIT_DESIGNATED;
         else strategy = KVATTN_SPLIT_LASTBLOCK;
     }
     p.strategy = strategy;
-    p.lat = latency_bound(B, NH, total_hint, ragged && auto_strategy);
+    p.lat = latency_bound(B, NH, total_hint, ragged && auto_strategy, is_8bit(kv_dtype) && !paged);
     if (strategy == KVATTN_FUSED_SINGLE) {
         p.slots = 1;
         p.seg_rows = 0;
